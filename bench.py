@@ -1,0 +1,310 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X non-GEMM primitives at BASELINE.json's 30B-class shapes.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--reps R] [--no-cpu] [--only OP]
+
+A step is one pass of the three headline primitives over their BASELINE
+configs, inputs resident in HBM:
+  residual-add + RMSNorm   bf16 [4096, 5120] (+ w [5120]), eps 1e-6      configs[1]
+  SwiGLU                   bf16 gate/up [4096, 25600]                     configs[2]
+  causal row softmax       f32 scores [40, 2048, 2048] -> bf16, 1/sqrt(128) configs[3]
+`value` is the whole step's algorithmic HBM bytes (each tensor read or written
+once) divided by the measured step time, in GB/s. Every other primitive
+(RoPE, decode softmax, Q8_0 dequant, vocab lse/argmax/top-64, decode-shape
+RMSNorm) is timed on its own under "ops". Inputs are seeded synthetic data
+drawn with torch's generator on the device (N(0,1) activations, N(1,0.05)
+weights, N(0,3) scores, U{-127..127} quants, U[1e-3,2e-2] f16 scales, N(0,4)
+logits). Per-op times are the median of R launches bracketed by HIP events on
+the launch stream, with a 512 MiB buffer rewritten before each launch so no op
+is served from the 256 MiB Infinity Cache.
+
+`cpu_baseline` times the CPU restatement of the reference's own tensor path
+(oracle/liboracle.so: f64 twin arithmetic with OpenMP over rows, as
+src/muse_glimmer.hpp runs it) on a bounded sample of the same three ops and
+reports it in the same unit.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "muse-glimmer-intel-serve_amd")
+sys.path.insert(0, PKG)
+
+METRIC = "achieved HBM GB/s (% of 8 TB/s) + us/op for RMSNorm/SwiGLU/softmax, 30B shapes"
+PEAK_GBPS = 8000.0
+
+T, D = 4096, 5120
+FFN = 25600
+SM_H, SM_Q, SM_K = 40, 2048, 2048
+DEC_K = 131072
+Q_H, K_H, HD = 40, 8, 128
+Q8_R, Q8_C = 25600, 5120
+V_ROWS, VOCAB, TOPK = 64, 201088, 64
+
+# algorithmic bytes: every input read once, every output written once
+BYTES = {
+    "residual_rmsnorm": 4 * 2 * T * D + 2 * D,
+    "swiglu": 3 * 2 * T * FFN,
+    "softmax_causal": SM_H * (SM_Q * (SM_Q + 1) // 2) * 4 + SM_H * SM_Q * SM_K * 2,
+    "rope": 2 * 2 * (T * Q_H * HD + T * K_H * HD) + 2 * 2 * T * (HD // 2),
+    "softmax_decode": SM_H * DEC_K * (4 + 2),
+    "dequant_q8_0": Q8_R * Q8_C + Q8_R * (Q8_C // 32) * 2 + Q8_R * Q8_C * 2,
+    "vocab_lse_argmax_top64": V_ROWS * VOCAB * 4 + V_ROWS * (8 + 8) + V_ROWS * TOPK * (8 + 4),
+}
+STEP_OPS = ("residual_rmsnorm", "swiglu", "softmax_causal")
+KERNEL_OF = {
+    "residual_rmsnorm": "k_norm_tree",
+    "swiglu": "k_gate_lut",
+    "softmax_causal": "k_softmax_wave",
+    "rope": "k_rope",
+    "softmax_decode": "k_softmax_partial + k_softmax_finish",
+    "dequant_q8_0": "k_dequant_q8_0",
+    "vocab_lse_argmax_top64": "k_vocab_chunk + k_vocab_merge",
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--reps", type=int, default=20, help="launches per op for the per-op medians")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default=None, help="run only this op, --steps times (for profilers)")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "pmc_traffic.txt"),
+                    help="measured HBM bytes per launch (kernel  fetch_bytes  write_bytes)")
+    return ap.parse_args()
+
+
+def make_inputs(torch, P):
+    import mgprims as M
+    dev = "cuda:0"
+    g = torch.Generator(device=dev)
+    g.manual_seed(20261201)
+    bf = torch.bfloat16
+
+    def randn(shape, mean=0.0, std=1.0, dtype=bf):
+        return (torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std + mean).to(dtype)
+
+    I = {}
+    I["h"] = randn((T, D))
+    I["x"] = randn((T, D))
+    I["w"] = randn((D,), 1.0, 0.05)
+    I["y"] = torch.empty((T, D), dtype=bf, device=dev)
+    I["gate"] = randn((T, FFN))
+    I["up"] = randn((T, FFN))
+    I["act"] = torch.empty((T, FFN), dtype=bf, device=dev)
+    I["scores"] = randn((SM_H, SM_Q, SM_K), 0.0, 3.0, torch.float32)
+    I["probs"] = torch.empty((SM_H, SM_Q, SM_K), dtype=bf, device=dev)
+    I["q"] = randn((T, Q_H, HD))
+    I["k"] = randn((T, K_H, HD))
+    I["cos"], I["sin"] = P.build_rope_table(1e6, HD, T, bf)
+    I["dscores"] = randn((SM_H, 1, DEC_K), 0.0, 3.0, torch.float32)
+    I["dprobs"] = torch.empty((SM_H, 1, DEC_K), dtype=bf, device=dev)
+    I["qs"] = torch.randint(-127, 128, (Q8_R, Q8_C), generator=g, device=dev, dtype=torch.int8)
+    I["qd"] = (torch.rand((Q8_R, Q8_C // 32), generator=g, device=dev) * (2e-2 - 1e-3) + 1e-3).to(torch.float16)
+    I["deq"] = torch.empty((Q8_R, Q8_C), dtype=bf, device=dev)
+    I["logits"] = randn((V_ROWS, VOCAB), 0.0, 4.0, torch.float32)
+    I["lse"] = torch.empty(V_ROWS, dtype=torch.float64, device=dev)
+    I["amax"] = torch.empty(V_ROWS, dtype=torch.int64, device=dev)
+    I["tidx"] = torch.empty((V_ROWS, TOPK), dtype=torch.int64, device=dev)
+    I["tval"] = torch.empty((V_ROWS, TOPK), dtype=torch.float32, device=dev)
+    I["hdec"] = randn((64, D))
+    I["xdec"] = randn((64, D))
+    I["ydec"] = torch.empty((64, D), dtype=bf, device=dev)
+    torch.cuda.synchronize()
+
+    scale = 1.0 / math.sqrt(HD)
+    ops = {
+        "residual_rmsnorm": lambda: P.residual_rmsnorm(M.PLAIN, I["h"], I["x"], I["w"], 1e-6, I["y"]),
+        "swiglu": lambda: P.swiglu(I["gate"], I["up"], I["act"]),
+        "softmax_causal": lambda: P.softmax_rows(I["scores"], I["probs"], scale, M.MASK_CAUSAL),
+        "rope": lambda: P.apply_rope(I["q"], I["k"], I["cos"], I["sin"]),
+        "softmax_decode": lambda: P.softmax_rows(I["dscores"], I["dprobs"], scale, M.MASK_CAUSAL, 0, DEC_K - 1),
+        "dequant_q8_0": lambda: P.dequant_q8_0(I["qs"], I["qd"], I["deq"]),
+        "vocab_lse_argmax_top64": lambda: P.vocab_reduce(I["logits"], TOPK, I["lse"], I["amax"], I["tidx"], I["tval"]),
+    }
+    for t in (1, 4, 16, 64):
+        ops[f"residual_rmsnorm_T{t}"] = (lambda t=t: P.residual_rmsnorm(
+            M.PLAIN, I["hdec"][:t], I["xdec"][:t], I["w"], 1e-6, I["ydec"][:t]))
+        BYTES[f"residual_rmsnorm_T{t}"] = 4 * 2 * t * D + 2 * D
+        KERNEL_OF[f"residual_rmsnorm_T{t}"] = "k_norm_tree"
+    return ops
+
+
+def time_op(torch, fn, reps, flush):
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        fn()
+    times = []
+    for _ in range(reps):
+        flush.zero_()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn()
+        b.record(stream)
+        b.synchronize()
+        times.append(a.elapsed_time(b) * 1e3)  # us
+    return statistics.median(times), min(times)
+
+
+def read_traffic(path, kernel):
+    """Measured HBM bytes per launch for `kernel` from the rocprofv3 PMC summary, or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) >= 3 and parts[0] == kernel and not line.startswith("#"):
+                    return int(float(parts[1]) + float(parts[2]))
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline():
+    """The reference's CPU tensor path (the oracle restatement, OpenMP over rows)
+    on a bounded sample of the step's three ops, in the same unit (GB/s)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    rows_n, rows_s, sm_h = 512, 256, 2
+    sample = {
+        "residual_rmsnorm": (rows_n, 4 * 2 * rows_n * D + 2 * D),
+        "swiglu": (rows_s, 3 * 2 * rows_s * FFN),
+        "softmax_causal": (sm_h, sm_h * (SM_Q * (SM_Q + 1) // 2) * 4 + sm_h * SM_Q * SM_K * 2),
+    }
+    h = O.to_f64(O.normal(1, (rows_n, D), 0, 1, O.BF16), O.BF16)
+    x = O.to_f64(O.normal(2, (rows_n, D), 0, 1, O.BF16), O.BF16)
+    w = O.to_f64(O.normal(3, (D,), 1, 0.05, O.BF16), O.BF16)
+    gt = O.to_f64(O.normal(4, (rows_s, FFN), 0, 1, O.BF16), O.BF16)
+    up = O.to_f64(O.normal(5, (rows_s, FFN), 0, 1, O.BF16), O.BF16)
+    sc = O.to_f64(O.normal(8, (sm_h, SM_Q, SM_K), 0, 3, O.F32), O.F32)
+    fns = {
+        "residual_rmsnorm": lambda: O.residual_rmsnorm(O.PLAIN, h, x, w, 1e-6, O.BF16),
+        "swiglu": lambda: O.swiglu(gt, up, O.BF16),
+        "softmax_causal": lambda: O.softmax_rows(sc, 1 / math.sqrt(HD), O.MASK_CAUSAL, 0, 0, 0.0, O.F32, O.BF16),
+    }
+    per = {}
+    tot_b = tot_s = 0.0
+    for name, fn in fns.items():
+        fn()
+        reps = 3
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        dt = (time.perf_counter() - t0) / reps
+        b = sample[name][1]
+        per[name] = {"us": round(dt * 1e6, 1), "GBps": round(b / dt / 1e9, 3)}
+        tot_b += b
+        tot_s += dt
+    del np
+    return {
+        "value": round(tot_b / tot_s / 1e9, 3),
+        "unit": "GB/s",
+        "cores": O.num_threads(),
+        "kind": "port",
+        "sample": (f"residual_rmsnorm bf16-twin [{rows_n},{D}], swiglu bf16-twin [{rows_s},{FFN}], "
+                   f"causal softmax f32->bf16 [{sm_h},{SM_Q},{SM_K}]; f64 arrays as src/muse_glimmer.hpp holds them; "
+                   f"OpenMP threads={O.num_threads()}, host nproc={os.cpu_count()}"),
+        "ops": per,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(every primitive is row-independent; multi-GPU sharding is described in DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import mgprims
+    torch.cuda.set_device(0)
+    P = mgprims.Prims(0)
+    ops = make_inputs(torch, P)
+
+    if args.only:
+        fn = ops[args.only]
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) / args.steps * 1e6
+        print(json.dumps({"op": args.only, "us_per_op_wall": round(us, 2)}), flush=True)
+        return
+
+    def step():
+        for n in STEP_OPS:
+            ops[n]()
+
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(args.steps):
+        step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    step_bytes = sum(BYTES[n] for n in STEP_OPS)
+    value = step_bytes / (ms * 1e-3) / 1e9
+    print(f"# step: {ms * 1e3:.1f} us, {value:.1f} GB/s", file=sys.stderr, flush=True)
+
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0")
+    per = {}
+    for name, fn in ops.items():
+        med, best = time_op(torch, fn, args.reps, flush)
+        gbps = BYTES[name] / (med * 1e-6) / 1e9
+        per[name] = {"us": round(med, 2), "us_min": round(best, 2), "bytes": BYTES[name],
+                     "GBps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
+                     "kernel": KERNEL_OF[name]}
+        print(f"# {name:28s} {med:9.2f} us  {gbps:8.1f} GB/s  {100 * gbps / PEAK_GBPS:5.1f} %",
+              file=sys.stderr, flush=True)
+
+    dom = max(STEP_OPS, key=lambda n: per[n]["us"])
+    kern = KERNEL_OF[dom]
+    achieved = BYTES[dom] / (per[dom]["us"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": kern, "op": dom, "achieved": round(achieved, 1),
+                "peak": PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
+                "traffic": read_traffic(args.traffic, kern), "algorithmic_bytes": BYTES[dom]}
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch generator on device; BASELINE.json distributions)",
+        "config": {"workload": "30B-class non-GEMM step: residual-add+RMSNorm bf16 [4096,5120] + "
+                               "SwiGLU bf16 [4096,25600] + causal softmax f32->bf16 [40,2048,2048]",
+                   "step_bytes": step_bytes, "pct_peak": round(100 * value / PEAK_GBPS, 1)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "ops": per,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

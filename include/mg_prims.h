@@ -1,0 +1,153 @@
+/* mg_prims.h — C ABI of the MI355X (gfx950) non-GEMM tensor primitives.
+ *
+ * One library (libmgprims.so), HIP kernels only; no CPU fallback. Conventions
+ * follow the reference's C ABI over its GPU engine (src/gpu/c_api.cpp):
+ *   - an opaque context created once; every device buffer the library needs
+ *     (lookup tables, reduction partials) is allocated in mg_open, and no entry
+ *     point allocates device memory afterwards (c_api.cpp:9-14);
+ *   - no exception crosses the boundary: every entry point returns 0 on success
+ *     and -1 on failure, with the message readable from mg_last_error() on the
+ *     same thread (c_api.cpp:15-17, 170-188);
+ *   - a context is not thread-safe; calls are asynchronous on the context's
+ *     stream, and mg_sync() waits for them;
+ *   - all tensor pointers are DEVICE pointers, row-major and contiguous unless
+ *     a leading dimension argument says otherwise; counts are int64.
+ *
+ * Storage dtypes (the reference's prec::Dtype order, src/rounding.hpp:31-36,
+ * plus f32): bf16 and f16 travel as their 16-bit patterns.
+ *
+ * Numerics: each op's result is the reference's f64 oracle / bf16-f16 twin
+ * value (src/muse_glimmer.hpp) rounded to the output dtype through
+ * f64 -> f32 -> storage RNE (src/rounding.hpp:64-166). Elementwise ops are
+ * bit-exact against the twin; norms use f64 internals; the softmax and vocab
+ * reductions compute in f32 with f64 merges. */
+#ifndef MG_PRIMS_H
+#define MG_PRIMS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mg_ctx mg_ctx;
+
+enum mg_dtype { MG_F64 = 0, MG_BF16 = 1, MG_F16 = 2, MG_F32 = 3 };
+
+/* muse::NormKind (src/muse_glimmer.hpp:558-563) */
+enum mg_norm_kind { MG_NORM_CENTERED = 0, MG_NORM_PLAIN = 1, MG_NORM_WEIGHTLESS = 2 };
+
+/* mask of a [heads, q, k] score block; qpos = q_pos0 + row.
+ * causal: key j visible iff j <= qpos; window: qpos - window < j <= qpos
+ * (src/muse_glimmer.hpp:838-843, the sliding-window rule). */
+enum mg_mask { MG_MASK_NONE = 0, MG_MASK_CAUSAL = 1, MG_MASK_WINDOW = 2 };
+
+/* Thread-local message of the last failing call on this thread
+ * (muse_last_error, src/gpu/c_api.cpp:35, 170-188). */
+const char *mg_last_error(void);
+
+/* Create a context on HIP device `device`. `stream` is a hipStream_t to launch
+ * on, or NULL for a new stream of default priority owned by the context.
+ * `workspace_bytes` sizes the reduction-partials buffer (0 = 64 MiB); calls
+ * whose partials would not fit fail with an error instead of allocating.
+ * (muse_open, src/gpu/c_api.cpp:88-168) */
+int mg_open(int device, void *stream, int64_t workspace_bytes, mg_ctx **out);
+int mg_close(mg_ctx *ctx);
+/* Wait for all work queued on the context's stream. */
+int mg_sync(mg_ctx *ctx);
+/* Point the context at another stream (hipStream_t; NULL = its own). */
+int mg_set_stream(mg_ctx *ctx, void *stream);
+void *mg_get_stream(mg_ctx *ctx);
+
+/* y[r,:] = norm(x[r,:]) — replaces muse::rmsnorm_rows (src/muse_glimmer.hpp:572-608)
+ * and bf16exec norm_rows (src/bf16exec.hpp:398-421); GPU k_rmsnorm_auto
+ * (src/gpu/gpu_engine.cpp:285-390). Centered: x*rs*(1+w); Plain: x*rs*w;
+ * Weightless: x*rs (w may be NULL); rs = 1/sqrt(mean(x^2)+eps), f64 internals,
+ * one rounding to `dtype`. ldx/ldy: row strides in elements (0 = dim).
+ * In place (y == x) is allowed. */
+int mg_rmsnorm_rows(mg_ctx *ctx, int kind, const void *x, int64_t ldx, const void *w,
+                    double eps, void *y, int64_t ldy, int64_t rows, int64_t dim, int dtype);
+
+/* Fused residual add + norm: h[r,:] = rnd(h[r,:] + x[r,:]) (updated in place),
+ * then y[r,:] = norm(h[r,:]). Replaces the residual loop
+ * (src/muse_glimmer.hpp:1023-1024, 1048-1049; src/bf16exec.hpp:608-610, 641-643;
+ * GPU k_residual src/gpu/gpu_engine.cpp:1886-1893) followed by the next
+ * rmsnorm_rows call on the updated stream (src/muse_glimmer.hpp:1028-1031). */
+int mg_residual_rmsnorm(mg_ctx *ctx, int kind, void *h, const void *x, const void *w, double eps,
+                        void *y, int64_t rows, int64_t dim, int dtype);
+
+/* h = rnd(h + x), elementwise (src/muse_glimmer.hpp:1023-1024). */
+int mg_residual_add(mg_ctx *ctx, void *h, const void *x, int64_t n, int dtype);
+
+/* out = rnd(rnd(silu(gate)) * up) — the SwiGLU loop (src/muse_glimmer.hpp:1036-1039;
+ * src/bf16exec.hpp:626-631; GPU k_swiglu src/gpu/gpu_engine.cpp:1895-1904).
+ * silu is the twin's f64 FDLIBM form (src/muse_glimmer.hpp:493). */
+int mg_swiglu(mg_ctx *ctx, const void *gate, const void *up, void *out, int64_t n, int dtype);
+
+/* out = rnd(pv * rnd(sigmoid(gate))) — attention output gate
+ * (src/muse_glimmer.hpp:896-906; GPU k_out_gate src/gpu/gpu_engine.cpp:1873-1883). */
+int mg_sigmoid_gate(mg_ctx *ctx, const void *pv, const void *gate, void *out, int64_t n,
+                    int dtype);
+
+/* x = rnd(x * s), s taken as an f32 opmath scalar for bf16/f16/f32 — the q-only
+ * qk_scale (src/muse_glimmer.hpp:803-807; GPU k_scale_bf16 gpu_engine.cpp:433-440). */
+int mg_scale(mg_ctx *ctx, void *x, int64_t n, double s, int dtype);
+
+/* RoPE table [positions, head_dim/2] of cos and sin, stored at `dtype` —
+ * muse::build_rope_table (src/muse_glimmer.hpp:625-674): f32 inverse-frequency
+ * chain for bf16/f16/f32, f64 chain for f64; FDLIBM pow/cos/sin on the device. */
+int mg_rope_table(mg_ctx *ctx, double theta, int64_t head_dim, int64_t positions, int dtype,
+                  void *cos_out, void *sin_out);
+
+/* Rotate-half RoPE in place on q [tokens, q_heads, head_dim] and (optionally,
+ * k may be NULL) k [tokens, k_heads, head_dim]; token t uses table row
+ * positions[t] (device int64 array) or, when positions is NULL, pos0 + t.
+ * Row strides between tokens: ldq/ldk elements (0 = heads*head_dim).
+ * Replaces muse::apply_rope over (t, head) (src/muse_glimmer.hpp:681-705, 809-819)
+ * and GPU k_rope (src/gpu/gpu_engine.cpp:444-476). `table_rows` bounds positions. */
+int mg_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k, int64_t k_heads,
+            int64_t ldk, int64_t tokens, int64_t head_dim, const void *cos_t, const void *sin_t,
+            int64_t table_rows, const int64_t *positions, int64_t pos0, int dtype);
+
+/* Scaled, masked row softmax over a contiguous [heads, q, k] score block — the
+ * softmax of attention_forward (src/muse_glimmer.hpp:828-885) as a row operator:
+ * s = x*scale (f32 opmath), optional tanh softcap s = cap*tanh(s/cap) in
+ * apply_output_tail's op order (src/muse_glimmer.hpp:920-943; cap 0 = off),
+ * masked keys get probability exactly 0, p = exp(s - max)/sum.
+ * dtype_in: f32, bf16 or f16 scores; dtype_out: bf16, f16 or f32 probs.
+ * Rows longer than one work-group's registers are split across work-groups
+ * and merged in chunk order (the k_attn_decode_combine rule,
+ * src/gpu/gpu_engine.cpp:1816-1857). */
+int mg_softmax_rows(mg_ctx *ctx, const void *x, void *y, int64_t heads, int64_t q_rows,
+                    int64_t k_cols, double scale, int mask, int64_t window, int64_t q_pos0,
+                    double softcap, int dtype_in, int dtype_out);
+
+/* Output tail z = rnd(z*mult); z = rnd(cap*rnd(tanh(rnd(z/cap)))) in place
+ * (muse::apply_output_tail src/muse_glimmer.hpp:920-943; GPU k_softcap
+ * src/gpu/gpu_engine.cpp:1906-1919). mult 1 / cap 0 skip their steps. */
+int mg_softcap(mg_ctx *ctx, void *z, int64_t n, double mult, double cap, int dtype);
+
+/* Q8_0 dequantize: out[r,i] = rnd(f32(qs[r,i]) * f32(d[r,i/32])) with the
+ * reference's separate-arrays layout (QW, src/gpu/gpu_engine.cpp:120-141):
+ * qs int8 [rows, in], d f16 bits [rows, in/32]; `in` must be a multiple of 32.
+ * Replaces k_dequant_q8 (src/gpu/gpu_engine.cpp:1117-1171). dtype_out bf16/f16/f32. */
+int mg_dequant_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, void *out, int64_t rows,
+                    int64_t in, int dtype_out);
+
+/* Per row of logits [rows, V] (dtype_in f32 or bf16), one fused pass:
+ *   lse[r]     = m + log(sum exp(x - m)) over finite entries, m their max
+ *                (serve/sampler.py:168-171); -inf for a row with none
+ *   argmax[r]  = first index of the maximum, the strict '>' scan from index 0
+ *                (src/main.cpp:475-483; src/bf16exec.hpp:686-693)
+ *   top_idx/top_val [rows, K] = the K largest by value, ties by lower index
+ *                (src/main.cpp:604-615 and serve/sampler.py:84-89, whose tie
+ *                order is unspecified; this one is total), 0 < K <= 256.
+ * Any output pointer may be NULL to skip it (all device pointers). */
+int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, int dtype_in,
+                    int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MG_PRIMS_H */

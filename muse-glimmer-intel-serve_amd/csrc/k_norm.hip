@@ -1,0 +1,239 @@
+// RMSNorm rows and fused residual-add + RMSNorm for gfx950.
+//
+// Semantics: the reference's rmsnorm_rows pure/twin branch
+// (src/muse_glimmer.hpp:572-608): rs = 1/sqrt(mean(x^2) + eps) and
+// y = x*rs*(1+w) | x*rs*w | x*rs in f64, one rounding to storage. With a
+// residual operand the stream is first updated h = rnd(h + x)
+// (src/muse_glimmer.hpp:1023-1024); rnd(a + b) of two stored values is computed
+// in f32 for the 16-bit formats, which equals the twin's f64 add followed by
+// f64 -> f32 -> storage (an f32 add of f32-representable operands is the f32
+// rounding of the exact sum, and rounding to f64 first cannot change that:
+// 53 >= 2*24 + 2).
+//
+// Two kernels, chosen by shape only (never by a measurement, the rule of
+// k_rmsnorm_auto, src/gpu/gpu_engine.cpp:379-390):
+//   dim <= 128  k_norm_ordered: 32 rows per work-group; eight lanes per row run
+//               mean_sq's eight interleaved f64 accumulators in its exact order
+//               and combine them with its tree (src/muse_glimmer.hpp:509-527),
+//               so the result is bit-identical to the twin in every dtype.
+//   dim  > 128  k_norm_tree: one work-group per row, the row held in registers
+//               (16-byte loads), f64 sum of squares reduced in a fixed
+//               lane/wave order (deterministic, within 1e-16 relative of the
+//               twin's order; the bf16 output equals the twin's except where
+//               x*rs*w lies within that distance of a rounding boundary).
+#include "mg_device.hpp"
+#include "mg_internal.hpp"
+
+namespace mg
+{
+    constexpr int kOrderedMaxDim = 128;
+    constexpr int kOrderedRows = 32; // 8 lanes per row, 256 threads
+
+    MG_DEV double norm_out(int kind, double v, double rs, double w)
+    {
+        double t = v * rs;
+        if (kind == 0)
+            t = t * (1.0 + w);
+        else if (kind == 1)
+            t = t * w;
+        return t;
+    }
+
+    template <class S>
+    __global__ __launch_bounds__(256) void k_norm_ordered(int kind, typename S::raw *h,
+                                                          const typename S::raw *__restrict__ x,
+                                                          int64_t ldh, int64_t ldx,
+                                                          const typename S::raw *__restrict__ w,
+                                                          double eps, typename S::raw *y,
+                                                          int64_t ldy, int64_t rows, int dim)
+    {
+        using raw = typename S::raw;
+        extern __shared__ double smem_d[];
+        double *rsq = smem_d;                                    // [kOrderedRows]
+        raw *st = reinterpret_cast<raw *>(smem_d + kOrderedRows); // [kOrderedRows][dim]
+        const int64_t r0 = int64_t(blockIdx.x) * kOrderedRows;
+        const int nr = int(rows - r0 < kOrderedRows ? rows - r0 : kOrderedRows);
+
+        // stage the rows (after the residual update) in LDS
+        for (int idx = threadIdx.x; idx < nr * dim; idx += blockDim.x) {
+            const int rr = idx / dim, i = idx - rr * dim;
+            raw v = h[(r0 + rr) * ldh + i];
+            if (x) {
+                v = S::enc(S::dec(v) + S::dec(x[(r0 + rr) * ldx + i]));
+                h[(r0 + rr) * ldh + i] = v;
+            }
+            st[rr * dim + i] = v;
+        }
+        __syncthreads();
+
+        // mean_sq: lane l of a row's 8-lane group owns accumulator a_l
+        const int rr = threadIdx.x >> 3, l = threadIdx.x & 7;
+        const int full = dim & ~7;
+        double a = 0.0;
+        if (rr < nr)
+            for (int i = l; i < full; i += 8) {
+                const double v = double(S::dec(st[rr * dim + i]));
+                a += v * v;
+            }
+        const double s1 = a + __shfl_xor(a, 1, 64);   // a0+a1, a2+a3, ...
+        const double s2 = s1 + __shfl_xor(s1, 2, 64);  // (a0+a1)+(a2+a3), (a4+a5)+(a6+a7)
+        const double s3 = s2 + __shfl_xor(s2, 4, 64);  // the fixed tree
+        if (rr < nr && l == 0) {
+            double tail = 0.0;
+            for (int i = full; i < dim; ++i) {
+                const double v = double(S::dec(st[rr * dim + i]));
+                tail += v * v;
+            }
+            const double ms = (s3 + tail) / double(dim);
+            rsq[rr] = 1.0 / __builtin_sqrt(ms + eps);
+        }
+        __syncthreads();
+
+        for (int idx = threadIdx.x; idx < nr * dim; idx += blockDim.x) {
+            const int r = idx / dim, i = idx - r * dim;
+            const double wv = kind == 2 ? 0.0 : double(S::dec(w[i]));
+            y[(r0 + r) * ldy + i] = S::enc64(norm_out(kind, double(S::dec(st[r * dim + i])), rsq[r], wv));
+        }
+    }
+
+    // Sum over the work-group in a fixed order: butterfly inside each wave,
+    // then the wave partials in wave order. Every thread returns the same value.
+    MG_DEV double block_sum(double v, double *part)
+    {
+        v = wave_sum(v);
+        const int wid = threadIdx.x >> 6;
+        if ((threadIdx.x & 63) == 0) part[wid] = v;
+        __syncthreads();
+        const int nw = (blockDim.x + 63) >> 6;
+        double t = 0.0;
+        for (int i = 0; i < nw; ++i) t += part[i];
+        return t;
+    }
+
+    template <class S, int VEC, int CPT>
+    __global__ __launch_bounds__(1024) void k_norm_tree(int kind, typename S::raw *h,
+                                                        const typename S::raw *__restrict__ x,
+                                                        int64_t ldh, int64_t ldx,
+                                                        const typename S::raw *__restrict__ w,
+                                                        double eps, typename S::raw *y, int64_t ldy,
+                                                        int dim)
+    {
+        using raw = typename S::raw;
+        using comp = typename S::comp;
+        __shared__ double part[16];
+        const int64_t row = blockIdx.x;
+        raw *hr = h + row * ldh;
+        const raw *xr = x ? x + row * ldx : nullptr;
+        raw *yr = y + row * ldy;
+        const int nchunk = dim / VEC;
+
+        comp v[CPT][VEC];
+        double ss = 0.0;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int ch = threadIdx.x + c * blockDim.x;
+            if (ch < nchunk) {
+                Vec<raw, VEC> a = *reinterpret_cast<const Vec<raw, VEC> *>(hr + ch * VEC);
+                if (xr) {
+                    const Vec<raw, VEC> b = *reinterpret_cast<const Vec<raw, VEC> *>(xr + ch * VEC);
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) a.v[e] = S::enc(S::dec(a.v[e]) + S::dec(b.v[e]));
+                    *reinterpret_cast<Vec<raw, VEC> *>(hr + ch * VEC) = a;
+                }
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    v[c][e] = S::dec(a.v[e]);
+                    const double d = double(v[c][e]);
+                    ss += d * d;
+                }
+            }
+        }
+        const double tot = block_sum(ss, part);
+        const double rs = 1.0 / __builtin_sqrt(tot / double(dim) + eps);
+
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int ch = threadIdx.x + c * blockDim.x;
+            if (ch < nchunk) {
+                Vec<raw, VEC> wv;
+                if (kind != 2) wv = *reinterpret_cast<const Vec<raw, VEC> *>(w + ch * VEC);
+                Vec<raw, VEC> o;
+#pragma unroll
+                for (int e = 0; e < VEC; ++e)
+                    o.v[e] = S::enc64(norm_out(kind, double(v[c][e]), rs, kind != 2 ? double(S::dec(wv.v[e])) : 0.0));
+                *reinterpret_cast<Vec<raw, VEC> *>(yr + ch * VEC) = o;
+            }
+        }
+    }
+
+    template <class S, int VEC>
+    void launch_tree(mg_ctx *c, int kind, void *h, const void *x, int64_t ldh, int64_t ldx,
+                     const void *w, double eps, void *y, int64_t ldy, int64_t rows, int dim)
+    {
+        using raw = typename S::raw;
+        const int nchunk = dim / VEC;
+        // threads per row <= 512 where possible; up to 16 chunks per thread
+        int cpt = 1;
+        while ((nchunk + cpt - 1) / cpt > 512 && cpt < 16) cpt *= 2;
+        int nt = (nchunk + cpt - 1) / cpt;
+        need(nt <= 1024, "rmsnorm: dim " + std::to_string(dim) + " too large");
+        nt = (nt + 63) / 64 * 64;
+        auto args = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(unsigned(rows)), dim3(unsigned(nt)), 0, c->stream, kind,
+                               static_cast<raw *>(h), static_cast<const raw *>(x), ldh, ldx,
+                               static_cast<const raw *>(w), eps, static_cast<raw *>(y), ldy, dim);
+        };
+        switch (cpt) {
+        case 1: args(k_norm_tree<S, VEC, 1>); break;
+        case 2: args(k_norm_tree<S, VEC, 2>); break;
+        case 4: args(k_norm_tree<S, VEC, 4>); break;
+        case 8: args(k_norm_tree<S, VEC, 8>); break;
+        default: args(k_norm_tree<S, VEC, 16>); break;
+        }
+        check_launch("k_norm_tree");
+    }
+
+    template <class S>
+    void launch_norm_t(mg_ctx *c, int kind, void *h, const void *x, int64_t ldh, int64_t ldx,
+                       const void *w, double eps, void *y, int64_t ldy, int64_t rows, int dim)
+    {
+        using raw = typename S::raw;
+        if (dim <= kOrderedMaxDim) {
+            const size_t smem = kOrderedRows * sizeof(double) + size_t(kOrderedRows) * dim * sizeof(raw);
+            const unsigned blocks = unsigned((rows + kOrderedRows - 1) / kOrderedRows);
+            hipLaunchKernelGGL(k_norm_ordered<S>, dim3(blocks), dim3(256), smem, c->stream, kind,
+                               static_cast<raw *>(h), static_cast<const raw *>(x), ldh, ldx,
+                               static_cast<const raw *>(w), eps, static_cast<raw *>(y), ldy, rows, dim);
+            check_launch("k_norm_ordered");
+            return;
+        }
+        constexpr int V = 16 / sizeof(raw);
+        const bool vec = dim % V == 0 && ldh % V == 0 && ldy % V == 0 && (!x || ldx % V == 0) &&
+                         aligned16(h) && aligned16(y) && (!x || aligned16(x)) && (kind == 2 || aligned16(w));
+        if (vec)
+            launch_tree<S, V>(c, kind, h, x, ldh, ldx, w, eps, y, ldy, rows, dim);
+        else
+            launch_tree<S, 1>(c, kind, h, x, ldh, ldx, w, eps, y, ldy, rows, dim);
+    }
+
+    void launch_norm(mg_ctx *c, int kind, void *h, const void *x, int64_t ldh, int64_t ldx,
+                     const void *w, double eps, void *y, int64_t ldy, int64_t rows, int64_t dim,
+                     int dt)
+    {
+        need(kind >= 0 && kind <= 2, "rmsnorm: unknown norm kind " + std::to_string(kind));
+        need(rows >= 0 && dim > 0, "rmsnorm: bad shape");
+        need(dim <= (int64_t(1) << 20), "rmsnorm: dim too large");
+        need(rows <= int64_t(0x7fffffff), "rmsnorm: too many rows");
+        need(kind == 2 || w != nullptr, "rmsnorm: weight is NULL for a weighted norm");
+        need(h != nullptr && y != nullptr, "rmsnorm: NULL tensor");
+        need(ldh >= dim && ldy >= dim && (!x || ldx >= dim), "rmsnorm: leading dimension < dim");
+        if (rows == 0) return;
+        switch (dt) {
+        case BF16: launch_norm_t<SBf16>(c, kind, h, x, ldh, ldx, w, eps, y, ldy, rows, int(dim)); break;
+        case F16: launch_norm_t<SF16>(c, kind, h, x, ldh, ldx, w, eps, y, ldy, rows, int(dim)); break;
+        case F32: launch_norm_t<SF32>(c, kind, h, x, ldh, ldx, w, eps, y, ldy, rows, int(dim)); break;
+        case F64: launch_norm_t<SF64>(c, kind, h, x, ldh, ldx, w, eps, y, ldy, rows, int(dim)); break;
+        default: fail("rmsnorm: unknown dtype " + std::to_string(dt));
+        }
+    }
+} // namespace mg

@@ -1,0 +1,341 @@
+// Scaled, masked row softmax for gfx950.
+//
+// Row operator of attention_forward's softmax (src/muse_glimmer.hpp:828-885):
+//   s = rnd_in(x * scale)            scale as an f32 opmath value; s rounds to
+//                                    the input dtype as the eager path does (844-845)
+//   softcap (cap != 0):              s = rnd_in(cap * rnd_in(tanh(rnd_in(s / cap)))),
+//                                    apply_output_tail's op order (920-943), with
+//                                    FDLIBM tanh in f64: the capped score is exact
+//   masked keys (causal / window):   excluded, probability exactly 0
+//   p = exp(s - max) / sum           written once at the output dtype
+// The reference evaluates the exponentials and the sum in f64 (twin) or f32
+// (compat, 856-870); here they are f32 (an accurate exp, f32 sums reduced in a
+// fixed order), which keeps p within a few f32 ulp of the f64 value: the bf16
+// output is within 1 ulp of the twin's and the f32 output within 1e-6 relative.
+//
+// Rows of up to 2048 keys: one wave per row, the row in registers (8 keys per
+// lane per chunk), one read and one write of HBM. Longer rows (decode,
+// q = 1, k = 131072): split over work-groups of 4096 keys; pass A writes each
+// chunk's (max, sum) partial, pass B merges the partials of its row in chunk
+// order (the k_attn_decode_combine rule, src/gpu/gpu_engine.cpp:1816-1857, with
+// the sum rescaled in f64), re-reads its chunk (an L2 hit: a chunk goes to the
+// same XCD in both passes) and writes the probabilities.
+#include "mg_device.hpp"
+#include "mg_internal.hpp"
+
+namespace mg
+{
+    constexpr int kSplitChunk = 4096; // keys per work-group in the split path (256 x 16)
+    constexpr float kNegInf = -__builtin_huge_valf();
+
+    struct SmArgs
+    {
+        int64_t nrows, q, kc;
+        float scale, cap;
+        int mask;
+        int64_t window, q_pos0;
+    };
+
+    // visible key range [lo, hi] of the row
+    MG_DEV void row_range(const SmArgs &a, int64_t row, int64_t &lo, int64_t &hi)
+    {
+        const int64_t qpos = a.q_pos0 + row % a.q;
+        lo = 0;
+        hi = a.kc - 1;
+        if (a.mask >= 1) hi = qpos < hi ? qpos : hi;
+        if (a.mask == 2) {
+            const int64_t l = qpos - a.window + 1;
+            lo = l > 0 ? l : 0;
+        }
+    }
+
+    // score transform: scale (and softcap) with the input dtype's materializations
+    template <class SI>
+    MG_DEV float score(const SmArgs &a, float x)
+    {
+        float s = SI::dec(SI::enc32(x * a.scale));
+        if (a.cap != 0.0f) {
+            // the twin's FDLIBM tanh in f64, so the capped score is bit-identical
+            s = SI::dec(SI::enc32(s / a.cap));
+            s = SI::dec(SI::enc64(mgm::tanh(double(s))));
+            s = SI::dec(SI::enc32(s * a.cap));
+        }
+        return s;
+    }
+
+    // 8 consecutive values -> f32 (two 16-byte loads for f32, one for 16-bit)
+    template <class SI>
+    MG_DEV void load8(const typename SI::raw *p, float *v)
+    {
+        if constexpr (sizeof(typename SI::raw) == 4) {
+            const Vec<float, 4> a = ld16<float, 4>(reinterpret_cast<const float *>(p));
+            const Vec<float, 4> b = ld16<float, 4>(reinterpret_cast<const float *>(p) + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = a.v[e];
+                v[e + 4] = b.v[e];
+            }
+        } else {
+            const Vec<uint16_t, 8> a = ld16<uint16_t, 8>(reinterpret_cast<const uint16_t *>(p));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = SI::dec(a.v[e]);
+        }
+    }
+    template <class SO>
+    MG_DEV void store8(typename SO::raw *p, const float *v)
+    {
+        if constexpr (sizeof(typename SO::raw) == 4) {
+            Vec<float, 4> a, b;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                a.v[e] = v[e];
+                b.v[e] = v[e + 4];
+            }
+            st16<float, 4>(reinterpret_cast<float *>(p), a);
+            st16<float, 4>(reinterpret_cast<float *>(p) + 4, b);
+        } else {
+            Vec<uint16_t, 8> a;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a.v[e] = SO::enc32(v[e]);
+            st16<uint16_t, 8>(reinterpret_cast<uint16_t *>(p), a);
+        }
+    }
+
+    // load the 8 keys j0..j0+7 of a row as transformed scores; masked or
+    // out-of-row keys become -inf
+    template <class SI>
+    MG_DEV void load_scores(const SmArgs &a, const typename SI::raw *xr, int64_t j0, int64_t lo,
+                            int64_t hi, bool vec, float *s)
+    {
+        if (j0 > hi || j0 + 7 < lo || j0 >= a.kc) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[e] = kNegInf;
+            return;
+        }
+        float v[8];
+        if (vec && j0 + 8 <= a.kc) {
+            load8<SI>(xr + j0, v);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = j0 + e < a.kc ? float(SI::dec(xr[j0 + e])) : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t j = j0 + e;
+            s[e] = (j >= lo && j <= hi) ? score<SI>(a, v[e]) : kNegInf;
+        }
+    }
+
+    template <class SO>
+    MG_DEV void store_probs(const SmArgs &a, typename SO::raw *yr, int64_t j0, bool vec, const float *p)
+    {
+        if (j0 >= a.kc) return;
+        if (vec && j0 + 8 <= a.kc) {
+            store8<SO>(yr + j0, p);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (j0 + e < a.kc) yr[j0 + e] = SO::enc32(p[e]);
+        }
+    }
+
+    // --------------------------------------------------------- one wave per row
+    template <class SI, class SO, int CH>
+    __global__ __launch_bounds__(256) void k_softmax_wave(const typename SI::raw *__restrict__ x,
+                                                          typename SO::raw *__restrict__ y, SmArgs a,
+                                                          bool vec)
+    {
+        const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+        const int lane = threadIdx.x & 63;
+        if (row >= a.nrows) return; // whole wave leaves; no block barrier below
+        int64_t lo, hi;
+        row_range(a, row, lo, hi);
+        const typename SI::raw *xr = x + row * a.kc;
+        typename SO::raw *yr = y + row * a.kc;
+
+        float s[CH][8];
+        float m = kNegInf;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            load_scores<SI>(a, xr, int64_t(lane + 64 * c) * 8, lo, hi, vec, s[c]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = s[c][e] > m ? s[c][e] : m;
+        }
+        m = wave_max(m);
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                s[c][e] = s[c][e] == kNegInf ? 0.0f : exp_f32(s[c][e] - m);
+                sum += s[c][e];
+            }
+        sum = wave_sum(sum);
+        const float inv = m == kNegInf ? 0.0f : 1.0f / sum;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[c][e] *= inv;
+            store_probs<SO>(a, yr, int64_t(lane + 64 * c) * 8, vec, s[c]);
+        }
+    }
+
+    // ------------------------------------------------------------- split rows
+    MG_DEV float block_max_f32(float v, float *red)
+    {
+        v = wave_max(v);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        float t = red[0];
+        for (int i = 1; i < int(blockDim.x >> 6); ++i) t = red[i] > t ? red[i] : t;
+        __syncthreads();
+        return t;
+    }
+    MG_DEV float block_sum_f32(float v, float *red)
+    {
+        v = wave_sum(v);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        float t = 0.0f;
+        for (int i = 0; i < int(blockDim.x >> 6); ++i) t += red[i];
+        __syncthreads();
+        return t;
+    }
+
+    // pass A: partial (max, sum exp(s - max)) of chunk blockIdx.x of row blockIdx.y
+    template <class SI>
+    __global__ __launch_bounds__(256) void k_softmax_partial(const typename SI::raw *__restrict__ x, SmArgs a,
+                                                             bool vec, float2 *__restrict__ part)
+    {
+        __shared__ float red[4];
+        const int64_t row = blockIdx.y;
+        int64_t lo, hi;
+        row_range(a, row, lo, hi);
+        const typename SI::raw *xr = x + row * a.kc;
+        const int64_t base = int64_t(blockIdx.x) * kSplitChunk;
+        float s[2][8];
+        float m = kNegInf;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            load_scores<SI>(a, xr, base + int64_t(threadIdx.x + 256 * c) * 8, lo, hi, vec, s[c]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = s[c][e] > m ? s[c][e] : m;
+        }
+        m = block_max_f32(m, red);
+        float sum = 0.0f;
+        if (m != kNegInf)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sum += s[c][e] == kNegInf ? 0.0f : exp_f32(s[c][e] - m);
+        sum = block_sum_f32(sum, red);
+        if (threadIdx.x == 0) part[row * gridDim.x + blockIdx.x] = make_float2(m, sum);
+    }
+
+    // pass B: merge the row's partials in chunk order, then write this chunk
+    template <class SI, class SO>
+    __global__ __launch_bounds__(256) void k_softmax_finish(const typename SI::raw *__restrict__ x,
+                                                            typename SO::raw *__restrict__ y, SmArgs a,
+                                                            bool vec, const float2 *__restrict__ part)
+    {
+        __shared__ float mrg[2];
+        const int64_t row = blockIdx.y;
+        const int nch = int(gridDim.x);
+        if (threadIdx.x == 0) {
+            const float2 *pr = part + row * nch;
+            float M = kNegInf;
+            for (int i = 0; i < nch; ++i) M = pr[i].x > M ? pr[i].x : M;
+            double L = 0.0;
+            if (M != kNegInf)
+                for (int i = 0; i < nch; ++i)
+                    if (pr[i].x != kNegInf) L += double(pr[i].y) * mgm::exp(double(pr[i].x) - double(M));
+            mrg[0] = M;
+            mrg[1] = M == kNegInf ? 0.0f : float(1.0 / L);
+        }
+        __syncthreads();
+        const float M = mrg[0], inv = mrg[1];
+        int64_t lo, hi;
+        row_range(a, row, lo, hi);
+        const typename SI::raw *xr = x + row * a.kc;
+        typename SO::raw *yr = y + row * a.kc;
+        const int64_t base = int64_t(blockIdx.x) * kSplitChunk;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int64_t j0 = base + int64_t(threadIdx.x + 256 * c) * 8;
+            float s[8];
+            load_scores<SI>(a, xr, j0, lo, hi, vec, s);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[e] = s[e] == kNegInf ? 0.0f : exp_f32(s[e] - M) * inv;
+            store_probs<SO>(a, yr, j0, vec, s);
+        }
+    }
+
+    template <class SI, class SO>
+    void launch_softmax_t(mg_ctx *c, const void *x, void *y, const SmArgs &a)
+    {
+        using ri = typename SI::raw;
+        using ro = typename SO::raw;
+        const bool vec = a.kc % 8 == 0 && aligned16(x) && aligned16(y);
+        const ri *xi = static_cast<const ri *>(x);
+        ro *yo = static_cast<ro *>(y);
+        if (a.kc <= 2048) {
+            const unsigned blocks = unsigned((a.nrows + 3) / 4);
+            need((a.nrows + 3) / 4 < (int64_t(1) << 31), "softmax: too many rows");
+            if (a.kc <= 512)
+                hipLaunchKernelGGL((k_softmax_wave<SI, SO, 1>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, vec);
+            else if (a.kc <= 1024)
+                hipLaunchKernelGGL((k_softmax_wave<SI, SO, 2>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, vec);
+            else
+                hipLaunchKernelGGL((k_softmax_wave<SI, SO, 4>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, vec);
+            check_launch("k_softmax_wave");
+            return;
+        }
+        const int64_t nch = (a.kc + kSplitChunk - 1) / kSplitChunk;
+        need(a.nrows <= 65535, "softmax: split path takes at most 65535 rows");
+        need(a.nrows * nch * int64_t(sizeof(float2)) <= c->work_bytes,
+             "softmax: partials exceed the context workspace (raise workspace_bytes at mg_open)");
+        float2 *part = static_cast<float2 *>(c->work);
+        const dim3 grid{unsigned(nch), unsigned(a.nrows), 1u};
+        hipLaunchKernelGGL(k_softmax_partial<SI>, grid, dim3(256), 0, c->stream, xi, a, vec, part);
+        check_launch("k_softmax_partial");
+        hipLaunchKernelGGL((k_softmax_finish<SI, SO>), grid, dim3(256), 0, c->stream, xi, yo, a, vec, part);
+        check_launch("k_softmax_finish");
+    }
+
+    template <class SI>
+    void launch_softmax_out(mg_ctx *c, const void *x, void *y, const SmArgs &a, int dt_out)
+    {
+        switch (dt_out) {
+        case BF16: launch_softmax_t<SI, SBf16>(c, x, y, a); break;
+        case F16: launch_softmax_t<SI, SF16>(c, x, y, a); break;
+        case F32: launch_softmax_t<SI, SF32>(c, x, y, a); break;
+        default: fail("softmax: output dtype must be bf16, f16 or f32");
+        }
+    }
+
+    void launch_softmax(mg_ctx *c, const void *x, void *y, int64_t heads, int64_t q, int64_t kc,
+                        double scale, int mask, int64_t window, int64_t q_pos0, double softcap,
+                        int dt_in, int dt_out)
+    {
+        need(heads >= 0 && q >= 0 && kc >= 0, "softmax: bad shape");
+        need(x && y, "softmax: NULL tensor");
+        need(mask >= 0 && mask <= 2, "softmax: unknown mask kind");
+        need(mask != 2 || window > 0, "softmax: window mask needs window > 0");
+        if (heads == 0 || q == 0 || kc == 0) return;
+        SmArgs a;
+        a.nrows = heads * q;
+        a.q = q;
+        a.kc = kc;
+        a.scale = float(scale);
+        a.cap = float(softcap);
+        a.mask = mask;
+        a.window = window;
+        a.q_pos0 = q_pos0;
+        switch (dt_in) {
+        case F32: launch_softmax_out<SF32>(c, x, y, a, dt_out); break;
+        case BF16: launch_softmax_out<SBf16>(c, x, y, a, dt_out); break;
+        case F16: launch_softmax_out<SF16>(c, x, y, a, dt_out); break;
+        default: fail("softmax: input dtype must be f32, bf16 or f16");
+        }
+    }
+} // namespace mg

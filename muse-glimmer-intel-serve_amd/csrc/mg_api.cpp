@@ -1,0 +1,237 @@
+// C ABI of libmgprims (include/mg_prims.h).
+//
+// The boundary follows the reference's C ABI over its GPU engine
+// (src/gpu/c_api.cpp): no exception crosses it (each entry point catches and
+// stores the message in a thread-local string read by mg_last_error,
+// c_api.cpp:15-17, 35, 170-188) and nothing allocates device memory after
+// mg_open returns (c_api.cpp:9-14): the lookup tables and the reduction
+// workspace are allocated there, and a call whose partials would not fit the
+// workspace fails instead of growing it.
+#include "mg_prims.h"
+
+#include "mg_internal.hpp"
+
+#include <exception>
+#include <string>
+
+namespace
+{
+    thread_local std::string g_err;
+    constexpr int64_t kDefaultWorkspace = int64_t(64) << 20;
+}
+
+// one shape for every entry point: BODY may return; a throw becomes FAIL
+#define MG_GUARD(FAIL, BODY)                         \
+    do {                                             \
+        g_err.clear();                               \
+        try {                                        \
+            BODY                                     \
+        } catch (const std::exception &ex) {         \
+            g_err = ex.what();                       \
+            return FAIL;                             \
+        } catch (...) {                              \
+            g_err = "unknown error";                 \
+            return FAIL;                             \
+        }                                            \
+    } while (0)
+
+namespace
+{
+    mg_ctx *ctx_of(mg_ctx *c)
+    {
+        if (!c) mg::fail("NULL context");
+        mg::check(hipSetDevice(c->device), "hipSetDevice");
+        return c;
+    }
+
+    void release(mg_ctx *c)
+    {
+        if (!c) return;
+        hipSetDevice(c->device);
+        if (c->stream) hipStreamSynchronize(c->stream);
+        if (c->lut) hipFree(c->lut);
+        if (c->work) hipFree(c->work);
+        if (c->own_stream) hipStreamDestroy(c->own_stream);
+        delete c;
+    }
+}
+
+extern "C" {
+
+const char *mg_last_error(void) { return g_err.c_str(); }
+
+int mg_open(int device, void *stream, int64_t workspace_bytes, mg_ctx **out)
+{
+    MG_GUARD(-1, {
+        if (!out) mg::fail("mg_open: NULL out pointer");
+        *out = nullptr;
+        int n = 0;
+        mg::check(hipGetDeviceCount(&n), "hipGetDeviceCount");
+        if (device < 0 || device >= n) mg::fail("mg_open: no HIP device " + std::to_string(device));
+        mg_ctx *c = new mg_ctx();
+        try {
+            c->device = device;
+            mg::check(hipSetDevice(device), "hipSetDevice");
+            hipDeviceProp_t prop;
+            mg::check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+            c->num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+            if (stream) {
+                c->stream = static_cast<hipStream_t>(stream);
+            } else {
+                mg::check(hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "hipStreamCreate");
+                c->stream = c->own_stream;
+            }
+            c->work_bytes = workspace_bytes > 0 ? workspace_bytes : kDefaultWorkspace;
+            mg::check(hipMalloc(&c->work, size_t(c->work_bytes)), "hipMalloc(workspace)");
+            mg::check(hipMalloc(reinterpret_cast<void **>(&c->lut), 4 * 65536 * sizeof(uint16_t)), "hipMalloc(lut)");
+            mg::build_luts(c);
+            mg::check(hipStreamSynchronize(c->stream), "building lookup tables");
+        } catch (...) {
+            release(c);
+            throw;
+        }
+        *out = c;
+        return 0;
+    });
+}
+
+int mg_close(mg_ctx *ctx)
+{
+    MG_GUARD(-1, {
+        release(ctx);
+        return 0;
+    });
+}
+
+int mg_sync(mg_ctx *ctx)
+{
+    MG_GUARD(-1, {
+        mg::check(hipStreamSynchronize(ctx_of(ctx)->stream), "hipStreamSynchronize");
+        return 0;
+    });
+}
+
+int mg_set_stream(mg_ctx *ctx, void *stream)
+{
+    MG_GUARD(-1, {
+        mg_ctx *c = ctx_of(ctx);
+        c->stream = stream ? static_cast<hipStream_t>(stream) : c->own_stream;
+        if (!c->stream) mg::fail("mg_set_stream: NULL stream and the context owns none");
+        return 0;
+    });
+}
+
+void *mg_get_stream(mg_ctx *ctx) { return ctx ? static_cast<void *>(ctx->stream) : nullptr; }
+
+int mg_rmsnorm_rows(mg_ctx *ctx, int kind, const void *x, int64_t ldx, const void *w, double eps,
+                    void *y, int64_t ldy, int64_t rows, int64_t dim, int dtype)
+{
+    MG_GUARD(-1, {
+        mg::launch_norm(ctx_of(ctx), kind, const_cast<void *>(x), nullptr, ldx ? ldx : dim, 0, w, eps, y,
+                        ldy ? ldy : dim, rows, dim, dtype);
+        return 0;
+    });
+}
+
+int mg_residual_rmsnorm(mg_ctx *ctx, int kind, void *h, const void *x, const void *w, double eps,
+                        void *y, int64_t rows, int64_t dim, int dtype)
+{
+    MG_GUARD(-1, {
+        if (!x) mg::fail("residual_rmsnorm: NULL residual operand");
+        mg::launch_norm(ctx_of(ctx), kind, h, x, dim, dim, w, eps, y, dim, rows, dim, dtype);
+        return 0;
+    });
+}
+
+int mg_residual_add(mg_ctx *ctx, void *h, const void *x, int64_t n, int dtype)
+{
+    MG_GUARD(-1, {
+        mg::launch_residual_add(ctx_of(ctx), h, x, n, dtype);
+        return 0;
+    });
+}
+
+int mg_swiglu(mg_ctx *ctx, const void *gate, const void *up, void *out, int64_t n, int dtype)
+{
+    MG_GUARD(-1, {
+        mg::launch_swiglu(ctx_of(ctx), gate, up, out, n, dtype, false);
+        return 0;
+    });
+}
+
+int mg_sigmoid_gate(mg_ctx *ctx, const void *pv, const void *gate, void *out, int64_t n, int dtype)
+{
+    MG_GUARD(-1, {
+        mg::launch_swiglu(ctx_of(ctx), gate, pv, out, n, dtype, true);
+        return 0;
+    });
+}
+
+int mg_scale(mg_ctx *ctx, void *x, int64_t n, double s, int dtype)
+{
+    MG_GUARD(-1, {
+        mg::launch_scale(ctx_of(ctx), x, n, s, dtype);
+        return 0;
+    });
+}
+
+int mg_rope_table(mg_ctx *ctx, double theta, int64_t head_dim, int64_t positions, int dtype,
+                  void *cos_out, void *sin_out)
+{
+    MG_GUARD(-1, {
+        mg::launch_rope_table(ctx_of(ctx), theta, head_dim, positions, dtype, cos_out, sin_out);
+        return 0;
+    });
+}
+
+int mg_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k, int64_t k_heads,
+            int64_t ldk, int64_t tokens, int64_t head_dim, const void *cos_t, const void *sin_t,
+            int64_t table_rows, const int64_t *positions, int64_t pos0, int dtype)
+{
+    MG_GUARD(-1, {
+        if (!positions && (pos0 < 0 || pos0 + tokens > table_rows))
+            mg::fail("rope: positions pos0..pos0+tokens-1 fall outside the table");
+        mg::launch_rope(ctx_of(ctx), q, q_heads, ldq, k, k_heads, ldk, tokens, head_dim, cos_t, sin_t,
+                        table_rows, positions, pos0, dtype);
+        return 0;
+    });
+}
+
+int mg_softmax_rows(mg_ctx *ctx, const void *x, void *y, int64_t heads, int64_t q_rows,
+                    int64_t k_cols, double scale, int mask, int64_t window, int64_t q_pos0,
+                    double softcap, int dtype_in, int dtype_out)
+{
+    MG_GUARD(-1, {
+        mg::launch_softmax(ctx_of(ctx), x, y, heads, q_rows, k_cols, scale, mask, window, q_pos0, softcap,
+                           dtype_in, dtype_out);
+        return 0;
+    });
+}
+
+int mg_softcap(mg_ctx *ctx, void *z, int64_t n, double mult, double cap, int dtype)
+{
+    MG_GUARD(-1, {
+        mg::launch_softcap(ctx_of(ctx), z, n, mult, cap, dtype);
+        return 0;
+    });
+}
+
+int mg_dequant_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, void *out, int64_t rows,
+                    int64_t in, int dtype_out)
+{
+    MG_GUARD(-1, {
+        mg::launch_dequant_q8_0(ctx_of(ctx), qs, d, out, rows, in, dtype_out);
+        return 0;
+    });
+}
+
+int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, int dtype_in,
+                    int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val)
+{
+    MG_GUARD(-1, {
+        mg::launch_vocab(ctx_of(ctx), logits, rows, V, dtype_in, K, lse, argmax, top_idx, top_val);
+        return 0;
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,159 @@
+// Device-side helpers shared by the gfx950 kernels: storage formats, the
+// twin's rounding chain, wave64 reductions, and an accurate f32 exp.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mg_fdlibm.hpp"
+
+#define MG_DEV __device__ __forceinline__
+
+namespace mg
+{
+    enum Dt : int { F64 = 0, BF16 = 1, F16 = 2, F32 = 3 };
+
+    // ------------------------------------------------------------ rounding
+    // f32 -> bf16 bits, RNE (the gfx950 v_cvt_pk_bf16_f32 conversion), NaN
+    // canonicalized to 0x7FC0 as c10 and the twin do (reference rounding.hpp:64-75).
+    MG_DEV uint16_t bf16_bits(float f)
+    {
+        const uint16_t b = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+        return f != f ? uint16_t(0x7fc0) : b;
+    }
+    // f32 -> f16 bits, RNE with subnormals (v_cvt_f16_f32), >= 65520 -> inf,
+    // NaN -> sign | 0x7E00 (reference rounding.hpp:78-123)
+    MG_DEV uint16_t f16_bits(float f)
+    {
+        const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+        return f != f ? uint16_t((h & 0x8000u) | 0x7e00u) : h;
+    }
+    MG_DEV float bf16_f32(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+    MG_DEV float f16_f32(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
+
+    // Storage formats. `comp` is the register type that holds a stored value
+    // exactly (f32 for the 16-bit formats and f32, f64 for f64); `enc64`
+    // rounds an f64 result to storage through f64 -> f32 -> storage RNE, the
+    // twin's chain; `enc` rounds a comp value once.
+    struct SBf16
+    {
+        using raw = uint16_t;
+        using comp = float;
+        static constexpr int dt = BF16;
+        static MG_DEV float dec(raw r) { return bf16_f32(r); }
+        static MG_DEV raw enc32(float f) { return bf16_bits(f); }
+        static MG_DEV raw enc64(double d) { return bf16_bits(float(d)); }
+        static MG_DEV raw enc(comp c) { return bf16_bits(c); }
+    };
+    struct SF16
+    {
+        using raw = uint16_t;
+        using comp = float;
+        static constexpr int dt = F16;
+        static MG_DEV float dec(raw r) { return f16_f32(r); }
+        static MG_DEV raw enc32(float f) { return f16_bits(f); }
+        static MG_DEV raw enc64(double d) { return f16_bits(float(d)); }
+        static MG_DEV raw enc(comp c) { return f16_bits(c); }
+    };
+    struct SF32
+    {
+        using raw = float;
+        using comp = float;
+        static constexpr int dt = F32;
+        static MG_DEV float dec(raw r) { return r; }
+        static MG_DEV raw enc32(float f) { return f; }
+        static MG_DEV raw enc64(double d) { return float(d); }
+        static MG_DEV raw enc(comp c) { return c; }
+    };
+    struct SF64
+    {
+        using raw = double;
+        using comp = double;
+        static constexpr int dt = F64;
+        static MG_DEV double dec(raw r) { return r; }
+        static MG_DEV raw enc32(float f) { return double(f); }
+        static MG_DEV raw enc64(double d) { return d; }
+        static MG_DEV raw enc(comp c) { return c; }
+    };
+
+    // --------------------------------------------------------- 16-byte vectors
+    template <typename T, int N>
+    struct alignas(sizeof(T) * N) Vec
+    {
+        T v[N];
+    };
+    template <typename T, int N>
+    MG_DEV Vec<T, N> ld16(const T *p)
+    {
+        return *reinterpret_cast<const Vec<T, N> *>(p);
+    }
+    template <typename T, int N>
+    MG_DEV void st16(T *p, const Vec<T, N> &v)
+    {
+        *reinterpret_cast<Vec<T, N> *>(p) = v;
+    }
+    // streaming variants: data touched once, keep it out of the caches' way
+    template <typename T, int N>
+    MG_DEV Vec<T, N> ld16_stream(const T *p)
+    {
+        using U = Vec<uint32_t, 4>;
+        U u;
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) u.v[i] = __builtin_nontemporal_load(q + i);
+        return __builtin_bit_cast(Vec<T, N>, u);
+    }
+    template <typename T, int N>
+    MG_DEV void st16_stream(T *p, const Vec<T, N> &v)
+    {
+        using U = Vec<uint32_t, 4>;
+        const U u = __builtin_bit_cast(U, v);
+        uint32_t *q = reinterpret_cast<uint32_t *>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) __builtin_nontemporal_store(u.v[i], q + i);
+    }
+
+    // -------------------------------------------------------- wave64 reductions
+    template <typename T>
+    MG_DEV T wave_sum(T v)
+    {
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+        return v;
+    }
+    template <typename T>
+    MG_DEV T wave_max(T v)
+    {
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const T o = __shfl_xor(v, m, 64);
+            v = o > v ? o : v;
+        }
+        return v;
+    }
+
+    // ---------------------------------------------------------------- f32 exp
+    // e^x for the f32 reductions: Cody–Waite reduction x = n·ln2 + r with the
+    // Cephes two-constant split of ln2, then 2^(r·log2 e) on the hardware exp2
+    // (|r| <= ln2/2, so the f32 product adds < 2^-25 relative), scaled by 2^n.
+    // Relative error ~1.5 ulp; underflows smoothly through subnormals to 0.
+    MG_DEV float exp_f32(float x)
+    {
+        if (x < -104.0f) return 0.0f;
+        x = x > 88.72f ? 88.72f : x;
+        const float n = __builtin_rintf(x * 1.44269504088896341f);
+        float r = __builtin_fmaf(-n, 0.693359375f, x);
+        r = __builtin_fmaf(n, 2.12194440e-4f, r);
+        return __builtin_ldexpf(__builtin_amdgcn_exp2f(r * 1.44269504088896341f), int(n));
+    }
+    // order-preserving map of an f32 to u32 (larger float -> larger key)
+    MG_DEV uint32_t f32_key(float f)
+    {
+        const uint32_t u = __builtin_bit_cast(uint32_t, f);
+        return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    }
+    MG_DEV float key_f32(uint32_t k)
+    {
+        return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+    }
+} // namespace mg

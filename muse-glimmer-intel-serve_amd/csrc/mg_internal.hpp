@@ -1,0 +1,77 @@
+// Host-side internals of libmgprims: the context and the kernel launchers each
+// kernel file provides. Launchers validate shapes before they launch and throw
+// std::runtime_error; the C ABI turns that into -1 + mg_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+
+struct mg_ctx
+{
+    int device = 0;
+    hipStream_t stream = nullptr;     // where every call launches
+    hipStream_t own_stream = nullptr; // created by mg_open when the caller gave none
+    int num_cus = 256;
+    // silu/sigmoid of every 16-bit input, as output bits:
+    // [0] silu bf16, [1] sigmoid bf16, [2] silu f16, [3] sigmoid f16 (65536 each)
+    uint16_t *lut = nullptr;
+    void *work = nullptr; // reduction partials (softmax split rows, vocab chunks)
+    int64_t work_bytes = 0;
+};
+
+namespace mg
+{
+    [[noreturn]] inline void fail(const std::string &m) { throw std::runtime_error(m); }
+    inline void check(hipError_t e, const char *what)
+    {
+        if (e != hipSuccess) fail(std::string(what) + ": " + hipGetErrorString(e));
+    }
+    inline void check_launch(const char *what) { check(hipGetLastError(), what); }
+    inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+    inline int dt_size(int dt)
+    {
+        switch (dt) {
+        case 0: return 8;
+        case 1: case 2: return 2;
+        case 3: return 4;
+        default: fail("unknown dtype " + std::to_string(dt));
+        }
+    }
+    inline void need(bool ok, const std::string &m)
+    {
+        if (!ok) fail(m);
+    }
+
+    // lookup tables, built at mg_open (k_elementwise.hip)
+    void build_luts(mg_ctx *c);
+
+    // k_norm.hip
+    void launch_norm(mg_ctx *c, int kind, void *h, const void *x, int64_t ldh, int64_t ldx,
+                     const void *w, double eps, void *y, int64_t ldy, int64_t rows, int64_t dim,
+                     int dt);
+    // k_elementwise.hip
+    void launch_residual_add(mg_ctx *c, void *h, const void *x, int64_t n, int dt);
+    void launch_swiglu(mg_ctx *c, const void *g, const void *u, void *out, int64_t n, int dt,
+                       bool sigmoid_gate);
+    void launch_scale(mg_ctx *c, void *x, int64_t n, double s, int dt);
+    void launch_softcap(mg_ctx *c, void *z, int64_t n, double mult, double cap, int dt);
+    // k_rope.hip
+    void launch_rope_table(mg_ctx *c, double theta, int64_t dim, int64_t T, int dt, void *co,
+                           void *si);
+    void launch_rope(mg_ctx *c, void *q, int64_t qh, int64_t ldq, void *k, int64_t kh,
+                     int64_t ldk, int64_t tokens, int64_t dim, const void *co, const void *si,
+                     int64_t table_rows, const int64_t *pos, int64_t pos0, int dt);
+    // k_softmax.hip
+    void launch_softmax(mg_ctx *c, const void *x, void *y, int64_t heads, int64_t q,
+                        int64_t kc, double scale, int mask, int64_t window, int64_t q_pos0,
+                        double softcap, int dt_in, int dt_out);
+    // k_q8.hip
+    void launch_dequant_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, void *out,
+                             int64_t rows, int64_t in, int dt_out);
+    // k_vocab.hip
+    void launch_vocab(mg_ctx *c, const void *logits, int64_t rows, int64_t V, int dt_in,
+                      int64_t K, double *lse, int64_t *amax, int64_t *top_idx, float *top_val);
+} // namespace mg

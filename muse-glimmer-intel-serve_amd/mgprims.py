@@ -1,0 +1,212 @@
+"""Python binding of libmgprims (include/mg_prims.h) over ctypes.
+
+The host-side mirror of the reference's primitive interface for callers that
+hold device tensors in PyTorch: the names and argument meanings follow the
+reference's functions (``muse::rmsnorm_rows``, ``apply_rope``,
+``build_rope_table``, ``apply_output_tail`` in src/muse_glimmer.hpp, the
+residual / SwiGLU / output-gate loops of the layer body, the Q8_0 dequantize of
+src/gpu/gpu_engine.cpp, and the sampler's logsumexp / argmax / top-k), and
+errors surface as exceptions carrying ``mg_last_error()``, as the reference's
+host functions throw ``std::runtime_error``.
+
+PyTorch only supplies device memory and the stream: every op runs a HIP kernel
+of libmgprims.so on the context's stream (by default torch's current stream).
+There is no CPU fallback: constructing ``Prims`` fails if the library is not
+built or no GPU is visible.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "libmgprims.so")
+HEADER = os.path.join(ROOT, "include", "mg_prims.h")
+
+F64, BF16, F16, F32 = 0, 1, 2, 3
+CENTERED, PLAIN, WEIGHTLESS = 0, 1, 2
+MASK_NONE, MASK_CAUSAL, MASK_WINDOW = 0, 1, 2
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int64
+_D = ctypes.c_double
+_INT = ctypes.c_int
+
+_SIGS = {
+    "mg_last_error": ([], ctypes.c_char_p),
+    "mg_open": ([_INT, _P, _I, ctypes.POINTER(_P)], _INT),
+    "mg_close": ([_P], _INT),
+    "mg_sync": ([_P], _INT),
+    "mg_set_stream": ([_P, _P], _INT),
+    "mg_get_stream": ([_P], _P),
+    "mg_rmsnorm_rows": ([_P, _INT, _P, _I, _P, _D, _P, _I, _I, _I, _INT], _INT),
+    "mg_residual_rmsnorm": ([_P, _INT, _P, _P, _P, _D, _P, _I, _I, _INT], _INT),
+    "mg_residual_add": ([_P, _P, _P, _I, _INT], _INT),
+    "mg_swiglu": ([_P, _P, _P, _P, _I, _INT], _INT),
+    "mg_sigmoid_gate": ([_P, _P, _P, _P, _I, _INT], _INT),
+    "mg_scale": ([_P, _P, _I, _D, _INT], _INT),
+    "mg_rope_table": ([_P, _D, _I, _I, _INT, _P, _P], _INT),
+    "mg_rope": ([_P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _INT], _INT),
+    "mg_softmax_rows": ([_P, _P, _P, _I, _I, _I, _D, _INT, _I, _I, _D, _INT, _INT], _INT),
+    "mg_softcap": ([_P, _P, _I, _D, _D, _INT], _INT),
+    "mg_dequant_q8_0": ([_P, _P, _P, _P, _I, _I, _INT], _INT),
+    "mg_vocab_reduce": ([_P, _P, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
+}
+
+_lib = None
+
+
+def header_symbols():
+    """Every function the public header declares."""
+    with open(HEADER) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"\b(mg_[a-z0-9_]+)\s*\(", text)))
+
+
+def load_library(path: str = LIB_PATH):
+    """dlopen libmgprims.so and bind every exported signature (no GPU needed)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built: run `python muse-glimmer-intel-serve_amd/build.py`")
+        L = ctypes.CDLL(path)
+        for name, (args, res) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+class MgError(RuntimeError):
+    pass
+
+
+def _dtype_code(t):
+    import torch
+    return {torch.float64: F64, torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}[t.dtype]
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+class Prims:
+    """A libmgprims context bound to one device and stream."""
+
+    def __init__(self, device: int = 0, stream=None, workspace_bytes: int = 0):
+        import torch
+        self.lib = load_library()
+        if stream is None:
+            stream = torch.cuda.current_stream(device).cuda_stream
+        h = _P()
+        self._check(self.lib.mg_open(device, ctypes.c_void_p(stream), workspace_bytes, ctypes.byref(h)))
+        self.h = h
+        self.device = device
+
+    def _check(self, rc):
+        if rc != 0:
+            raise MgError(self.lib.mg_last_error().decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self._check(self.lib.mg_close(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def sync(self):
+        self._check(self.lib.mg_sync(self.h))
+
+    def set_stream(self, stream):
+        self._check(self.lib.mg_set_stream(self.h, ctypes.c_void_p(stream)))
+
+    def stream(self):
+        return self.lib.mg_get_stream(self.h)
+
+    # ------------------------------------------------------------- norms
+    def rmsnorm_rows(self, kind, X, w, eps, Y):
+        """muse::rmsnorm_rows (src/muse_glimmer.hpp:572-608); X, Y: [rows, dim]."""
+        rows, dim = X.shape
+        self._check(self.lib.mg_rmsnorm_rows(self.h, kind, _ptr(X), X.stride(0), _ptr(w), eps, _ptr(Y),
+                                             Y.stride(0), rows, dim, _dtype_code(X)))
+
+    def residual_rmsnorm(self, kind, h, x, w, eps, y):
+        """h = rnd(h + x) in place, then y = norm(h)."""
+        rows, dim = h.shape
+        assert h.is_contiguous() and x.is_contiguous() and y.is_contiguous()
+        self._check(self.lib.mg_residual_rmsnorm(self.h, kind, _ptr(h), _ptr(x), _ptr(w), eps, _ptr(y),
+                                                 rows, dim, _dtype_code(h)))
+
+    def residual_add(self, h, x):
+        self._check(self.lib.mg_residual_add(self.h, _ptr(h), _ptr(x), h.numel(), _dtype_code(h)))
+
+    # ------------------------------------------------------- elementwise
+    def swiglu(self, gate, up, out):
+        self._check(self.lib.mg_swiglu(self.h, _ptr(gate), _ptr(up), _ptr(out), gate.numel(), _dtype_code(gate)))
+
+    def sigmoid_gate(self, pv, gate, out):
+        self._check(self.lib.mg_sigmoid_gate(self.h, _ptr(pv), _ptr(gate), _ptr(out), pv.numel(), _dtype_code(pv)))
+
+    def scale(self, x, s):
+        self._check(self.lib.mg_scale(self.h, _ptr(x), x.numel(), s, _dtype_code(x)))
+
+    # --------------------------------------------------------------- rope
+    def build_rope_table(self, theta, head_dim, positions, dtype):
+        """muse::build_rope_table (src/muse_glimmer.hpp:625-674) -> (cos, sin) [positions, head_dim/2]."""
+        import torch
+        co = torch.empty((positions, head_dim // 2), dtype=dtype, device=f"cuda:{self.device}")
+        si = torch.empty_like(co)
+        self._check(self.lib.mg_rope_table(self.h, theta, head_dim, positions, _dtype_code(co), _ptr(co), _ptr(si)))
+        return co, si
+
+    def apply_rope(self, q, k, cos, sin, positions=None, pos0=0):
+        """In-place rotate-half RoPE (src/muse_glimmer.hpp:681-705) on q [T, Hq, D] and k [T, Hk, D]."""
+        T, qh, D = q.shape
+        kh = k.shape[1] if k is not None else 0
+        self._check(self.lib.mg_rope(self.h, _ptr(q), qh, q.stride(0), _ptr(k), kh,
+                                     k.stride(0) if k is not None else 0, T, D, _ptr(cos), _ptr(sin),
+                                     cos.shape[0], _ptr(positions), pos0, _dtype_code(q)))
+
+    # ------------------------------------------------------------ softmax
+    def softmax_rows(self, x, y, scale, mask=MASK_NONE, window=0, q_pos0=0, softcap=0.0):
+        """x [heads, q, k] scores -> y probabilities (attention_forward's softmax, src/muse_glimmer.hpp:828-885)."""
+        heads, q, kc = x.shape
+        assert x.is_contiguous() and y.is_contiguous()
+        self._check(self.lib.mg_softmax_rows(self.h, _ptr(x), _ptr(y), heads, q, kc, scale, mask, window, q_pos0,
+                                             softcap, _dtype_code(x), _dtype_code(y)))
+
+    def apply_output_tail(self, z, mult, cap):
+        """muse::apply_output_tail (src/muse_glimmer.hpp:920-943), in place."""
+        self._check(self.lib.mg_softcap(self.h, _ptr(z), z.numel(), mult, cap, _dtype_code(z)))
+
+    # --------------------------------------------------------------- Q8_0
+    def dequant_q8_0(self, qs, d, out):
+        """qs int8 [rows, in], d f16 scales [rows, in/32] -> out [rows, in] (k_dequant_q8)."""
+        rows, n_in = qs.shape
+        self._check(self.lib.mg_dequant_q8_0(self.h, _ptr(qs), _ptr(d), _ptr(out), rows, n_in, _dtype_code(out)))
+
+    # -------------------------------------------------------------- vocab
+    def vocab_reduce(self, logits, K, lse=None, argmax=None, top_idx=None, top_val=None):
+        """Per row: logsumexp, first argmax, top-K (value desc, index asc)."""
+        import torch
+        rows, V = logits.shape
+        dev = logits.device
+        if lse is None:
+            lse = torch.empty(rows, dtype=torch.float64, device=dev)
+        if argmax is None:
+            argmax = torch.empty(rows, dtype=torch.int64, device=dev)
+        if K > 0 and top_idx is None:
+            top_idx = torch.empty((rows, K), dtype=torch.int64, device=dev)
+        if K > 0 and top_val is None:
+            top_val = torch.empty((rows, K), dtype=torch.float32, device=dev)
+        self._check(self.lib.mg_vocab_reduce(self.h, _ptr(logits), rows, V, _dtype_code(logits), K, _ptr(lse),
+                                             _ptr(argmax), _ptr(top_idx) if K > 0 else None,
+                                             _ptr(top_val) if K > 0 else None))
+        return lse, argmax, top_idx, top_val

@@ -1,0 +1,532 @@
+// ORACLE — test infrastructure only.
+//
+// A CPU restatement of the reference's CPU tensor path for the non-GEMM
+// primitives: the f64 oracle and its bf16/f16 "twin" (exact f64 arithmetic
+// between materializations, storage rounding at each one). Only tests/,
+// __graft_entry__.smoke() and bench.py's cpu_baseline leg load this library,
+// and only as the checker or the timed CPU baseline. The shipped HIP library
+// never links, loads or calls it.
+//
+// Every function cites the reference lines it follows (paths relative to
+// /root/reference). Build flags follow the reference's (CMakeLists.txt:11-14):
+// -O3 -ffp-contract=off -fno-math-errno -fopenmp, never fast-math.
+//
+// Dtype codes: 0 = f64, 1 = bf16, 2 = f16 (prec::Dtype order, rounding.hpp:31-36),
+// 3 = f32 (this build's extra storage type; rounding = one f64->f32 RNE).
+//
+// Pinning (what checks each part independently of this restatement):
+//   rounding      exhaustive over all 2^16 bf16/f16 patterns + crafted f32 ties,
+//                 bitwise vs oracle/_ref (reference rounding.hpp compiled)
+//   fmath         bitwise vs oracle/_ref (reference fmath.hpp compiled), ulp vs libm
+//   mean_sq/norm  bitwise vs oracle/_ref (reference rmsnorm_rows compiled)
+//   rope          bitwise vs oracle/_ref (reference build_rope_table/apply_rope)
+//   silu/sigmoid  bitwise vs oracle/_ref (reference ok_siluv/ok_sigmoidv)
+//   output tail   bitwise vs oracle/_ref (reference apply_output_tail)
+//   residual/swiglu/gate loops: composition of the pinned pieces, plus
+//                 brute-force f64 identities in tests
+//   softmax       invariants (sum 1, masked exactly 0, shift invariance) and an
+//                 independent numpy f64 brute force in tests
+//   q8_0 dequant  exactness argument + brute force in tests (no CPU dequant
+//                 exists in the reference; formula from gpu_engine.cpp:1117-1171)
+//   q8_0 quantize parity unpinned against llama.cpp (not vendored); checked
+//                 against its own stated invariants only
+//   vocab         full numpy sort / np.argmax / f64 lse brute force in tests
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <numeric>
+#include <vector>
+
+#include "fmath_port.hpp"
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+namespace orc
+{
+    enum Dt : int { F64 = 0, BF16 = 1, F16 = 2, F32 = 3 };
+
+    // ---------------------------------------------------------------- rounding
+    // rounding.hpp:64-75 — f64 -> f32 (hardware RNE) -> bf16 (c10 RNE), NaN -> 0x7FC0
+    inline uint16_t bf16_bits(double x)
+    {
+        float f = float(x);
+        uint32_t u;
+        std::memcpy(&u, &f, 4);
+        if (f != f) return 0x7fc0;
+        return uint16_t((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    }
+    inline double bf16_value(uint16_t b)
+    {
+        const uint32_t u = uint32_t(b) << 16;
+        float f;
+        std::memcpy(&f, &u, 4);
+        return double(f);
+    }
+
+    // rounding.hpp:78-123 (encode step) — f64 -> f32 -> f16 RNE, subnormals kept,
+    // >= 65520 -> inf, NaN -> sign | 0x7E00
+    inline uint16_t f16_bits(double x)
+    {
+        const float f = float(x);
+        uint32_t u;
+        std::memcpy(&u, &f, 4);
+        const uint32_t sign = (u >> 16) & 0x8000u;
+        const uint32_t a = u & 0x7fffffffu;
+        if (a > 0x7f800000u) return uint16_t(sign | 0x7e00u);
+        if (a >= 0x477ff000u) return uint16_t(sign | 0x7c00u);
+        if (a < 0x38800000u) {
+            if (a < 0x33000000u) return uint16_t(sign);
+            const int sh = 126 - int(a >> 23);
+            const uint32_t m = (a & 0x007fffffu) | 0x00800000u;
+            uint32_t q = m >> sh;
+            const uint32_t rem = m & ((1u << sh) - 1u), halfway = 1u << (sh - 1);
+            if (rem > halfway || (rem == halfway && (q & 1u))) ++q;
+            return uint16_t(sign | q);
+        }
+        const uint32_t v = a + 0xc8000000u;
+        uint32_t q = v >> 13;
+        const uint32_t rem = v & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ++q;
+        return uint16_t(sign | q);
+    }
+    // safetensors.hpp:100-130 (st::f16_to_f64) — exact decode, subnormals normalized
+    inline double f16_value(uint16_t h)
+    {
+        const uint32_t s = uint32_t(h >> 15) << 31, e = (h >> 10) & 0x1fu;
+        uint32_t m = h & 0x3ffu, out;
+        if (e == 0) {
+            if (m == 0) out = s;
+            else {
+                int k = -1;
+                do { m <<= 1; ++k; } while (!(m & 0x400u));
+                out = s | (uint32_t(127 - 15 - k) << 23) | ((m & 0x3ffu) << 13);
+            }
+        } else if (e == 0x1fu) {
+            out = s | 0x7f800000u | (m << 13);
+        } else {
+            out = s | ((e + 112u) << 23) | (m << 13);
+        }
+        float f;
+        std::memcpy(&f, &out, 4);
+        return double(f);
+    }
+
+    // rounding.hpp:155-166 (round_act) extended with f32 storage
+    inline double rnd(int dt, double x)
+    {
+        switch (dt) {
+        case BF16: return bf16_value(bf16_bits(x));
+        case F16: return f16_value(f16_bits(x));
+        case F32: return double(float(x));
+        default: return x;
+        }
+    }
+    // python-float scalars become f32 opmath values in a low-precision run
+    // (muse_glimmer.hpp:769-773, 929-931)
+    inline double opmath(int dt, double s) { return dt == F64 ? s : double(float(s)); }
+
+    // muse_glimmer.hpp:493-494
+    inline double silu(double x) { return x / (1.0 + orc::exp(-x)); }
+    inline double sigmoid(double x) { return 1.0 / (1.0 + orc::exp(-x)); }
+
+    // muse_glimmer.hpp:509-527 — 8 interleaved accumulators, fixed tree, tail, /n
+    inline double mean_sq(const double *x, int64_t n)
+    {
+        double a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int64_t i = 0;
+        for (; i + 8 <= n; i += 8)
+            for (int l = 0; l < 8; ++l) a[l] += x[i + l] * x[i + l];
+        double tail = 0;
+        for (; i < n; ++i) tail += x[i] * x[i];
+        return ((((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail) / double(n);
+    }
+
+    // muse_glimmer.hpp:558-563
+    enum Norm : int { CENTERED = 0, PLAIN = 1, WEIGHTLESS = 2 };
+
+    // muse_glimmer.hpp:572-608 (pure / twin branch: f64 internals, one rounding)
+    inline void norm_row(int kind, const double *x, const double *w, double eps, double *y,
+                         int64_t dim, int dt)
+    {
+        const double rs = 1.0 / std::sqrt(mean_sq(x, dim) + eps);
+        for (int64_t i = 0; i < dim; ++i) {
+            double v = x[i] * rs;
+            if (kind == CENTERED) v = v * (1.0 + w[i]);
+            else if (kind == PLAIN) v = v * w[i];
+            y[i] = rnd(dt, v);
+        }
+    }
+
+    // 2^-53-scaled top 53 bits of one splitmix64 output
+    inline uint64_t splitmix(uint64_t seed, uint64_t i)
+    {
+        uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    inline double unif(uint64_t seed, uint64_t i) { return double(splitmix(seed, i) >> 11) * 0x1p-53; }
+
+    inline void store(int dt, void *dst, int64_t i, double v)
+    {
+        switch (dt) {
+        case BF16: static_cast<uint16_t *>(dst)[i] = bf16_bits(v); break;
+        case F16: static_cast<uint16_t *>(dst)[i] = f16_bits(v); break;
+        case F32: static_cast<float *>(dst)[i] = float(v); break;
+        default: static_cast<double *>(dst)[i] = v; break;
+        }
+    }
+    inline double load(int dt, const void *src, int64_t i)
+    {
+        switch (dt) {
+        case BF16: return bf16_value(static_cast<const uint16_t *>(src)[i]);
+        case F16: return f16_value(static_cast<const uint16_t *>(src)[i]);
+        case F32: return double(static_cast<const float *>(src)[i]);
+        default: return static_cast<const double *>(src)[i];
+        }
+    }
+} // namespace orc
+
+using namespace orc;
+
+extern "C"
+{
+    // ------------------------------------------------------------ conversions
+    void or_to_f64(const void *src, int dt, double *dst, int64_t n)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) dst[i] = load(dt, src, i);
+    }
+    void or_from_f64(const double *src, int dt, void *dst, int64_t n)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) store(dt, dst, i, src[i]);
+    }
+    // rounding.hpp:171-181 (round_rows), with f32 storage added
+    void or_round(int dt, double *x, int64_t n)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) x[i] = rnd(dt, x[i]);
+    }
+
+    // ------------------------------------------------------------- generators
+    // Portable seeded data: splitmix64 -> uniform [0,1) -> Box-Muller with the
+    // FDLIBM log/cos/sin above (no libm), so every platform draws the same bits.
+    void or_fill_normal(uint64_t seed, double mean, double stdv, int dt, void *out, int64_t n)
+    {
+        const double two_pi = 6.283185307179586;
+#pragma omp parallel for schedule(static)
+        for (int64_t p = 0; p < (n + 1) / 2; ++p) {
+            const double u1 = unif(seed, uint64_t(2 * p)), u2 = unif(seed, uint64_t(2 * p + 1));
+            const double r = std::sqrt(-2.0 * orc::log(1.0 - u1));
+            const double a = two_pi * u2;
+            store(dt, out, 2 * p, mean + stdv * (r * orc::cos(a)));
+            if (2 * p + 1 < n) store(dt, out, 2 * p + 1, mean + stdv * (r * orc::sin(a)));
+        }
+    }
+    void or_fill_uniform(uint64_t seed, double lo, double hi, int dt, void *out, int64_t n)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) store(dt, out, i, lo + (hi - lo) * unif(seed, uint64_t(i)));
+    }
+    // int8 uniform over [lo, hi] (inclusive)
+    void or_fill_int8(uint64_t seed, int lo, int hi, int8_t *out, int64_t n)
+    {
+        const uint64_t span = uint64_t(hi - lo + 1);
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) out[i] = int8_t(lo + int((splitmix(seed, uint64_t(i)) >> 32) % span));
+    }
+
+    // ------------------------------------------------------------------ fmath
+    void or_expv(const double *x, double *y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = orc::exp(x[i]); }
+    void or_logv(const double *x, double *y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = orc::log(x[i]); }
+    void or_expm1v(const double *x, double *y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = orc::expm1(x[i]); }
+    void or_tanhv(const double *x, double *y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = orc::tanh(x[i]); }
+    void or_sinv(const double *x, double *y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = orc::sin(x[i]); }
+    void or_cosv(const double *x, double *y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = orc::cos(x[i]); }
+    void or_powv(double base, const double *e, double *y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = orc::pow(base, e[i]); }
+    void or_siluv(const double *x, double *y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = silu(x[i]); }
+    void or_sigmoidv(const double *x, double *y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = sigmoid(x[i]); }
+    void or_meansq(const double *X, double *out, int64_t rows, int64_t dim)
+    {
+        for (int64_t r = 0; r < rows; ++r) out[r] = mean_sq(X + r * dim, dim);
+    }
+
+    // ------------------------------------------------------------------ norms
+    // muse_glimmer.hpp:572-608 — rmsnorm_rows(kind, X, w, eps, Y, rows, dim, false, dt)
+    void or_rmsnorm_rows(int kind, const double *X, const double *w, double eps, double *Y,
+                         int64_t rows, int64_t dim, int dt)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) norm_row(kind, X + r * dim, w, eps, Y + r * dim, dim, dt);
+    }
+
+    // Residual add (muse_glimmer.hpp:1023-1024, 1048-1049: h = rnd(h + m)) followed
+    // by the next norm on the updated stream (muse_glimmer.hpp:1028-1031). The
+    // reference runs them as two loops; the fused op has the same arithmetic.
+    void or_residual_rmsnorm(int kind, double *h, const double *x, const double *w, double eps,
+                             double *Y, int64_t rows, int64_t dim, int dt)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            double *hr = h + r * dim;
+            const double *xr = x + r * dim;
+            for (int64_t i = 0; i < dim; ++i) hr[i] = rnd(dt, hr[i] + xr[i]);
+            norm_row(kind, hr, w, eps, Y + r * dim, dim, dt);
+        }
+    }
+
+    // muse_glimmer.hpp:1023-1024 — h = rnd(h + x)
+    void or_residual_add(double *h, const double *x, int64_t n, int dt)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) h[i] = rnd(dt, h[i] + x[i]);
+    }
+
+    // ------------------------------------------------------------ elementwise
+    // muse_glimmer.hpp:1036-1039 — lp: rnd(rnd(silu(g)) * u); f64: silu(g) * u
+    void or_swiglu(const double *g, const double *u, double *out, int64_t n, int dt)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i)
+            out[i] = dt == F64 ? silu(g[i]) * u[i] : rnd(dt, rnd(dt, silu(g[i])) * u[i]);
+    }
+    // muse_glimmer.hpp:896-906 — lp: rnd(rnd(pv) * rnd(sigmoid(gate))); f64: pv * sigmoid(gate)
+    void or_sigmoid_gate(const double *pv, const double *gate, double *out, int64_t n, int dt)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i)
+            out[i] = dt == F64 ? pv[i] * sigmoid(gate[i])
+                               : rnd(dt, rnd(dt, pv[i]) * rnd(dt, sigmoid(gate[i])));
+    }
+    // muse_glimmer.hpp:803-807 — q = rnd(q * f32(qk_scale)) in lp, q * qk_scale in f64
+    void or_scale(double *x, int64_t n, double s, int dt)
+    {
+        const double sc = opmath(dt, s);
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) x[i] = rnd(dt, x[i] * sc);
+    }
+
+    // ------------------------------------------------------------------- rope
+    // muse_glimmer.hpp:625-674 — build_rope_table(c, T, f32_compat, dt). The f32
+    // chain runs when dt != f64 (or f32_compat); with dt == f32 the table is
+    // stored at f32 (the f32_compat branch, 654-656).
+    void or_rope_table(double theta, int64_t dim, int64_t T, int dt, double *cos_out, double *sin_out)
+    {
+        const int64_t half = dim / 2;
+        if (dt != F64) {
+            std::vector<float> inv(static_cast<size_t>(half));
+            for (int64_t j = 0; j < half; ++j) {
+                const float e = float(2 * j) / float(dim);
+                const float pw = float(orc::pow(double(float(theta)), double(e)));
+                inv[size_t(j)] = 1.0f / pw;
+            }
+#pragma omp parallel for schedule(static)
+            for (int64_t t = 0; t < T; ++t)
+                for (int64_t j = 0; j < half; ++j) {
+                    const float ang = float(t) * inv[size_t(j)];
+                    const double cv = orc::cos(double(ang)), sv = orc::sin(double(ang));
+                    cos_out[t * half + j] = rnd(dt, cv);
+                    sin_out[t * half + j] = rnd(dt, sv);
+                }
+            return;
+        }
+        std::vector<double> inv(static_cast<size_t>(half));
+        for (int64_t j = 0; j < half; ++j) inv[size_t(j)] = 1.0 / orc::pow(theta, double(2 * j) / double(dim));
+#pragma omp parallel for schedule(static)
+        for (int64_t t = 0; t < T; ++t)
+            for (int64_t j = 0; j < half; ++j) {
+                const double ang = double(t) * inv[size_t(j)];
+                cos_out[t * half + j] = orc::cos(ang);
+                sin_out[t * half + j] = orc::sin(ang);
+            }
+    }
+
+    // muse_glimmer.hpp:681-705 (apply_rope), driven over (token, head) as
+    // muse_glimmer.hpp:809-819 does. x is [tokens, heads, dim] with token stride
+    // `tok_stride` elements; token t uses table row pos[t].
+    void or_apply_rope(double *x, int64_t tokens, int64_t heads, int64_t dim, int64_t tok_stride,
+                       const double *cos_t, const double *sin_t, const int64_t *pos, int dt)
+    {
+        const int64_t half = dim / 2;
+#pragma omp parallel for schedule(static) collapse(2)
+        for (int64_t t = 0; t < tokens; ++t)
+            for (int64_t h = 0; h < heads; ++h) {
+                double *p = x + t * tok_stride + h * dim;
+                const double *co = cos_t + pos[t] * half, *si = sin_t + pos[t] * half;
+                for (int64_t j = 0; j < half; ++j) {
+                    const double lo = p[j], hi = p[j + half];
+                    if (dt != F64) {
+                        p[j] = rnd(dt, rnd(dt, lo * co[j]) + rnd(dt, -hi * si[j]));
+                        p[j + half] = rnd(dt, rnd(dt, hi * co[j]) + rnd(dt, lo * si[j]));
+                    } else {
+                        p[j] = lo * co[j] - hi * si[j];
+                        p[j + half] = hi * co[j] + lo * si[j];
+                    }
+                }
+            }
+    }
+
+    // ------------------------------------------------------------ output tail
+    // muse_glimmer.hpp:920-943 — z*mult, z/cap, tanh, z*cap, each materialized in lp
+    void or_softcap(double *z, int64_t n, double mult, double cap, int dt)
+    {
+        const double m = opmath(dt, mult), c = opmath(dt, cap);
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) {
+            double v = z[i];
+            if (m != 1.0) v = rnd(dt, v * m);
+            if (c != 0.0) {
+                v = rnd(dt, v / c);
+                v = rnd(dt, orc::tanh(v));
+                v = rnd(dt, v * c);
+            }
+            z[i] = v;
+        }
+    }
+
+    // ---------------------------------------------------------------- softmax
+    // The masked, scaled row softmax of attention_forward (muse_glimmer.hpp:828-885),
+    // as a standalone row operator over a [heads, q, k] score block:
+    //   s = x * scale  (scale as f32 opmath when dt_in != f64; s materializes at
+    //                   dt_in, the eager `rnd(rnd(dot) * scaling)` of 844-845)
+    //   optional tanh softcap in apply_output_tail's op order (920-943): s/cap,
+    //                   tanh, *cap, each materialized at dt_in
+    //   mask: 0 none, 1 causal (k <= qpos), 2 window (qpos-window < k <= qpos),
+    //         qpos = q_pos0 + row; masked keys are excluded exactly (p = 0)
+    //   m = max, e = exp(s - m) (FDLIBM, f64), ascending f64 sum, p = e / sum,
+    //   output rounded once to dt_out (the `.to(query.dtype)` of 866-868).
+    // A row with no unmasked key writes zeros.
+    void or_softmax_rows(const double *x, double *y, int64_t heads, int64_t q, int64_t kc,
+                         double scale, int mask, int64_t window, int64_t q_pos0, double softcap,
+                         int dt_in, int dt_out)
+    {
+        const double sc = opmath(dt_in, scale), cap = opmath(dt_in, softcap);
+#pragma omp parallel
+        {
+            std::vector<double> s(static_cast<size_t>(kc));
+#pragma omp for schedule(static) collapse(2)
+            for (int64_t h = 0; h < heads; ++h)
+                for (int64_t r = 0; r < q; ++r) {
+                    const double *xr = x + (h * q + r) * kc;
+                    double *yr = y + (h * q + r) * kc;
+                    const int64_t qpos = q_pos0 + r;
+                    int64_t lo = 0, hi = kc - 1;
+                    if (mask >= 1) hi = std::min<int64_t>(hi, qpos);
+                    if (mask == 2) lo = std::max<int64_t>(0, qpos - window + 1);
+                    for (int64_t j = 0; j < kc; ++j) yr[j] = 0.0;
+                    if (hi < lo) continue;
+                    double mx = -HUGE_VAL;
+                    for (int64_t j = lo; j <= hi; ++j) {
+                        double v = rnd(dt_in, xr[j] * sc);
+                        if (cap != 0.0) {
+                            v = rnd(dt_in, v / cap);
+                            v = rnd(dt_in, orc::tanh(v));
+                            v = rnd(dt_in, v * cap);
+                        }
+                        s[size_t(j)] = v;
+                        mx = std::max(mx, v);
+                    }
+                    double sum = 0;
+                    for (int64_t j = lo; j <= hi; ++j) {
+                        s[size_t(j)] = orc::exp(s[size_t(j)] - mx);
+                        sum += s[size_t(j)];
+                    }
+                    for (int64_t j = lo; j <= hi; ++j) yr[j] = rnd(dt_out, s[size_t(j)] / sum);
+                }
+        }
+    }
+
+    // ------------------------------------------------------------------- Q8_0
+    // k_dequant_q8 (gpu_engine.cpp:1117-1171): out = rnd(f32(int8 q) * f32(f16 d));
+    // layout QW (gpu_engine.cpp:120-141): quants [rows, in], scales [rows, in/32].
+    void or_dequant_q8_0(const int8_t *qs, const uint16_t *d, double *out, int64_t rows, int64_t in,
+                         int dt_out)
+    {
+        const int64_t nb = in / 32;
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < rows; ++r)
+            for (int64_t i = 0; i < in; ++i)
+                out[r * in + i] = rnd(dt_out, double(qs[r * in + i]) * f16_value(d[r * nb + i / 32]));
+    }
+
+    // up_w (gpu_engine.cpp:2722-2755) — llama.cpp's quantize_row_q8_0_ref
+    // semantics as the reference states them: per 32, amax over the bf16 values in
+    // f32, d = amax/127, id = d ? 1/d : 0, scale = f16(d) (RNE, subnormals kept,
+    // gpu_engine.cpp:152-158), q = lround(x*id) (f32 product).
+    void or_quantize_q8_0(const uint16_t *w, int8_t *qs, uint16_t *d, int64_t rows, int64_t in)
+    {
+        const int64_t nb = in / 32;
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < rows; ++r)
+            for (int64_t b = 0; b < nb; ++b) {
+                const uint16_t *row = w + r * in + b * 32;
+                float amax = 0.f;
+                for (int i = 0; i < 32; ++i) amax = std::max(amax, std::fabs(float(bf16_value(row[i]))));
+                const float dd = amax / 127.f;
+                const float id = dd != 0.f ? 1.f / dd : 0.f;
+                d[r * nb + b] = f16_bits(double(dd));
+                for (int i = 0; i < 32; ++i)
+                    qs[r * in + b * 32 + i] = int8_t(std::lround(float(bf16_value(row[i])) * id));
+            }
+    }
+
+    // ------------------------------------------------------------------ vocab
+    // Per row of logits [rows, V]:
+    //   lse     serve/sampler.py:168-171 — m = max of finite entries,
+    //           m + log(sum exp(x - m)) over finite entries (here in f64, FDLIBM,
+    //           ascending); -inf when the row has no finite entry
+    //   argmax  src/main.cpp:475-483 — strict '>' scan from index 0 (first max wins)
+    //   top-K   src/main.cpp:604-615 (partial_sort, a > b) with the tie order made
+    //           total: value descending, then index ascending
+    void or_vocab_reduce(const double *L, int64_t rows, int64_t V, int64_t K, double *lse,
+                         int64_t *amax, int64_t *top_idx, double *top_val)
+    {
+#pragma omp parallel
+        {
+            std::vector<int64_t> idx(static_cast<size_t>(V));
+#pragma omp for schedule(static)
+            for (int64_t r = 0; r < rows; ++r) {
+                const double *p = L + r * V;
+                double m = -HUGE_VAL;
+                bool any = false;
+                for (int64_t v = 0; v < V; ++v)
+                    if (std::isfinite(p[v])) { m = any ? std::max(m, p[v]) : p[v]; any = true; }
+                if (any) {
+                    double s = 0;
+                    for (int64_t v = 0; v < V; ++v)
+                        if (std::isfinite(p[v])) s += orc::exp(p[v] - m);
+                    lse[r] = m + orc::log(s);
+                } else {
+                    lse[r] = -HUGE_VAL;
+                }
+                int64_t best = 0;
+                for (int64_t v = 1; v < V; ++v)
+                    if (p[v] > p[best]) best = v;
+                amax[r] = best;
+                if (K > 0) {
+                    std::iota(idx.begin(), idx.end(), int64_t(0));
+                    const int64_t k = std::min(K, V);
+                    std::partial_sort(idx.begin(), idx.begin() + k, idx.end(),
+                                      [&](int64_t a, int64_t b) { return p[a] > p[b] || (p[a] == p[b] && a < b); });
+                    for (int64_t i = 0; i < k; ++i) {
+                        top_idx[r * K + i] = idx[size_t(i)];
+                        top_val[r * K + i] = p[idx[size_t(i)]];
+                    }
+                }
+            }
+        }
+    }
+
+    int or_num_threads(void)
+    {
+#ifdef _OPENMP
+        return omp_get_max_threads();
+#else
+        return 1;
+#endif
+    }
+} // extern "C"

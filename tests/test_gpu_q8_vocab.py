@@ -1,0 +1,157 @@
+"""GPU parity: Q8_0 dequantize and the vocab logsumexp / argmax / top-K pass.
+
+Q8_0: k_dequant_q8 (src/gpu/gpu_engine.cpp:1117-1171) with the QW layout
+(120-141); bitwise (int8 x f16 is exact in f32, one rounding), including
+subnormal f16 scales (145-151).
+Vocab: serve/sampler.py:168-171 (lse), src/main.cpp:475-483 (argmax),
+src/main.cpp:604-615 (top-K, ties by lower index). lse within 1e-6 relative
+of the f64 oracle; argmax and top-K indices identical.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from util import BF16, F16, F32, from_dev, same_bits, storage, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def q8_case(rows, n_in, seed=9, lo=1e-3, hi=2e-2):
+    qs = O.int8_uniform(seed, (rows, n_in))
+    d = O.uniform(seed + 1, (rows, n_in // 32), lo, hi, F16)
+    return qs, d
+
+
+@pytest.mark.parametrize("dt_out", (BF16, F16, F32))
+def test_dequant_bitwise(prims, dt_out):
+    import torch
+    qs, d = q8_case(300, 5120)
+    dq = torch.from_numpy(qs).to("cuda:0")
+    dd = torch.from_numpy(d.view(np.int16)).to("cuda:0")
+    out = to_dev(np.zeros(qs.shape, np.float32 if dt_out == F32 else np.uint16), dt_out)
+    prims.dequant_q8_0(dq, dd, out)
+    ref = O.dequant_q8_0(qs, d, dt_out)
+    assert same_bits(from_dev(out, dt_out), O.from_f64(ref, dt_out))
+
+
+def test_dequant_subnormal_and_special_scales(prims):
+    import torch
+    rows, n_in = 64, 2048
+    qs = O.int8_uniform(3, (rows, n_in), -128, 127)
+    # every f16 subnormal and a spread of normals, zero and the largest scale
+    d = np.concatenate([np.arange(1, 1024, dtype=np.uint16), np.array([0, 0x7bff, 0x3c00], np.uint16)])
+    d = np.resize(d, (rows, n_in // 32)).astype(np.uint16)
+    out = to_dev(np.zeros(qs.shape, np.uint16), BF16)
+    prims.dequant_q8_0(torch.from_numpy(qs).to("cuda:0"), torch.from_numpy(d.view(np.int16)).to("cuda:0"), out)
+    ref = O.dequant_q8_0(qs, d, BF16)
+    assert same_bits(from_dev(out, BF16), O.from_f64(ref, BF16))
+    # exactness argument, checked directly: q*d in f64 equals the f32 product
+    qf = qs.astype(np.float32) * np.repeat(O.to_f64(d, F16).astype(np.float32), 32, axis=1)
+    assert np.array_equal(qf.astype(np.float64), qs.astype(np.float64) * np.repeat(O.to_f64(d, F16), 32, axis=1))
+
+
+def test_dequant_config5_full(prims):
+    """Config 5 at full size: [25600 x 5120] int8 ~ U[-127,127], f16 scales ~ U[1e-3, 2e-2]."""
+    import torch
+    qs, d = q8_case(25600, 5120)
+    out = to_dev(np.zeros(qs.shape, np.uint16), BF16)
+    prims.dequant_q8_0(torch.from_numpy(qs).to("cuda:0"), torch.from_numpy(d.view(np.int16)).to("cuda:0"), out)
+    ref = O.dequant_q8_0(qs, d, BF16)
+    assert same_bits(from_dev(out, BF16), O.from_f64(ref, BF16))
+
+
+def test_dequant_errors(prims):
+    import mgprims
+    import torch
+    q = torch.zeros((2, 48), dtype=torch.int8, device="cuda:0")
+    d = torch.zeros((2, 2), dtype=torch.float16, device="cuda:0")
+    out = torch.zeros((2, 48), dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(mgprims.MgError, match="multiple of 32"):
+        prims.dequant_q8_0(q, d, out)
+
+
+# ---------------------------------------------------------------------- vocab
+def vocab_check(prims, L_store, dt, K):
+    L = O.to_f64(L_store, dt)
+    dL = to_dev(L_store, dt)
+    lse, am, ti, tv = prims.vocab_reduce(dL, K)
+    r_lse, r_am, r_ti, r_tv = O.vocab_reduce(L, K)
+    lse = lse.cpu().numpy()
+    fin = np.isfinite(r_lse)
+    assert np.array_equal(np.isfinite(lse), fin)
+    if fin.any():
+        rel = np.abs(lse[fin] - r_lse[fin]) / np.abs(r_lse[fin])
+        assert rel.max() <= 1e-6, rel.max()
+    assert np.array_equal(am.cpu().numpy(), r_am)
+    assert np.array_equal(ti.cpu().numpy(), r_ti)
+    tvv = tv.cpu().numpy().astype(np.float64)
+    assert np.array_equal(tvv[~np.isnan(r_tv)], r_tv[~np.isnan(r_tv)])
+    return lse, am, ti
+
+
+def test_vocab_config5_full(prims):
+    """Config 5: logits f32 [64, 201088] ~ N(0, 4), lse + argmax + top-64."""
+    Ls = O.normal(11, (64, 201088), 0.0, 4.0, F32)
+    vocab_check(prims, Ls, F32, 64)
+
+
+@pytest.mark.parametrize("K", (1, 5, 20, 64, 256))
+def test_vocab_k(prims, K):
+    Ls = O.normal(12, (7, 50000), 0.0, 4.0, F32)
+    vocab_check(prims, Ls, F32, K)
+
+
+def test_vocab_ties(prims):
+    """coarsely quantized logits: many equal values, ties broken by lower index"""
+    L = np.round(O.to_f64(O.normal(13, (16, 202048), 0.0, 2.0, F32), F32) * 2) / 2
+    vocab_check(prims, O.from_f64(L, F32), F32, 64)
+
+
+def test_vocab_all_equal(prims):
+    """every logit equal: ties resolve to indices 0..K-1 (lower index first)"""
+    L = np.zeros((3, 30000))
+    _, am, ti = vocab_check(prims, O.from_f64(L, F32), F32, 64)
+    assert np.array_equal(ti.cpu().numpy(), np.tile(np.arange(64), (3, 1)))
+
+
+def test_vocab_masked_entries(prims):
+    L = O.to_f64(O.normal(14, (4, 20000), 0.0, 4.0, F32), F32)
+    L[0, ::3] = -np.inf
+    L[1, :] = -np.inf          # no finite entry: lse -inf, argmax 0
+    L[2, 100:] = -np.inf
+    vocab_check(prims, O.from_f64(L, F32), F32, 64)
+
+
+def test_vocab_bf16_and_small_V(prims):
+    vocab_check(prims, O.normal(15, (5, 202048), 0.0, 4.0, BF16), BF16, 64)
+    vocab_check(prims, O.normal(16, (9, 64), 0.0, 4.0, F32), F32, 64)
+    vocab_check(prims, O.normal(17, (2, 8193), 0.0, 4.0, F32), F32, 64)
+
+
+def test_vocab_nan_at_zero(prims):
+    L = O.to_f64(O.normal(18, (2, 1000), 0.0, 4.0, F32), F32)
+    L[0, 0] = np.nan
+    L[1, 5] = np.nan
+    lse, am, ti, tv = prims.vocab_reduce(to_dev(O.from_f64(L, F32), F32), 8)
+    _, r_am, _, _ = O.vocab_reduce(L, 8)
+    assert np.array_equal(am.cpu().numpy(), r_am) and r_am[0] == 0
+
+
+def test_vocab_chunk_fallback_bisection(prims):
+    """K = 256 with every element of the top threads above the threshold: more
+    than 2048 candidates in a chunk, so pass 1 bisects for the exact K-th key"""
+    V = 8192 * 2
+    j = np.arange(V)
+    L = -(j % 256) * 1000.0 - (j // 256)
+    vocab_check(prims, O.from_f64(np.tile(L, (2, 1)), F32), F32, 256)
+
+
+def test_vocab_merge_fallback_bisection(prims):
+    """25 chunks whose top-256 interleave: more than 2048 row candidates above
+    the merge threshold, so pass 2 bisects"""
+    V = 201088
+    L = np.full(V, -1e6)
+    for c in range((V + 8191) // 8192):
+        m = np.arange(256)
+        L[c * 8192 + m] = 1000.0 - c - 25.0 * m
+    vocab_check(prims, O.from_f64(L[None, :], F32), F32, 256)

@@ -1,0 +1,129 @@
+"""GPU parity: scaled, masked row softmax.
+
+Reference: the softmax of attention_forward (src/muse_glimmer.hpp:828-885) as a
+row operator (oracle/oracle.cpp or_softmax_rows); softcap in apply_output_tail's
+op order (920-943). Gates: bf16 probabilities within 1 ulp of the twin (f64
+internals, one rounding); f32 probabilities within 1e-6 relative of the f64
+oracle; masked probabilities exactly 0.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from util import BF16, F16, F32, from_dev, same_bits, storage, to_dev, ulp_diff16
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 1.0 / math.sqrt(128.0)
+
+
+def run(prims, heads, q, kc, dt_in=F32, dt_out=BF16, mask=O.MASK_CAUSAL, window=0, q_pos0=0,
+        softcap=0.0, seed=8, std=3.0):
+    xs, x = storage(seed, (heads, q, kc), dt_in, 0.0, std)
+    dx = to_dev(xs, dt_in)
+    dy = to_dev(np.zeros((heads, q, kc), np.float32 if dt_out == F32 else np.uint16), dt_out)
+    prims.softmax_rows(dx, dy, SCALE, mask, window, q_pos0, softcap)
+    y = from_dev(dy, dt_out)
+    ref = O.softmax_rows(x, SCALE, mask, window, q_pos0, softcap, dt_in, O.F64)
+    return y, ref
+
+
+def visible(heads, q, kc, mask, window, q_pos0):
+    qpos = q_pos0 + np.arange(q)[:, None]
+    j = np.arange(kc)[None, :]
+    v = np.ones((q, kc), bool)
+    if mask >= 1:
+        v &= j <= qpos
+    if mask == 2:
+        v &= j > qpos - window
+    return np.broadcast_to(v, (heads, q, kc))
+
+
+def check(y, ref, dt_out, vis, max_frac=2e-3):
+    assert np.all(O.to_f64(y, dt_out)[~vis] == 0.0), "masked probability not exactly 0"
+    if dt_out == F32:
+        yv = y.astype(np.float64)[vis]
+        rv = ref[vis]
+        rel = np.abs(yv - rv) / rv
+        assert rel.max() <= 1e-6, rel.max()
+        return 0
+    d = ulp_diff16(y, O.from_f64(ref, dt_out))
+    assert d.max() <= 1, d.max()
+    frac = (d > 0).mean()
+    assert frac <= max_frac, frac
+    return int((d > 0).sum())
+
+
+@pytest.mark.parametrize("dt_out", (BF16, F32, F16))
+@pytest.mark.parametrize("mask", (O.MASK_NONE, O.MASK_CAUSAL))
+def test_prefill_rows(prims, dt_out, mask):
+    y, ref = run(prims, 8, 256, 256, dt_out=dt_out, mask=mask)
+    check(y, ref, dt_out, visible(8, 256, 256, mask, 0, 0))
+
+
+@pytest.mark.parametrize("kc", (2048, 1024, 512, 100, 8, 1))
+def test_row_lengths(prims, kc):
+    y, ref = run(prims, 3, 40, kc, q_pos0=kc - 40 if kc > 40 else 0)
+    check(y, ref, BF16, visible(3, 40, kc, O.MASK_CAUSAL, 0, kc - 40 if kc > 40 else 0))
+
+
+@pytest.mark.parametrize("dt_out", (BF16, F32))
+def test_softcap(prims, dt_out):
+    y, ref = run(prims, 4, 128, 1024, dt_out=dt_out, softcap=30.0, std=60.0)
+    check(y, ref, dt_out, visible(4, 128, 1024, O.MASK_CAUSAL, 0, 0))
+
+
+def test_window_mask(prims):
+    y, ref = run(prims, 4, 64, 512, mask=O.MASK_WINDOW, window=100, q_pos0=300)
+    check(y, ref, BF16, visible(4, 64, 512, O.MASK_WINDOW, 100, 300))
+
+
+@pytest.mark.parametrize("dt_in", (BF16, F16))
+def test_16bit_scores(prims, dt_in):
+    y, ref = run(prims, 4, 64, 2048, dt_in=dt_in, q_pos0=1984)
+    check(y, ref, BF16, visible(4, 64, 2048, O.MASK_CAUSAL, 0, 1984))
+
+
+@pytest.mark.parametrize("dt_out", (BF16, F32))
+def test_decode_split_rows(prims, dt_out):
+    """Config 4 decode: [40, 1, 131072], every key visible (split path)."""
+    y, ref = run(prims, 40, 1, 131072, dt_out=dt_out, q_pos0=131071)
+    check(y, ref, dt_out, visible(40, 1, 131072, O.MASK_CAUSAL, 0, 131071))
+
+
+def test_split_ragged_and_masked(prims):
+    """split rows with k % 8 != 0 and a causal cut inside the row"""
+    y, ref = run(prims, 3, 2, 9000 + 5, q_pos0=5000)
+    check(y, ref, BF16, visible(3, 2, 9005, O.MASK_CAUSAL, 0, 5000))
+    y, ref = run(prims, 2, 3, 20000, mask=O.MASK_WINDOW, window=7000, q_pos0=15000, dt_out=F32)
+    check(y, ref, F32, visible(2, 3, 20000, O.MASK_WINDOW, 7000, 15000))
+
+
+def test_all_masked_row_is_zero(prims):
+    """window rows with q_pos0 < 0 see no key at all: zeros, not NaN"""
+    y, ref = run(prims, 1, 4, 64, mask=O.MASK_WINDOW, window=2, q_pos0=-10)
+    assert np.all(O.to_f64(y, BF16) == 0.0)
+
+
+def test_config4_full(prims):
+    """Config 4 prefill at full size: f32 [40, 2048, 2048] ~ N(0, 3), causal, bf16 out."""
+    y, ref = run(prims, 40, 2048, 2048)
+    n = check(y, ref, BF16, visible(40, 2048, 2048, O.MASK_CAUSAL, 0, 0))
+    print(f"config4: {n} of {y.size} probabilities differ from the twin by 1 ulp")
+
+
+def test_rows_sum_to_one(prims):
+    y, _ = run(prims, 4, 64, 2048, dt_out=F32)
+    s = y.astype(np.float64).sum(-1)
+    assert np.abs(s - 1).max() < 1e-5
+
+
+def test_errors(prims):
+    import mgprims
+    import torch
+    x = torch.zeros((1, 1, 64), dtype=torch.float64, device="cuda:0")
+    y = torch.zeros((1, 1, 64), dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(mgprims.MgError, match="input dtype"):
+        prims.softmax_rows(x, y, 1.0)
