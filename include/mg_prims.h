@@ -46,8 +46,8 @@ enum mg_mask { MG_MASK_NONE = 0, MG_MASK_CAUSAL = 1, MG_MASK_WINDOW = 2 };
  * (muse_last_error, src/gpu/c_api.cpp:35, 170-188). */
 const char *mg_last_error(void);
 
-/* Create a context on HIP device `device`. `stream` is a hipStream_t to launch
- * on, or NULL for a new stream of default priority owned by the context.
+/* Create a context on HIP device `device`. `stream` is the hipStream_t every
+ * call launches on; NULL is the device's default (null) stream.
  * `workspace_bytes` sizes the reduction-partials buffer (0 = 64 MiB); calls
  * whose partials would not fit fail with an error instead of allocating.
  * (muse_open, src/gpu/c_api.cpp:88-168) */
@@ -55,7 +55,7 @@ int mg_open(int device, void *stream, int64_t workspace_bytes, mg_ctx **out);
 int mg_close(mg_ctx *ctx);
 /* Wait for all work queued on the context's stream. */
 int mg_sync(mg_ctx *ctx);
-/* Point the context at another stream (hipStream_t; NULL = its own). */
+/* Point the context at another stream (hipStream_t; NULL = the default stream). */
 int mg_set_stream(mg_ctx *ctx, void *stream);
 void *mg_get_stream(mg_ctx *ctx);
 

@@ -9,9 +9,10 @@
 //   masked keys (causal / window):   excluded, probability exactly 0
 //   p = exp(s - max) / sum           written once at the output dtype
 // The reference evaluates the exponentials and the sum in f64 (twin) or f32
-// (compat, 856-870); here they are f32 (an accurate exp, f32 sums reduced in a
-// fixed order), which keeps p within a few f32 ulp of the f64 value: the bf16
-// output is within 1 ulp of the twin's and the f32 output within 1e-6 relative.
+// (compat, 856-870); here the exponentials are f32 (an accurate exp of the
+// exactly formed s - max) summed in f64 in a fixed order, which keeps p within
+// a few f32 ulp of the f64 value: the bf16 output is within 1 ulp of the
+// twin's and the f32 output within 1e-6 relative.
 //
 // Rows of up to 2048 keys: one wave per row, the row in registers (8 keys per
 // lane per chunk), one read and one write of HBM. Longer rows (decode,
@@ -162,16 +163,16 @@ namespace mg
             for (int e = 0; e < 8; ++e) m = s[c][e] > m ? s[c][e] : m;
         }
         m = wave_max(m);
-        float sum = 0.0f;
+        double sum = 0.0; // f64: the row sum adds no error at the f32 output's scale
 #pragma unroll
         for (int c = 0; c < CH; ++c)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                s[c][e] = s[c][e] == kNegInf ? 0.0f : exp_f32(s[c][e] - m);
-                sum += s[c][e];
+                s[c][e] = s[c][e] == kNegInf ? 0.0f : exp_diff(s[c][e], m);
+                sum += double(s[c][e]);
             }
         sum = wave_sum(sum);
-        const float inv = m == kNegInf ? 0.0f : 1.0f / sum;
+        const float inv = m == kNegInf ? 0.0f : float(1.0 / sum);
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
 #pragma unroll
@@ -191,12 +192,12 @@ namespace mg
         __syncthreads();
         return t;
     }
-    MG_DEV float block_sum_f32(float v, float *red)
+    MG_DEV double block_sum_f64(double v, double *red)
     {
         v = wave_sum(v);
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
         __syncthreads();
-        float t = 0.0f;
+        double t = 0.0;
         for (int i = 0; i < int(blockDim.x >> 6); ++i) t += red[i];
         __syncthreads();
         return t;
@@ -208,6 +209,7 @@ namespace mg
                                                              bool vec, float2 *__restrict__ part)
     {
         __shared__ float red[4];
+        __shared__ double redd[4];
         const int64_t row = blockIdx.y;
         int64_t lo, hi;
         row_range(a, row, lo, hi);
@@ -222,14 +224,14 @@ namespace mg
             for (int e = 0; e < 8; ++e) m = s[c][e] > m ? s[c][e] : m;
         }
         m = block_max_f32(m, red);
-        float sum = 0.0f;
+        double sum = 0.0;
         if (m != kNegInf)
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) sum += s[c][e] == kNegInf ? 0.0f : exp_f32(s[c][e] - m);
-        sum = block_sum_f32(sum, red);
-        if (threadIdx.x == 0) part[row * gridDim.x + blockIdx.x] = make_float2(m, sum);
+                for (int e = 0; e < 8; ++e) sum += s[c][e] == kNegInf ? 0.0 : double(exp_diff(s[c][e], m));
+        sum = block_sum_f64(sum, redd);
+        if (threadIdx.x == 0) part[row * gridDim.x + blockIdx.x] = make_float2(m, float(sum));
     }
 
     // pass B: merge the row's partials in chunk order, then write this chunk
@@ -265,7 +267,7 @@ namespace mg
             float s[8];
             load_scores<SI>(a, xr, j0, lo, hi, vec, s);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s[e] = s[e] == kNegInf ? 0.0f : exp_f32(s[e] - M) * inv;
+            for (int e = 0; e < 8; ++e) s[e] = s[e] == kNegInf ? 0.0f : exp_diff(s[e], M) * inv;
             store_probs<SO>(a, yr, j0, vec, s);
         }
     }

@@ -17,8 +17,8 @@
 // below is deterministic however the work is split.
 //
 // Pass 1, one work-group per 8192-key chunk of a row (1600 groups at the
-// 64 x 201088 shape): the chunk's finite max and f32 sum of exp(x - max)
-// (reduced in f64 in a fixed order), its argmax, and its own top-K. The top-K
+// 64 x 201088 shape): the chunk's finite max and the f64 sum of f32 exp(x - max)
+// (in a fixed order), its argmax, and its own top-K. The top-K
 // uses a threshold that cannot miss: the K-th largest of the 256 per-thread
 // maximum keys bounds the chunk's K-th largest from below, so every key at
 // or above it is a candidate (about K + K/8 of them for random logits); the
@@ -201,12 +201,12 @@ namespace mg
         nfin = block_sum_i(nfin, redi);
         block_argmax(bv, bi, redf, redi);
 
-        float ls = 0.0f;
+        double ls = 0.0;
         if (nfin > 0)
 #pragma unroll
             for (int i = 0; i < kVEPT; ++i)
-                if (i < nv && __builtin_isfinite(v[i])) ls += exp_f32(v[i] - m);
-        const double l = block_sum_d(double(ls), redd);
+                if (i < nv && __builtin_isfinite(v[i])) ls += double(exp_diff(v[i], m));
+        const double l = block_sum_d(ls, redd);
 
         // threshold: K-th largest per-thread max key
         sk[tid] = kmax;

@@ -48,10 +48,9 @@ namespace
     {
         if (!c) return;
         hipSetDevice(c->device);
-        if (c->stream) hipStreamSynchronize(c->stream);
+        hipStreamSynchronize(c->stream);
         if (c->lut) hipFree(c->lut);
         if (c->work) hipFree(c->work);
-        if (c->own_stream) hipStreamDestroy(c->own_stream);
         delete c;
     }
 }
@@ -75,12 +74,7 @@ int mg_open(int device, void *stream, int64_t workspace_bytes, mg_ctx **out)
             hipDeviceProp_t prop;
             mg::check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
             c->num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
-            if (stream) {
-                c->stream = static_cast<hipStream_t>(stream);
-            } else {
-                mg::check(hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking), "hipStreamCreate");
-                c->stream = c->own_stream;
-            }
+            c->stream = static_cast<hipStream_t>(stream);
             c->work_bytes = workspace_bytes > 0 ? workspace_bytes : kDefaultWorkspace;
             mg::check(hipMalloc(&c->work, size_t(c->work_bytes)), "hipMalloc(workspace)");
             mg::check(hipMalloc(reinterpret_cast<void **>(&c->lut), 4 * 65536 * sizeof(uint16_t)), "hipMalloc(lut)");
@@ -114,9 +108,7 @@ int mg_sync(mg_ctx *ctx)
 int mg_set_stream(mg_ctx *ctx, void *stream)
 {
     MG_GUARD(-1, {
-        mg_ctx *c = ctx_of(ctx);
-        c->stream = stream ? static_cast<hipStream_t>(stream) : c->own_stream;
-        if (!c->stream) mg::fail("mg_set_stream: NULL stream and the context owns none");
+        ctx_of(ctx)->stream = static_cast<hipStream_t>(stream);
         return 0;
     });
 }

@@ -133,19 +133,31 @@ namespace mg
     }
 
     // ---------------------------------------------------------------- f32 exp
-    // e^x for the f32 reductions: Cody–Waite reduction x = n·ln2 + r with the
-    // Cephes two-constant split of ln2, then 2^(r·log2 e) on the hardware exp2
+    // e^(x + lo) for the f32 reductions, lo a small correction term (|lo| <=
+    // ulp(x)/2): Cody–Waite reduction x = n·ln2 + r with the Cephes
+    // two-constant split of ln2, r += lo, then 2^(r·log2 e) on the hardware exp2
     // (|r| <= ln2/2, so the f32 product adds < 2^-25 relative), scaled by 2^n.
     // Relative error ~1.5 ulp; underflows smoothly through subnormals to 0.
-    MG_DEV float exp_f32(float x)
+    MG_DEV float exp_f32(float x, float lo = 0.0f)
     {
         if (x < -104.0f) return 0.0f;
         x = x > 88.72f ? 88.72f : x;
         const float n = __builtin_rintf(x * 1.44269504088896341f);
         float r = __builtin_fmaf(-n, 0.693359375f, x);
-        r = __builtin_fmaf(n, 2.12194440e-4f, r);
+        r = __builtin_fmaf(n, 2.12194440e-4f, r) + lo;
         return __builtin_ldexpf(__builtin_amdgcn_exp2f(r * 1.44269504088896341f), int(n));
     }
+    // e^(s - m) with the subtraction made exact (Knuth's TwoSum: d + err = s - m
+    // exactly), so scores far from the row max lose nothing to the f32 rounding
+    // of s - m (up to 2^-19 absolute at |s| ~ 30, a softcapped score's range).
+    MG_DEV float exp_diff(float s, float m)
+    {
+        const float d = s - m;
+        const float bp = d - s;
+        const float err = (s - (d - bp)) + (-m - bp);
+        return exp_f32(d, err);
+    }
+
     // order-preserving map of an f32 to u32 (larger float -> larger key)
     MG_DEV uint32_t f32_key(float f)
     {

@@ -12,8 +12,7 @@
 struct mg_ctx
 {
     int device = 0;
-    hipStream_t stream = nullptr;     // where every call launches
-    hipStream_t own_stream = nullptr; // created by mg_open when the caller gave none
+    hipStream_t stream = nullptr; // where every call launches (NULL: the default stream)
     int num_cus = 256;
     // silu/sigmoid of every 16-bit input, as output bits:
     // [0] silu bf16, [1] sigmoid bf16, [2] silu f16, [3] sigmoid f16 (65536 each)

@@ -21,6 +21,32 @@ def all16(dt):
     return bits, O.to_f64(bits, dt)
 
 
+def mismatches(a, b, *cols, n=12):
+    """first differing positions with the values that produced them"""
+    idx = np.nonzero(a != b)[0][:n]
+    return [(int(i), int(a[i]), int(b[i]), *(float(c[i]) for c in cols)) for i in idx]
+
+
+@pytest.mark.parametrize("dt", (BF16, F16))
+@pytest.mark.parametrize("gate", (False, True))
+@pytest.mark.parametrize("unit", (1.0, -1.0))
+def test_table_contents(prims, dt, gate, unit):
+    """with the other operand = +-1 the output is +-rnd(f(g)) itself: every table
+    entry against the twin's rnd(silu(g)) / rnd(sigmoid(g))"""
+    gb, g = all16(dt)
+    one = np.full(65536, unit)
+    dg, d1 = to_dev(gb, dt), to_dev(O.from_f64(one, dt), dt)
+    dout = to_dev(np.zeros(65536, np.uint16), dt)
+    if gate:
+        prims.sigmoid_gate(d1, dg, dout)
+        ref = O.sigmoid_gate(one, g, dt)
+    else:
+        prims.swiglu(dg, d1, dout)
+        ref = O.swiglu(g, one, dt)
+    out, rb = from_dev(dout, dt), O.from_f64(ref, dt)
+    assert same_bits_or_nan(out, rb, dt), mismatches(out, rb, g)
+
+
 @pytest.mark.parametrize("dt", (BF16, F16))
 @pytest.mark.parametrize("gate", (False, True))
 def test_exhaustive_16bit_gate_inputs(prims, dt, gate):
@@ -35,7 +61,8 @@ def test_exhaustive_16bit_gate_inputs(prims, dt, gate):
     else:
         prims.swiglu(dg, du, dout)
         ref = O.swiglu(g, u, dt)
-    assert same_bits_or_nan(from_dev(dout, dt), O.from_f64(ref, dt), dt)
+    out, rb = from_dev(dout, dt), O.from_f64(ref, dt)
+    assert same_bits_or_nan(out, rb, dt), mismatches(out, rb, g, u)
 
 
 @pytest.mark.parametrize("dt", (BF16, F16, F32, F64))

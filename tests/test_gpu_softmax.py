@@ -47,7 +47,8 @@ def check(y, ref, dt_out, vis, max_frac=2e-3):
         yv = y.astype(np.float64)[vis]
         rv = ref[vis]
         rel = np.abs(yv - rv) / rv
-        assert rel.max() <= 1e-6, rel.max()
+        i = int(np.argmax(rel))
+        assert rel.max() <= 1e-6, (rel.max(), float(yv[i]), float(rv[i]), i)
         return 0
     d = ulp_diff16(y, O.from_f64(ref, dt_out))
     assert d.max() <= 1, d.max()
