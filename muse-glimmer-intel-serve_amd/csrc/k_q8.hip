@@ -20,12 +20,11 @@ namespace mg
     __global__ __launch_bounds__(256) void k_dequant_q8_0(const int8_t *__restrict__ qs,
                                                           const uint16_t *__restrict__ d,
                                                           typename SO::raw *__restrict__ out,
-                                                          int64_t ngroups, int64_t in)
+                                                          int64_t ngroups)
     {
         using raw = typename SO::raw;
         constexpr int U = 4;
         const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-        const int64_t gpr = in / 16; // 16-quant groups per row
         for (int64_t base = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; base < ngroups; base += stride * U) {
             Vec<int8_t, 16> q[U];
             float sc[U];
@@ -34,8 +33,9 @@ namespace mg
                 const int64_t g = base + k * stride;
                 if (g < ngroups) {
                     q[k] = ld16_stream<int8_t, 16>(qs + 16 * g);
-                    const int64_t r = g / gpr, gc = g - r * gpr;
-                    sc[k] = f16_f32(d[r * (in / 32) + gc / 2]);
+                    // `in` is a multiple of 32, so group g's 32-block is g / 2 in
+                    // the row-major [rows, in/32] scale array
+                    sc[k] = f16_f32(d[g >> 1]);
                 }
             }
 #pragma unroll
@@ -43,8 +43,14 @@ namespace mg
                 const int64_t g = base + k * stride;
                 if (g < ngroups) {
                     raw o[16];
+                    if (__builtin_isfinite(sc[k])) {
+                        // int8 x finite scale: finite products, no NaN to canonicalize
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) o[e] = SO::enc32(float(q[k].v[e]) * sc[k]);
+                        for (int e = 0; e < 16; ++e) o[e] = SO::enc_finite(float(q[k].v[e]) * sc[k]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) o[e] = SO::enc32(float(q[k].v[e]) * sc[k]);
+                    }
                     constexpr int V = 16 / sizeof(raw);
 #pragma unroll
                     for (int p = 0; p < 16 / V; ++p) {
@@ -69,9 +75,9 @@ namespace mg
         const int64_t ngroups = rows * (in / 16);
         const unsigned blocks = unsigned(std::min<int64_t>((ngroups + 1023) / 1024, int64_t(c->num_cus) * 32));
         switch (dt_out) {
-        case BF16: hipLaunchKernelGGL(k_dequant_q8_0<SBf16>, dim3(blocks), dim3(256), 0, c->stream, qs, d, static_cast<uint16_t *>(out), ngroups, in); break;
-        case F16: hipLaunchKernelGGL(k_dequant_q8_0<SF16>, dim3(blocks), dim3(256), 0, c->stream, qs, d, static_cast<uint16_t *>(out), ngroups, in); break;
-        case F32: hipLaunchKernelGGL(k_dequant_q8_0<SF32>, dim3(blocks), dim3(256), 0, c->stream, qs, d, static_cast<float *>(out), ngroups, in); break;
+        case BF16: hipLaunchKernelGGL(k_dequant_q8_0<SBf16>, dim3(blocks), dim3(256), 0, c->stream, qs, d, static_cast<uint16_t *>(out), ngroups); break;
+        case F16: hipLaunchKernelGGL(k_dequant_q8_0<SF16>, dim3(blocks), dim3(256), 0, c->stream, qs, d, static_cast<uint16_t *>(out), ngroups); break;
+        case F32: hipLaunchKernelGGL(k_dequant_q8_0<SF32>, dim3(blocks), dim3(256), 0, c->stream, qs, d, static_cast<float *>(out), ngroups); break;
         default: fail("dequant_q8_0: output dtype must be bf16, f16 or f32");
         }
         check_launch("k_dequant_q8_0");

@@ -51,11 +51,11 @@ namespace mg
     }
 
     // score transform: scale (and softcap) with the input dtype's materializations
-    template <class SI>
+    template <class SI, bool CAP>
     MG_DEV float score(const SmArgs &a, float x)
     {
         float s = SI::dec(SI::enc32(x * a.scale));
-        if (a.cap != 0.0f) {
+        if (CAP) {
             // the twin's FDLIBM tanh in f64, so the capped score is bit-identical
             s = SI::dec(SI::enc32(s / a.cap));
             s = SI::dec(SI::enc64(mgm::tanh(double(s))));
@@ -104,7 +104,7 @@ namespace mg
 
     // load the 8 keys j0..j0+7 of a row as transformed scores; masked or
     // out-of-row keys become -inf
-    template <class SI>
+    template <class SI, bool CAP>
     MG_DEV void load_scores(const SmArgs &a, const typename SI::raw *xr, int64_t j0, int64_t lo,
                             int64_t hi, bool vec, float *s)
     {
@@ -123,7 +123,7 @@ namespace mg
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int64_t j = j0 + e;
-            s[e] = (j >= lo && j <= hi) ? score<SI>(a, v[e]) : kNegInf;
+            s[e] = (j >= lo && j <= hi) ? score<SI, CAP>(a, v[e]) : kNegInf;
         }
     }
 
@@ -141,7 +141,7 @@ namespace mg
     }
 
     // --------------------------------------------------------- one wave per row
-    template <class SI, class SO, int CH>
+    template <class SI, class SO, int CH, bool CAP>
     __global__ __launch_bounds__(256) void k_softmax_wave(const typename SI::raw *__restrict__ x,
                                                           typename SO::raw *__restrict__ y, SmArgs a,
                                                           bool vec)
@@ -158,7 +158,7 @@ namespace mg
         float m = kNegInf;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            load_scores<SI>(a, xr, int64_t(lane + 64 * c) * 8, lo, hi, vec, s[c]);
+            load_scores<SI, CAP>(a, xr, int64_t(lane + 64 * c) * 8, lo, hi, vec, s[c]);
 #pragma unroll
             for (int e = 0; e < 8; ++e) m = s[c][e] > m ? s[c][e] : m;
         }
@@ -204,7 +204,7 @@ namespace mg
     }
 
     // pass A: partial (max, sum exp(s - max)) of chunk blockIdx.x of row blockIdx.y
-    template <class SI>
+    template <class SI, bool CAP>
     __global__ __launch_bounds__(256) void k_softmax_partial(const typename SI::raw *__restrict__ x, SmArgs a,
                                                              bool vec, float2 *__restrict__ part)
     {
@@ -219,7 +219,7 @@ namespace mg
         float m = kNegInf;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            load_scores<SI>(a, xr, base + int64_t(threadIdx.x + 256 * c) * 8, lo, hi, vec, s[c]);
+            load_scores<SI, CAP>(a, xr, base + int64_t(threadIdx.x + 256 * c) * 8, lo, hi, vec, s[c]);
 #pragma unroll
             for (int e = 0; e < 8; ++e) m = s[c][e] > m ? s[c][e] : m;
         }
@@ -234,28 +234,29 @@ namespace mg
         if (threadIdx.x == 0) part[row * gridDim.x + blockIdx.x] = make_float2(m, float(sum));
     }
 
-    // pass B: merge the row's partials in chunk order, then write this chunk
-    template <class SI, class SO>
+    // pass B: merge the row's partials, then write this chunk. Every work-group
+    // of the row forms the same merge: max over the chunk maxima, then
+    // sum_c l_c * exp(m_c - M) in f64 (FDLIBM exp), each thread over chunks
+    // t, t+256, ... in order and the threads in a fixed tree.
+    template <class SI, class SO, bool CAP>
     __global__ __launch_bounds__(256) void k_softmax_finish(const typename SI::raw *__restrict__ x,
                                                             typename SO::raw *__restrict__ y, SmArgs a,
                                                             bool vec, const float2 *__restrict__ part)
     {
-        __shared__ float mrg[2];
+        __shared__ float red[4];
+        __shared__ double redd[4];
         const int64_t row = blockIdx.y;
         const int nch = int(gridDim.x);
-        if (threadIdx.x == 0) {
-            const float2 *pr = part + row * nch;
-            float M = kNegInf;
-            for (int i = 0; i < nch; ++i) M = pr[i].x > M ? pr[i].x : M;
-            double L = 0.0;
-            if (M != kNegInf)
-                for (int i = 0; i < nch; ++i)
-                    if (pr[i].x != kNegInf) L += double(pr[i].y) * mgm::exp(double(pr[i].x) - double(M));
-            mrg[0] = M;
-            mrg[1] = M == kNegInf ? 0.0f : float(1.0 / L);
-        }
-        __syncthreads();
-        const float M = mrg[0], inv = mrg[1];
+        const float2 *pr = part + row * nch;
+        float M = kNegInf;
+        for (int i = threadIdx.x; i < nch; i += blockDim.x) M = pr[i].x > M ? pr[i].x : M;
+        M = block_max_f32(M, red);
+        double L = 0.0;
+        if (M != kNegInf)
+            for (int i = threadIdx.x; i < nch; i += blockDim.x)
+                if (pr[i].x != kNegInf) L += double(pr[i].y) * mgm::exp(double(pr[i].x) - double(M));
+        L = block_sum_f64(L, redd);
+        const float inv = M == kNegInf ? 0.0f : float(1.0 / L);
         int64_t lo, hi;
         row_range(a, row, lo, hi);
         const typename SI::raw *xr = x + row * a.kc;
@@ -265,14 +266,14 @@ namespace mg
         for (int c = 0; c < 2; ++c) {
             const int64_t j0 = base + int64_t(threadIdx.x + 256 * c) * 8;
             float s[8];
-            load_scores<SI>(a, xr, j0, lo, hi, vec, s);
+            load_scores<SI, CAP>(a, xr, j0, lo, hi, vec, s);
 #pragma unroll
             for (int e = 0; e < 8; ++e) s[e] = s[e] == kNegInf ? 0.0f : exp_diff(s[e], M) * inv;
             store_probs<SO>(a, yr, j0, vec, s);
         }
     }
 
-    template <class SI, class SO>
+    template <class SI, class SO, bool CAP>
     void launch_softmax_t(mg_ctx *c, const void *x, void *y, const SmArgs &a)
     {
         using ri = typename SI::raw;
@@ -284,11 +285,11 @@ namespace mg
             const unsigned blocks = unsigned((a.nrows + 3) / 4);
             need((a.nrows + 3) / 4 < (int64_t(1) << 31), "softmax: too many rows");
             if (a.kc <= 512)
-                hipLaunchKernelGGL((k_softmax_wave<SI, SO, 1>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, vec);
+                hipLaunchKernelGGL((k_softmax_wave<SI, SO, 1, CAP>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, vec);
             else if (a.kc <= 1024)
-                hipLaunchKernelGGL((k_softmax_wave<SI, SO, 2>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, vec);
+                hipLaunchKernelGGL((k_softmax_wave<SI, SO, 2, CAP>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, vec);
             else
-                hipLaunchKernelGGL((k_softmax_wave<SI, SO, 4>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, vec);
+                hipLaunchKernelGGL((k_softmax_wave<SI, SO, 4, CAP>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, vec);
             check_launch("k_softmax_wave");
             return;
         }
@@ -298,9 +299,9 @@ namespace mg
              "softmax: partials exceed the context workspace (raise workspace_bytes at mg_open)");
         float2 *part = static_cast<float2 *>(c->work);
         const dim3 grid{unsigned(nch), unsigned(a.nrows), 1u};
-        hipLaunchKernelGGL(k_softmax_partial<SI>, grid, dim3(256), 0, c->stream, xi, a, vec, part);
+        hipLaunchKernelGGL((k_softmax_partial<SI, CAP>), grid, dim3(256), 0, c->stream, xi, a, vec, part);
         check_launch("k_softmax_partial");
-        hipLaunchKernelGGL((k_softmax_finish<SI, SO>), grid, dim3(256), 0, c->stream, xi, yo, a, vec, part);
+        hipLaunchKernelGGL((k_softmax_finish<SI, SO, CAP>), grid, dim3(256), 0, c->stream, xi, yo, a, vec, part);
         check_launch("k_softmax_finish");
     }
 
@@ -308,9 +309,9 @@ namespace mg
     void launch_softmax_out(mg_ctx *c, const void *x, void *y, const SmArgs &a, int dt_out)
     {
         switch (dt_out) {
-        case BF16: launch_softmax_t<SI, SBf16>(c, x, y, a); break;
-        case F16: launch_softmax_t<SI, SF16>(c, x, y, a); break;
-        case F32: launch_softmax_t<SI, SF32>(c, x, y, a); break;
+        case BF16: a.cap != 0.0f ? launch_softmax_t<SI, SBf16, true>(c, x, y, a) : launch_softmax_t<SI, SBf16, false>(c, x, y, a); break;
+        case F16: a.cap != 0.0f ? launch_softmax_t<SI, SF16, true>(c, x, y, a) : launch_softmax_t<SI, SF16, false>(c, x, y, a); break;
+        case F32: a.cap != 0.0f ? launch_softmax_t<SI, SF32, true>(c, x, y, a) : launch_softmax_t<SI, SF32, false>(c, x, y, a); break;
         default: fail("softmax: output dtype must be bf16, f16 or f32");
         }
     }

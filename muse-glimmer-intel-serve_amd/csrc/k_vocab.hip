@@ -25,7 +25,7 @@
 // candidates are compacted to LDS and bitonic-sorted. If a pathological chunk
 // (mass ties) yields more than kCap candidates, a bisection over the key space
 // finds the exact K-th key first.
-// Pass 2, one work-group per row: merge the chunk partials in chunk order
+// Pass 2, one work-group per row: merge the chunk partials in a fixed order
 // (max, rescaled f64 sum, FDLIBM log), fold the argmaxes, and select the
 // row's top-K from the chunks' lists with the same threshold argument (the
 // largest chunk K-th key bounds the row's K-th key from below).
@@ -83,6 +83,21 @@ namespace mg
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
         __syncthreads();
         float t = red[0];
+        for (int i = 1; i < int(blockDim.x >> 6); ++i) t = red[i] > t ? red[i] : t;
+        __syncthreads();
+        return t;
+    }
+
+    MG_DEV uint64_t block_max_u64(uint64_t v, uint64_t *red)
+    {
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const uint64_t o = __shfl_xor(v, m, 64);
+            v = o > v ? o : v;
+        }
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        uint64_t t = red[0];
         for (int i = 1; i < int(blockDim.x >> 6); ++i) t = red[i] > t ? red[i] : t;
         __syncthreads();
         return t;
@@ -275,6 +290,9 @@ namespace mg
     {
         __shared__ uint64_t sk[kCap];
         __shared__ int redi[4];
+        __shared__ float redf[4];
+        __shared__ double redd[4];
+        __shared__ uint64_t redu[4];
         __shared__ unsigned slot;
         __shared__ uint64_t thr;
         const int64_t row = blockIdx.x;
@@ -282,40 +300,43 @@ namespace mg
         const VPart *pr = part + row * nch;
         const uint64_t *cr = cand + row * nch * int64_t(K);
 
-        if (tid == 0) {
-            // logsumexp merge in chunk order
-            float M = -__builtin_huge_valf();
-            bool any = false;
-            for (int c = 0; c < nch; ++c)
-                if (pr[c].nfin > 0) {
-                    M = any ? (pr[c].m > M ? pr[c].m : M) : pr[c].m;
-                    any = true;
-                }
-            if (lse) {
-                if (any) {
-                    double S = 0.0;
-                    for (int c = 0; c < nch; ++c)
-                        if (pr[c].nfin > 0) S += pr[c].l * mgm::exp(double(pr[c].m) - double(M));
-                    lse[row] = double(M) + mgm::log(S);
-                } else {
-                    lse[row] = -__builtin_huge_val();
-                }
+        // merge the chunk partials: every thread folds chunks tid, tid+256, ...
+        // (in order), then the threads fold in a fixed tree
+        float M = -__builtin_huge_valf();
+        int nfin = 0;
+        float bv = 0.0f;
+        int bi = -1;
+        uint64_t t = 0;
+        for (int c = tid; c < nch; c += kVT) {
+            const VPart p = pr[c];
+            if (p.nfin > 0) {
+                M = p.m > M ? p.m : M;
+                nfin += p.nfin;
             }
-            // argmax fold in chunk order; the scan starts at index 0
-            float bv = 0.0f;
-            int bi = -1;
-            for (int c = 0; c < nch; ++c)
-                if (beats(pr[c].bv, pr[c].bi, bv, bi)) {
-                    bv = pr[c].bv;
-                    bi = pr[c].bi;
-                }
-            const float x0 = float(SI::dec(L[row * V]));
-            if (x0 != x0 || bi < 0) bi = 0;
-            if (amax) amax[row] = bi;
+            if (beats(p.bv, p.bi, bv, bi)) {
+                bv = p.bv;
+                bi = p.bi;
+            }
             // lower bound on the row's K-th key: the largest full chunk's K-th key
-            uint64_t t = 0;
-            for (int c = 0; c < nch; ++c)
-                if (pr[c].ncand == K) t = cr[c * int64_t(K) + K - 1] > t ? cr[c * int64_t(K) + K - 1] : t;
+            if (p.ncand == K) {
+                const uint64_t kk = cr[c * int64_t(K) + K - 1];
+                t = kk > t ? kk : t;
+            }
+        }
+        M = block_max_f(M, redf);
+        nfin = block_sum_i(nfin, redi);
+        block_argmax(bv, bi, redf, redi);
+        t = block_max_u64(t, redu);
+        double S = 0.0;
+        if (nfin > 0)
+            for (int c = tid; c < nch; c += kVT)
+                if (pr[c].nfin > 0) S += pr[c].l * mgm::exp(double(pr[c].m) - double(M));
+        S = block_sum_d(S, redd);
+        if (tid == 0) {
+            if (lse) lse[row] = nfin > 0 ? double(M) + mgm::log(S) : -__builtin_huge_val();
+            // the scan starts at index 0: a NaN there is never beaten
+            const float x0 = float(SI::dec(L[row * V]));
+            if (amax) amax[row] = (x0 != x0 || bi < 0) ? 0 : bi;
             thr = t;
             slot = 0;
         }

@@ -28,6 +28,14 @@ namespace mg
         const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
         return f != f ? uint16_t((h & 0x8000u) | 0x7e00u) : h;
     }
+    // Opaque copy of an f32 value. Without it the backend may fold
+    // f16(f32(a) * f32(b)) into v_fma_mixlo_f16 a, b, +0, which turns a -0
+    // product into +0 (-0 + +0 = +0); the twin keeps the sign of zero.
+    MG_DEV float opaque(float f)
+    {
+        __asm__("" : "+v"(f));
+        return f;
+    }
     MG_DEV float bf16_f32(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
     MG_DEV float f16_f32(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 
@@ -41,9 +49,10 @@ namespace mg
         using comp = float;
         static constexpr int dt = BF16;
         static MG_DEV float dec(raw r) { return bf16_f32(r); }
-        static MG_DEV raw enc32(float f) { return bf16_bits(f); }
+        static MG_DEV raw enc32(float f) { return bf16_bits(opaque(f)); }
         static MG_DEV raw enc64(double d) { return bf16_bits(float(d)); }
-        static MG_DEV raw enc(comp c) { return bf16_bits(c); }
+        static MG_DEV raw enc(comp c) { return bf16_bits(opaque(c)); }
+        static MG_DEV raw enc_finite(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(opaque(f))); }
     };
     struct SF16
     {
@@ -51,9 +60,10 @@ namespace mg
         using comp = float;
         static constexpr int dt = F16;
         static MG_DEV float dec(raw r) { return f16_f32(r); }
-        static MG_DEV raw enc32(float f) { return f16_bits(f); }
+        static MG_DEV raw enc32(float f) { return f16_bits(opaque(f)); }
         static MG_DEV raw enc64(double d) { return f16_bits(float(d)); }
-        static MG_DEV raw enc(comp c) { return f16_bits(c); }
+        static MG_DEV raw enc(comp c) { return f16_bits(opaque(c)); }
+        static MG_DEV raw enc_finite(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(opaque(f))); }
     };
     struct SF32
     {
@@ -64,6 +74,7 @@ namespace mg
         static MG_DEV raw enc32(float f) { return f; }
         static MG_DEV raw enc64(double d) { return float(d); }
         static MG_DEV raw enc(comp c) { return c; }
+        static MG_DEV raw enc_finite(float f) { return f; }
     };
     struct SF64
     {

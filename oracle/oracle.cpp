@@ -305,9 +305,10 @@ extern "C"
     // muse_glimmer.hpp:803-807 — q = rnd(q * f32(qk_scale)) in lp, q * qk_scale in f64
     void or_scale(double *x, int64_t n, double s, int dt)
     {
-        const double sc = opmath(dt, s);
+        // scalars formed per element, not captured from outside the OpenMP
+        // region (see or_softmax_rows)
 #pragma omp parallel for schedule(static)
-        for (int64_t i = 0; i < n; ++i) x[i] = rnd(dt, x[i] * sc);
+        for (int64_t i = 0; i < n; ++i) x[i] = rnd(dt, x[i] * opmath(dt, s));
     }
 
     // ------------------------------------------------------------------- rope
@@ -374,9 +375,9 @@ extern "C"
     // muse_glimmer.hpp:920-943 — z*mult, z/cap, tanh, z*cap, each materialized in lp
     void or_softcap(double *z, int64_t n, double mult, double cap, int dt)
     {
-        const double m = opmath(dt, mult), c = opmath(dt, cap);
 #pragma omp parallel for schedule(static)
         for (int64_t i = 0; i < n; ++i) {
+            const double m = opmath(dt, mult), c = opmath(dt, cap); // see or_softmax_rows
             double v = z[i];
             if (m != 1.0) v = rnd(dt, v * m);
             if (c != 0.0) {
@@ -404,9 +405,12 @@ extern "C"
                          double scale, int mask, int64_t window, int64_t q_pos0, double softcap,
                          int dt_in, int dt_out)
     {
-        const double sc = opmath(dt_in, scale), cap = opmath(dt_in, softcap);
 #pragma omp parallel
         {
+            // The f32 opmath scalars are formed inside the parallel region: with a
+            // const local formed outside it, g++ 11 passed the unrounded arguments
+            // into the outlined body (caught by tests/test_oracle_math.py).
+            const double sc = opmath(dt_in, scale), cap = opmath(dt_in, softcap);
             std::vector<double> s(static_cast<size_t>(kc));
 #pragma omp for schedule(static) collapse(2)
             for (int64_t h = 0; h < heads; ++h)

@@ -73,7 +73,19 @@ def test_row_lengths(prims, kc):
 @pytest.mark.parametrize("dt_out", (BF16, F32))
 def test_softcap(prims, dt_out):
     y, ref = run(prims, 4, 128, 1024, dt_out=dt_out, softcap=30.0, std=60.0)
-    check(y, ref, dt_out, visible(4, 128, 1024, O.MASK_CAUSAL, 0, 0))
+    vis = visible(4, 128, 1024, O.MASK_CAUSAL, 0, 0)
+    if dt_out == F32:
+        # where a probability is off, how far off is the score it implies (in f32 ulps)?
+        xs, x = storage(8, (4, 128, 1024), F32, 0.0, 60.0)
+        s = O.softcap(O.rnd(x * np.float64(np.float32(SCALE)), F32), 1.0, 30.0, F32)
+        s = np.where(vis, s, -np.inf)
+        m = s.max(-1, keepdims=True)
+        S = np.where(vis, np.exp(s - m), 0).sum(-1, keepdims=True)
+        d_gpu = np.log(np.maximum(y.astype(np.float64), 1e-300) * S)
+        dev = np.where(vis, (d_gpu - (s - m)) / np.spacing(np.abs(s).astype(np.float32)).astype(np.float64), 0)
+        i = np.unravel_index(np.argmax(np.abs(dev)), dev.shape)
+        print("worst implied score deviation (f32 ulps):", float(dev[i]), "at", i, "s =", float(s[i]), "m =", float(m[i[0], i[1], 0]))
+    check(y, ref, dt_out, vis)
 
 
 def test_window_mask(prims):
