@@ -13,7 +13,10 @@
 // context holds it as a 65536-entry table built on the device at mg_open with
 // the same f64 code; the hot kernel stages the 128 KiB table in LDS (gfx950
 // has 160 KiB per CU) and gathers from it, turning ~45 f64 operations per
-// element into one LDS read. f32/f64 operands evaluate the f64 form per element.
+// element into one LDS read. (Evaluating silu in f32 and proving each rounding
+// unambiguous, with the table as a fallback, is exact too but measured about
+// 1.8x slower here: ALU-bound at ~30 instructions per element.) f32/f64
+// operands evaluate the f64 form per element.
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
 
@@ -180,13 +183,13 @@ namespace mg
         const int64_t stride = int64_t(gridDim.x) * blockDim.x;
         const int64_t t0 = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
         for (int64_t i = t0; i < nvec; i += stride) {
-            Vec<raw, V> a = ld16<raw, V>(h + V * i);
+            Vec<raw, V> a = ldv<raw, V>(h + V * i);
             Vec<raw, V> b;
-            if (OP == 0) b = ld16<raw, V>(x + V * i);
+            if (OP == 0) b = ldv<raw, V>(x + V * i);
 #pragma unroll
             for (int e = 0; e < V; ++e)
                 a.v[e] = OP == 0 ? S::enc(S::dec(a.v[e]) + S::dec(b.v[e])) : S::enc(S::dec(a.v[e]) * s);
-            st16<raw, V>(h + V * i, a);
+            stv<raw, V>(h + V * i, a);
         }
         for (int64_t i = nvec * V + t0; i < n; i += stride)
             h[i] = OP == 0 ? S::enc(S::dec(h[i]) + S::dec(x[i])) : S::enc(S::dec(h[i]) * s);

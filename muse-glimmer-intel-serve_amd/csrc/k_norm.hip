@@ -133,12 +133,12 @@ namespace mg
         for (int c = 0; c < CPT; ++c) {
             const int ch = threadIdx.x + c * blockDim.x;
             if (ch < nchunk) {
-                Vec<raw, VEC> a = *reinterpret_cast<const Vec<raw, VEC> *>(hr + ch * VEC);
+                Vec<raw, VEC> a = ldv<raw, VEC>(hr + ch * VEC);
                 if (xr) {
-                    const Vec<raw, VEC> b = *reinterpret_cast<const Vec<raw, VEC> *>(xr + ch * VEC);
+                    const Vec<raw, VEC> b = ldv<raw, VEC>(xr + ch * VEC);
 #pragma unroll
                     for (int e = 0; e < VEC; ++e) a.v[e] = S::enc(S::dec(a.v[e]) + S::dec(b.v[e]));
-                    *reinterpret_cast<Vec<raw, VEC> *>(hr + ch * VEC) = a;
+                    stv<raw, VEC>(hr + ch * VEC, a);
                 }
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) {
@@ -161,7 +161,7 @@ namespace mg
 #pragma unroll
                 for (int e = 0; e < VEC; ++e)
                     o.v[e] = S::enc64(norm_out(kind, double(v[c][e]), rs, kind != 2 ? double(S::dec(wv.v[e])) : 0.0));
-                *reinterpret_cast<Vec<raw, VEC> *>(yr + ch * VEC) = o;
+                stv<raw, VEC>(yr + ch * VEC, o);
             }
         }
     }

@@ -107,14 +107,14 @@ namespace mg
         if (p < 0 || p >= table_rows) return;
         raw *x = hh < qh ? q + t * ldq + int64_t(hh) * dim : k + t * ldk + int64_t(hh - qh) * dim;
         x += jv * VEC;
-        Vec<raw, VEC> lo = *reinterpret_cast<const Vec<raw, VEC> *>(x);
-        Vec<raw, VEC> hi = *reinterpret_cast<const Vec<raw, VEC> *>(x + half);
+        Vec<raw, VEC> lo = ldv<raw, VEC>(x);
+        Vec<raw, VEC> hi = ldv<raw, VEC>(x + half);
         const Vec<raw, VEC> c = *reinterpret_cast<const Vec<raw, VEC> *>(co + p * half + jv * VEC);
         const Vec<raw, VEC> s = *reinterpret_cast<const Vec<raw, VEC> *>(si + p * half + jv * VEC);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) rope_pair<S>(lo.v[e], hi.v[e], c.v[e], s.v[e]);
-        *reinterpret_cast<Vec<raw, VEC> *>(x) = lo;
-        *reinterpret_cast<Vec<raw, VEC> *>(x + half) = hi;
+        stv<raw, VEC>(x, lo);
+        stv<raw, VEC>(x + half, hi);
     }
 
     template <class S>

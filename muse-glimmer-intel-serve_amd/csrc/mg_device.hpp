@@ -124,6 +124,25 @@ namespace mg
         for (int i = 0; i < 4; ++i) __builtin_nontemporal_store(u.v[i], q + i);
     }
 
+    // N elements: one non-temporal 16-byte access when they fill 16 bytes,
+    // plain element accesses otherwise (unaligned fallbacks)
+    template <typename T, int N>
+    MG_DEV Vec<T, N> ldv(const T *p)
+    {
+        if constexpr (sizeof(T) * N == 16)
+            return ld16_stream<T, N>(p);
+        else
+            return *reinterpret_cast<const Vec<T, N> *>(p);
+    }
+    template <typename T, int N>
+    MG_DEV void stv(T *p, const Vec<T, N> &v)
+    {
+        if constexpr (sizeof(T) * N == 16)
+            st16_stream<T, N>(p, v);
+        else
+            *reinterpret_cast<Vec<T, N> *>(p) = v;
+    }
+
     // -------------------------------------------------------- wave64 reductions
     template <typename T>
     MG_DEV T wave_sum(T v)
