@@ -62,7 +62,7 @@ STEP_OPS = ("residual_rmsnorm", "swiglu", "softmax_causal")
 KERNEL_OF = {
     "residual_rmsnorm": "k_norm_tree",
     "swiglu": "k_gate_lut",
-    "softmax_causal": "k_softmax_wave",
+    "softmax_causal": "k_softmax_fast",
     "rope": "k_rope",
     "softmax_decode": "k_softmax_partial + k_softmax_finish",
     "dequant_q8_0": "k_dequant_q8_0",
@@ -77,7 +77,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--reps", type=int, default=20, help="launches per op for the per-op medians")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default=None, help="run only this op, --steps times (for profilers)")
+    ap.add_argument("--only", default=None,
+                    help="comma-separated ops to run --steps times each, with the cache flush before every "
+                         "launch (for profilers); 'copy' adds a plain 256 MiB device copy for counter calibration")
+    ap.add_argument("--cpu-seconds", type=float, default=5.0, help="CPU time per op in the CPU baseline")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "pmc_traffic.txt"),
                     help="measured HBM bytes per launch (kernel  fetch_bytes  write_bytes)")
     return ap.parse_args()
@@ -169,13 +172,14 @@ def read_traffic(path, kernel):
     return None
 
 
-def cpu_baseline():
+def cpu_baseline(seconds):
     """The reference's CPU tensor path (the oracle restatement, OpenMP over rows)
-    on a bounded sample of the step's three ops, in the same unit (GB/s)."""
+    on a bounded sample of the step's three ops, in the same unit (GB/s): each
+    op runs on its sample repeatedly for about `seconds`."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle as O
-    rows_n, rows_s, sm_h = 512, 256, 2
+    rows_n, rows_s, sm_h = 512, 512, 5
     sample = {
         "residual_rmsnorm": (rows_n, 4 * 2 * rows_n * D + 2 * D),
         "swiglu": (rows_s, 3 * 2 * rows_s * FFN),
@@ -196,13 +200,14 @@ def cpu_baseline():
     tot_b = tot_s = 0.0
     for name, fn in fns.items():
         fn()
-        reps = 3
+        reps = 0
         t0 = time.perf_counter()
-        for _ in range(reps):
+        while reps < 3 or time.perf_counter() - t0 < seconds:
             fn()
+            reps += 1
         dt = (time.perf_counter() - t0) / reps
         b = sample[name][1]
-        per[name] = {"us": round(dt * 1e6, 1), "GBps": round(b / dt / 1e9, 3)}
+        per[name] = {"us": round(dt * 1e6, 1), "GBps": round(b / dt / 1e9, 3), "reps": reps}
         tot_b += b
         tot_s += dt
     del np
@@ -212,7 +217,8 @@ def cpu_baseline():
         "cores": O.num_threads(),
         "kind": "port",
         "sample": (f"residual_rmsnorm bf16-twin [{rows_n},{D}], swiglu bf16-twin [{rows_s},{FFN}], "
-                   f"causal softmax f32->bf16 [{sm_h},{SM_Q},{SM_K}]; f64 arrays as src/muse_glimmer.hpp holds them; "
+                   f"causal softmax f32->bf16 [{sm_h},{SM_Q},{SM_K}] (1/8 of the step's rows each), repeated "
+                   f"~{seconds:g} s per op; f64 arrays as src/muse_glimmer.hpp holds them; "
                    f"OpenMP threads={O.num_threads()}, host nproc={os.cpu_count()}"),
         "ops": per,
     }
@@ -232,16 +238,25 @@ def main():
     ops = make_inputs(torch, P)
 
     if args.only:
-        fn = ops[args.only]
-        for _ in range(args.warmup):
-            fn()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            fn()
-        torch.cuda.synchronize()
-        us = (time.perf_counter() - t0) / args.steps * 1e6
-        print(json.dumps({"op": args.only, "us_per_op_wall": round(us, 2)}), flush=True)
+        flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0")
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        ops["copy"] = lambda: dst.copy_(src)
+        for name in args.only.split(","):
+            fn = ops[name]
+            for _ in range(args.warmup):
+                fn()
+            times = []
+            for _ in range(args.steps):
+                flush.zero_()
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record()
+                fn()
+                b.record()
+                b.synchronize()
+                times.append(a.elapsed_time(b) * 1e3)
+            print(json.dumps({"op": name, "us_median": round(statistics.median(times), 2)}), flush=True)
         return
 
     def step():
@@ -282,7 +297,7 @@ def main():
                 "peak": PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
                 "traffic": read_traffic(args.traffic, kern), "algorithmic_bytes": BYTES[dom]}
 
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     out = {
         "metric": METRIC,
         "value": round(value, 1),
