@@ -514,8 +514,14 @@ extern "C"
                 if (K > 0) {
                     std::iota(idx.begin(), idx.end(), int64_t(0));
                     const int64_t k = std::min(K, V);
+                    // value descending, ties by lower index, NaN below everything
+                    // (a strict weak order even with NaN present)
                     std::partial_sort(idx.begin(), idx.begin() + k, idx.end(),
-                                      [&](int64_t a, int64_t b) { return p[a] > p[b] || (p[a] == p[b] && a < b); });
+                                      [&](int64_t a, int64_t b) {
+                                          const bool na = std::isnan(p[a]), nb = std::isnan(p[b]);
+                                          if (na || nb) return na && nb ? a < b : nb;
+                                          return p[a] > p[b] || (p[a] == p[b] && a < b);
+                                      });
                     for (int64_t i = 0; i < k; ++i) {
                         top_idx[r * K + i] = idx[size_t(i)];
                         top_val[r * K + i] = p[idx[size_t(i)]];

@@ -155,3 +155,53 @@ def test_vocab_merge_fallback_bisection(prims):
         m = np.arange(256)
         L[c * 8192 + m] = 1000.0 - c - 25.0 * m
     vocab_check(prims, O.from_f64(L[None, :], F32), F32, 256)
+
+
+def special_rows():
+    L = O.to_f64(O.normal(19, (7, 30000), 0.0, 4.0, F32), F32)
+    L[0, 5::97] = np.nan                      # NaN inside chunks
+    L[1, [1234, 20000]] = np.inf              # +inf: lse over the finite rest
+    L[1, 7::50] = np.nan
+    L[2] = -np.abs(L[2])                      # the top entries are signed zeros
+    L[2, 3::11] = 0.0
+    L[2, 8::13] = -0.0
+    L[3, :] = np.nan                          # fewer than K non-NaN entries
+    L[3, 100::1000] = 1.5
+    L[4, :] = -np.inf                         # -inf and a single NaN
+    L[4, 29999] = np.nan
+    L[5, 0] = np.nan                          # NaN at index 0 wins the argmax
+    L[6, 2048 * 3:2048 * 3 + 300] = 7.0       # a tie block wider than K in one chunk
+    return L
+
+
+@pytest.mark.parametrize("K", (64, 100))
+def test_vocab_special_values(prims, K):
+    """NaN / +inf / -inf / signed zeros in chunks; K = 100 takes the exact
+    per-chunk selection everywhere"""
+    vocab_check(prims, O.from_f64(special_rows(), F32), F32, K)
+
+
+def test_vocab_special_values_bf16(prims):
+    vocab_check(prims, O.from_f64(special_rows(), BF16), BF16, 64)
+
+
+def test_vocab_merge_deep_chunk(prims):
+    """rows whose top-64 sit mostly in one or a few chunks: the first-8 merge
+    cannot prove its answer and selects over the full chunk lists"""
+    L = O.to_f64(O.normal(21, (3, 201088), 0.0, 1.0, F32), F32)
+    L[0, 5000:5064] = 50.0 + np.arange(64)    # all 64 in one chunk
+    for i, c in enumerate((3, 40, 77)):
+        L[1, c * 2048 + 10:c * 2048 + 32] = 40.0 - i - np.arange(22) / 32.0
+    vocab_check(prims, O.from_f64(L, F32), F32, 64)
+
+
+def test_vocab_large_V(prims):
+    """more chunks than the merge holds in registers (V = 300000)"""
+    vocab_check(prims, O.normal(20, (3, 300000), 0.0, 4.0, F32), F32, 64)
+    vocab_check(prims, O.normal(22, (2, 300000), 0.0, 4.0, F32), F32, 256)
+
+
+def test_vocab_short_tails(prims):
+    """last chunk holding 1, 63, 100 and 2047 entries"""
+    for V in (2048 * 3 + 1, 2048 + 63, 2048 * 5 + 100, 2048 * 2 + 2047):
+        vocab_check(prims, O.normal(23, (3, V), 0.0, 4.0, F32), F32, 64)

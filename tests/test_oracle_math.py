@@ -342,6 +342,33 @@ def test_vocab_vs_numpy():
         assert np.array_equal(ti[r], order) and np.array_equal(tv[r], L[r][order])
 
 
+def test_vocab_special_values():
+    """NaN ranks below -inf, -0 == +0 (ties by index), lse over finite entries,
+    argmax = first maximum of the non-NaN entries unless index 0 is NaN"""
+    from scipy.special import logsumexp
+    L = O.rnd(RNG.normal(0, 4, (5, 3000)), F32)
+    L[0, 5::97] = np.nan
+    L[1, [1234, 2000]] = np.inf
+    L[1, 7::50] = np.nan
+    L[2] = -np.abs(L[2])
+    L[2, 3::11] = 0.0
+    L[2, 8::13] = -0.0
+    L[3, :] = np.nan
+    L[3, 100::300] = 1.5
+    L[4, 0] = np.nan
+    lse, am, ti, tv = O.vocab_reduce(L, 64)
+    idx = np.arange(L.shape[1])
+    for r in range(5):
+        fin = np.isfinite(L[r])
+        if fin.any():
+            assert abs(lse[r] - logsumexp(L[r][fin])) <= 1e-13 * abs(lse[r])
+        nan = np.isnan(L[r])
+        assert am[r] == (0 if nan[0] else int(np.nanargmax(L[r])))
+        order = np.lexsort((idx, -np.where(nan, 0.0, L[r]), nan))[:64]
+        assert np.array_equal(ti[r], order)
+        assert np.array_equal(np.isnan(tv[r]), nan[order])
+
+
 def test_vocab_all_masked_row():
     L = np.full((1, 100), -np.inf)
     lse, am, ti, tv = O.vocab_reduce(L, 4)
