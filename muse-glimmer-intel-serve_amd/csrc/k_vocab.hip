@@ -18,20 +18,22 @@
 // selection below is deterministic however the work is split.
 //
 // Pass 1 (k_vocab_chunk): one wave per 2048-key chunk, 32 keys per lane held
-// in registers, no block barriers. Per chunk: the finite max, the sum of
-// exp(x - max) (f32 terms and lane sums, f64 across lanes), the first index of
-// the max, and the chunk's top-K keys sorted descending. The top-K (K <= 64)
-// uses a bound that cannot miss: every lane keeps its two largest values, and
-// the K-th largest of those 128 values has at least K elements at or above it,
-// so all top-K elements are candidates; for random logits about K + K/8 pass.
-// They are compacted through a ballot into LDS and bitonic-sorted in registers.
-// A chunk whose bound is -inf or lets more than 128 candidates through, and
-// every chunk when K > 64, selects the exact K-th key by bisection instead.
+// in registers, no block barriers and no shuffles in the per-element work:
+// counts are ballot popcounts, reductions are DPP. Per chunk: the finite max,
+// the sum of exp(x - max) (f32 terms and lane sums, f64 across lanes), the
+// first index of the max, a candidate list that contains the chunk's top-K,
+// and the chunk's top-8 keys (the "block"). For K <= 64 the list is every
+// element at or above a bound that cannot miss: each lane keeps its two
+// largest values, and the K-th largest of those 128 values has at least K
+// elements at or above it (about K + K/8 pass for random logits). When that
+// bound is -inf or lets more than 128 through, and for every chunk when
+// K > 64, the list is the exact top-K, selected by bit-by-bit bisection on the
+// keys.
 // Pass 2 (k_vocab_merge): one wave per row. lse and argmax fold the chunk
-// partials (f64, FDLIBM exp/log). The row's top-K is selected from the first
-// 8 keys of every chunk list; that is the exact answer when every list's 9th
-// key (the first one left out) is below the selected K-th key, since deeper
-// keys are smaller still. Otherwise the selection runs over the full lists.
+// partials (f64, FDLIBM exp/log). The row's K-th key is first selected from
+// the blocks alone; that is exact when every chunk whose list runs past its
+// block has its 8th key at or below the selected one (everything deeper is
+// smaller still). Otherwise the selection runs over the full lists.
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
 
@@ -41,17 +43,18 @@ namespace mg
     constexpr int kVChunk = 64 * kVLane; // 2048 keys per wave-chunk
     constexpr int kMaxK = 256;
     constexpr int kFastK = 64;           // pass 1 bound-based selection up to this K
-    constexpr int kDepth = 8;            // pass 2: keys taken from each chunk list first
-    constexpr int kMergeRegs = 16;       // pass 2: candidate keys per lane (1024 per row)
+    constexpr int kBlk = 8;              // keys per chunk block
+    constexpr int kMergeRegs = 16;       // pass 2: block keys per lane (1024 per row)
 
     struct VPart
     {
-        double l;    // sum over the chunk's finite x of exp(x - m)
-        float m;     // max of the chunk's finite x
-        float bv;    // argmax value
-        int32_t bi;  // argmax index (-1: the chunk holds only NaN)
-        int32_t fin; // 1 if the chunk holds a finite entry
-        int32_t nk;  // keys in the chunk's list: min(valid entries, K)
+        double l;      // sum over the chunk's finite x of exp(x - m)
+        uint64_t kd;   // the block's smallest key if keys outside the block can
+                       // reach the row's top-K, else 0
+        uint64_t top;  // the chunk's largest key: its argmax (first maximum, NaN lowest)
+        float m;       // max of the chunk's finite x
+        int32_t fin;   // 1 if the chunk holds a finite entry
+        int32_t nlist; // keys in the chunk's candidate list
         int32_t pad;
     };
 
@@ -68,48 +71,6 @@ namespace mg
     MG_DEV uint32_t vkey_index(uint64_t k)
     {
         return 0xffffffffu - uint32_t(k);
-    }
-
-    // (value, index) argmax rule of the '>' scan: a beats b
-    MG_DEV bool beats(float av, int ai, float bv, int bi)
-    {
-        if (ai < 0) return false;
-        if (bi < 0) return true;
-        return av > bv || (av == bv && ai < bi);
-    }
-
-    MG_DEV int wave_sum_i(int v)
-    {
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-        return v;
-    }
-    MG_DEV int wave_min_i(int v)
-    {
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const int o = __shfl_xor(v, m, 64);
-            v = o < v ? o : v;
-        }
-        return v;
-    }
-    MG_DEV uint32_t wave_max_u32(uint32_t v)
-    {
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const uint32_t o = __shfl_xor(v, m, 64);
-            v = o > v ? o : v;
-        }
-        return v;
-    }
-    MG_DEV uint32_t wave_min_u32(uint32_t v)
-    {
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const uint32_t o = __shfl_xor(v, m, 64);
-            v = o < v ? o : v;
-        }
-        return v;
     }
 
     // Descending bitonic sort of the 64*SL values a wave holds SL per lane
@@ -173,13 +134,108 @@ namespace mg
         return VW * lane + 64 * VW * (s / VW) + (s % VW);
     }
 
+    // Radix selection on 32-bit words held R per lane (0 = absent): the K-th
+    // largest present word, and how many of the words equal to it belong to
+    // the K largest (`take`). Bits shared by every present word are skipped;
+    // the rest are resolved 8 at a time from the top with a 256-bin LDS
+    // histogram (`hist`, this wave's own) and a DPP prefix sum over the lanes'
+    // bins, so a 32-bit word costs at most 4 passes.
+    template <int R>
+    MG_DEV uint32_t wave_select(const uint32_t (&h)[R], int K, uint32_t *hist, int &take)
+    {
+        const int lane = threadIdx.x & 63;
+        uint32_t hmin = 0xffffffffu, hmax = 0;
+#pragma unroll
+        for (int q = 0; q < R; ++q)
+            if (h[q]) {
+                hmin = h[q] < hmin ? h[q] : hmin;
+                hmax = h[q] > hmax ? h[q] : hmax;
+            }
+        hmin = dpp_min_u32(hmin);
+        hmax = dpp_max_u32(hmax);
+        const uint32_t d = hmin ^ hmax;
+        int nb = d ? 32 - __builtin_clz(d) : 0; // open bits: nb-1 .. 0
+        uint32_t prefix = nb == 32 ? 0u : (hmax & ~((1u << nb) - 1u));
+        int need = K;
+        while (nb > 0) {
+            const int w = nb < 8 ? nb : 8, sh = nb - w;
+            const uint32_t fixed = nb == 32 ? 0u : ~((1u << nb) - 1u);
+            wave_lds_sync();
+            *reinterpret_cast<Vec<uint32_t, 4> *>(hist + 4 * lane) = Vec<uint32_t, 4>{{0u, 0u, 0u, 0u}};
+            wave_lds_sync();
+#pragma unroll
+            for (int q = 0; q < R; ++q)
+                if (h[q] && (h[q] & fixed) == prefix) atomicAdd(hist + ((h[q] >> sh) & ((1u << w) - 1u)), 1u);
+            wave_lds_sync();
+            const Vec<uint32_t, 4> c = *reinterpret_cast<const Vec<uint32_t, 4> *>(hist + 4 * lane);
+            const int sl = int(c.v[0] + c.v[1] + c.v[2] + c.v[3]);
+            const int incl = wave_prefix_sum(sl);
+            const int above_lane = __builtin_amdgcn_readlane(incl, 63) - incl; // in higher bins
+            const bool mine = above_lane < need && need <= above_lane + sl;
+            int dg = 0, above = 0;
+            if (mine) {
+                int acc = above_lane;
+                for (int e = 3; e >= 0; --e) {
+                    if (acc + int(c.v[e]) >= need) {
+                        dg = 4 * lane + e;
+                        above = acc;
+                        break;
+                    }
+                    acc += int(c.v[e]);
+                }
+            }
+            const int src = int(__builtin_ctzll(__builtin_amdgcn_ballot_w64(mine)));
+            dg = __builtin_amdgcn_readlane(dg, src);
+            above = __builtin_amdgcn_readlane(above, src);
+            prefix |= uint32_t(dg) << sh;
+            need -= above;
+            nb = sh;
+        }
+        take = need;
+        return prefix;
+    }
+
+    // K-th largest of the nonzero keys a wave holds R per lane (at least K of
+    // them): the high word by radix selection, then, when more keys share it
+    // than remain to take, the low word by bit-by-bit bisection among them.
+    template <int R>
+    MG_DEV uint64_t wave_kth(const uint64_t (&r)[R], int K, uint32_t *hist)
+    {
+        uint32_t h[R];
+#pragma unroll
+        for (int q = 0; q < R; ++q) h[q] = uint32_t(r[q] >> 32); // keys have high word >= 1
+        int need = 0;
+        const uint32_t th = wave_select<R>(h, K, hist, need);
+        int eq = 0;
+        uint32_t lmin = 0xffffffffu;
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+            const bool e = h[q] == th;
+            eq += wave_count(e);
+            lmin = (e && uint32_t(r[q]) < lmin) ? uint32_t(r[q]) : lmin;
+        }
+        if (eq == need) return (uint64_t(th) << 32) | dpp_min_u32(lmin);
+        uint32_t lw = 0;
+        for (int b = 31; b >= 0; --b) {
+            const uint32_t t = lw | (1u << b);
+            int c = 0;
+#pragma unroll
+            for (int q = 0; q < R; ++q) c += wave_count(h[q] == th && uint32_t(r[q]) >= t);
+            if (c >= need) lw = t;
+        }
+        return (uint64_t(th) << 32) | lw;
+    }
+
     template <class SI, int VW, int SL>
     __global__ __launch_bounds__(256) void k_vocab_chunk(const typename SI::raw *__restrict__ L, int64_t V, int K,
                                                          int nch, VPart *__restrict__ part,
-                                                         uint64_t *__restrict__ cand)
+                                                         uint64_t *__restrict__ blk, uint64_t *__restrict__ lst)
     {
         using raw = typename SI::raw;
-        __shared__ uint64_t slots[4][64 * SL];
+        constexpr int CAP = 64 * SL; // list capacity
+        __shared__ uint32_t sbits[4][CAP];
+        __shared__ uint32_t soff[4][CAP];
+        __shared__ __align__(16) uint32_t shist[4][256];
         const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
         const int ch = int(blockIdx.x) * 4 + wv;
         const int64_t row = blockIdx.y;
@@ -189,7 +245,10 @@ namespace mg
         const bool full = nvalid == kVChunk;
         const raw *xr = L + row * V + cb;
 
-        float x[kVLane];
+        // the chunk as f32 bit patterns; the exact selection overwrites them
+        // with the keys' high words
+        uint32_t xb[kVLane];
+        auto x = [&](int s) { return __builtin_bit_cast(float, xb[s]); };
         bool loaded = false;
         if constexpr (VW > 1) {
             if (full) {
@@ -197,7 +256,7 @@ namespace mg
                 for (int i = 0; i < kVLane / VW; ++i) {
                     const Vec<raw, VW> v = ld16_stream<raw, VW>(xr + VW * lane + 64 * VW * i);
 #pragma unroll
-                    for (int e = 0; e < VW; ++e) x[VW * i + e] = float(SI::dec(v.v[e]));
+                    for (int e = 0; e < VW; ++e) xb[VW * i + e] = __builtin_bit_cast(uint32_t, float(SI::dec(v.v[e])));
                 }
                 loaded = true;
             }
@@ -205,261 +264,238 @@ namespace mg
         if (!loaded) {
             // tail chunk (or unaligned rows): -inf placeholders past V never
             // reach a sum, a max or the candidates, and are kept out of the
-            // argmax and the exact selection by index
+            // argmax and the exact selection by offset
 #pragma unroll
             for (int s = 0; s < kVLane; ++s) {
                 const int o = voff<VW>(lane, s);
-                x[s] = o < nvalid ? float(SI::dec(xr[o])) : -__builtin_huge_valf();
+                xb[s] = __builtin_bit_cast(uint32_t, o < nvalid ? float(SI::dec(xr[o])) : -__builtin_huge_valf());
             }
         }
 
-        // lane maximum and second maximum (two distinct elements), NaN/+inf flag
+        // lane maximum and second maximum (two distinct elements)
         float m1 = -__builtin_huge_valf(), m2 = -__builtin_huge_valf();
-        bool sp = false;
 #pragma unroll
         for (int s = 0; s < kVLane; ++s) {
-            sp |= !(x[s] < __builtin_huge_valf());
-            m2 = __builtin_fmaxf(m2, __builtin_fminf(m1, x[s]));
-            m1 = __builtin_fmaxf(m1, x[s]);
+            m2 = __builtin_fmaxf(m2, __builtin_fminf(m1, x(s)));
+            m1 = __builtin_fmaxf(m1, x(s));
         }
-        const bool special = __builtin_amdgcn_ballot_w64(sp) != 0;
+        const float MX = dpp_max(m1); // max over the non-NaN entries
+
+        // lse partial, first assuming every entry finite or -inf
+        constexpr float c = 1.44269504088896341f;
+        float FM = MX;
+        double l = 0.0;
+        bool special = !(MX < __builtin_huge_valf()) || !(MX > -__builtin_huge_valf());
+        if (!special) {
+            // 2^(x*c - rnd(MX*c)) with one fma; the rounding of MX*c, shared by
+            // every term, is divided out exactly below
+            const float FMc = MX * c;
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < kVLane; ++s) acc[s & 3] += __builtin_amdgcn_exp2f(__builtin_fmaf(x(s), c, -FMc));
+            const double S = dpp_sum(double((acc[0] + acc[1]) + (acc[2] + acc[3])));
+            const double dl = (double(FMc) - double(MX) * double(c)) * 0.69314718055994531;
+            l = S * (1.0 + dl + 0.5 * dl * dl);
+            special = S != S; // a NaN logit
+        }
         if (special) {
-            // NaN would pass through fminf as the other operand: redo with NaN
-            // as -inf (it is never a candidate element)
+            // NaN or +inf present, or no finite entry: the finite max, the sum
+            // over finite entries, and m1/m2 with NaN taken as -inf (fminf
+            // would otherwise pass NaN's partner through as a second element)
+            float fm = -__builtin_huge_valf();
+#pragma unroll
+            for (int s = 0; s < kVLane; ++s)
+                if (__builtin_isfinite(x(s))) fm = __builtin_fmaxf(fm, x(s));
+            FM = dpp_max(fm);
+            float acc = 0.0f;
+            if (FM > -__builtin_huge_valf())
+#pragma unroll
+                for (int s = 0; s < kVLane; ++s)
+                    acc += __builtin_isfinite(x(s)) ? __builtin_amdgcn_exp2f((x(s) - FM) * c) : 0.0f;
+            l = dpp_sum(double(acc));
             m1 = m2 = -__builtin_huge_valf();
 #pragma unroll
             for (int s = 0; s < kVLane; ++s) {
-                const float v = x[s] == x[s] ? x[s] : -__builtin_huge_valf();
+                const float v = x(s) == x(s) ? x(s) : -__builtin_huge_valf();
                 m2 = __builtin_fmaxf(m2, __builtin_fminf(m1, v));
                 m1 = __builtin_fmaxf(m1, v);
             }
         }
-        const float MX = wave_max(m1); // max over non-NaN entries (+inf included)
-
-        // argmax: the first index holding MX
-        int first = 0x7fffffff;
-#pragma unroll
-        for (int s = kVLane - 1; s >= 0; --s)
-            if (x[s] == MX) first = voff<VW>(lane, s);
-        first = wave_min_i(first);
-        const int bi = first < nvalid ? int(cb) + first : -1;
-
-        // lse partial over the finite entries
-        float FM = MX;
-        if (special) {
-            float fm = -__builtin_huge_valf();
-#pragma unroll
-            for (int s = 0; s < kVLane; ++s)
-                if (__builtin_isfinite(x[s])) fm = __builtin_fmaxf(fm, x[s]);
-            FM = wave_max(fm);
-        }
         const bool fin = FM > -__builtin_huge_valf();
-        float ls = 0.0f;
-        if (fin) {
-            constexpr float c = 1.44269504088896341f;
-            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (!special) {
-#pragma unroll
-                for (int s = 0; s < kVLane; ++s) acc[s & 3] += __builtin_amdgcn_exp2f((x[s] - FM) * c); // -inf -> 0
-            } else {
-#pragma unroll
-                for (int s = 0; s < kVLane; ++s)
-                    acc[s & 3] += __builtin_isfinite(x[s]) ? __builtin_amdgcn_exp2f((x[s] - FM) * c) : 0.0f;
-            }
-            ls = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-        }
-        const double l = wave_sum(double(ls));
 
-        // ---- the chunk's top-K keys
-        // hk = 0 past V: every count below looks at hk >= 1 only
-        uint32_t hk[kVLane];
-        if (full) {
-#pragma unroll
-            for (int s = 0; s < kVLane; ++s) hk[s] = vhi(x[s]);
-        } else {
-#pragma unroll
-            for (int s = 0; s < kVLane; ++s) hk[s] = voff<VW>(lane, s) < nvalid ? vhi(x[s]) : 0u;
-        }
+        // ---- candidates
         const int nk = nvalid < K ? nvalid : K;
-        bool exact = SL * 64 > 128 || K > kFastK;
-        uint32_t tk = 0;
+        bool exact = SL > 2;
+        float tau = -__builtin_huge_valf();
         if (!exact) {
-            float t[2] = {m1, m2};
-            wave_sort_desc<float, 2>(t);
-            const float tau = __shfl(t[(K - 1) & 1], (K - 1) >> 1, 64);
-            int cnt = 0;
-            tk = vhi(tau);
-#pragma unroll
-            for (int s = 0; s < kVLane; ++s) cnt += hk[s] >= tk ? 1 : 0;
-            exact = !(tau > -__builtin_huge_valf()) || wave_sum_i(cnt) > 64 * SL;
+            // tau: the K-th largest of the 128 lane top-2 values
+            const uint32_t k2[2] = {f32_key(m1 + 0.0f), f32_key(m2 + 0.0f)}; // >= key(-inf) > 0
+            int unused = 0;
+            tau = key_f32(wave_select<2>(k2, K, shist[wv], unused));
+            exact = !(tau > -__builtin_huge_valf());
         }
-        // candidates: hk > th, or hk == th with chunk offset <= to
-        uint32_t th = tk;
+        // exact: candidates are hk > th, or hk == th at offsets <= to
+        uint32_t th = 0;
         int to = kVChunk;
-        if (exact) {
-            // th: the largest h with at least nk entries at or above it (>= 1,
-            // since every valid entry has hk >= 1)
-            th = 0;
-            for (int b = 31; b >= 0; --b) {
-                const uint32_t t = th | (1u << b);
-                int c = 0;
+        auto select_exact = [&]() {
+            // the keys' high words replace the values (0 past V)
 #pragma unroll
-                for (int s = 0; s < kVLane; ++s) c += hk[s] >= t ? 1 : 0;
-                if (wave_sum_i(c) >= nk) th = t;
-            }
-            int gt = 0;
-#pragma unroll
-            for (int s = 0; s < kVLane; ++s) gt += hk[s] > th ? 1 : 0;
-            const int need = nk - wave_sum_i(gt); // >= 1 entries with hk == th, lowest offsets first
-            // to: the smallest offset with `need` tied entries at or below it
+            for (int s = 0; s < kVLane; ++s) xb[s] = (full || voff<VW>(lane, s) < nvalid) ? vhi(x(s)) : 0u;
+            int need = 0; // entries with hk == th to take, lowest offsets first
+            th = wave_select<kVLane>(xb, nk, shist[wv], need);
             int lo = -1, hi = kVChunk - 1;
             while (hi - lo > 1) {
                 const int mid = (lo + hi) / 2;
-                int c = 0;
+                int cnt = 0;
 #pragma unroll
-                for (int s = 0; s < kVLane; ++s) {
-                    c += (hk[s] == th && voff<VW>(lane, s) <= mid) ? 1 : 0;
-                }
-                if (wave_sum_i(c) >= need)
+                for (int s = 0; s < kVLane; ++s) cnt += wave_count(xb[s] == th && voff<VW>(lane, s) <= mid);
+                if (cnt >= need)
                     hi = mid;
                 else
                     lo = mid;
             }
             to = hi;
-        }
+        };
+        if (exact) select_exact();
 
-        // compact the candidates into this wave's LDS slots
-        uint64_t *sl = slots[wv];
+        // compact (bits, offset) of the candidates into this wave's LDS slots;
+        // more than CAP of them (possible only through ties at tau) sends
+        // the chunk to the exact selection
+        uint32_t *sb = sbits[wv], *so = soff[wv];
         int n = 0;
+        for (int pass = 0; pass < 2; ++pass) {
+            n = 0;
 #pragma unroll
-        for (int s = 0; s < kVLane; ++s) {
-            const int o = voff<VW>(lane, s);
-            const bool take = hk[s] > th || (hk[s] == th && o <= to);
-            const uint64_t mask = __builtin_amdgcn_ballot_w64(take);
-            if (mask) {
-                if (take) sl[n + lane_rank(mask)] = vkey(hk[s], uint32_t(cb + o));
-                n += __builtin_popcountll(mask);
+            for (int s = 0; s < kVLane; ++s) {
+                const int o = voff<VW>(lane, s);
+                const uint32_t bits = xb[s];
+                const bool take = exact ? (bits > th || (bits == th && o <= to)) : x(s) >= tau;
+                const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
+                if (mk) {
+                    const int p = n + lane_rank(mk);
+                    if (take && p < CAP) {
+                        sb[p] = bits;
+                        so[p] = uint32_t(o);
+                    }
+                    n += __builtin_popcountll(mk);
+                }
             }
+            if (n <= CAP) break;
+            // exact selection (the keys replace the values), then compact again
+            exact = true;
+            select_exact();
         }
         wave_lds_sync();
         uint64_t a[SL];
 #pragma unroll
         for (int q = 0; q < SL; ++q) {
             const int i = SL * lane + q;
-            a[q] = i < n ? sl[i] : 0;
+            a[q] = 0;
+            if (i < n) {
+                const uint32_t bits = sb[i];
+                a[q] = vkey(exact ? bits : vhi(__builtin_bit_cast(float, bits)), uint32_t(cb + so[i]));
+            }
         }
-        wave_sort_desc<uint64_t, SL>(a);
-        uint64_t *cr = cand + (row * nch + ch) * int64_t(K);
+        // the largest key is the chunk's argmax under the scan's rule
+        uint64_t top = a[0];
+#pragma unroll
+        for (int q = 1; q < SL; ++q) top = a[q] > top ? a[q] : top;
+        top = dpp_reduce(top, uint64_t(0), [](uint64_t u, uint64_t v) { return u > v ? u : v; });
+        const int64_t cid = row * nch + ch;
+        uint64_t *lr = lst + cid * CAP;
+#pragma unroll
+        for (int q = 0; q < SL; ++q)
+            if (SL * lane + q < n) lr[SL * lane + q] = a[q];
+
+        // the block: the list's (= the chunk's) top D keys, D = min(8, K)
+        const int D = K < kBlk ? K : kBlk;
+        const uint64_t kd = n > D ? wave_kth<SL>(a, D, shist[wv]) : 0;
+        uint64_t *br = blk + cid * kBlk;
+        int nb = 0;
 #pragma unroll
         for (int q = 0; q < SL; ++q) {
-            const int i = SL * lane + q;
-            if (i < K) cr[i] = i < nk ? a[q] : 0;
+            const bool take = a[q] != 0 && a[q] >= kd;
+            const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
+            if (take && nb + lane_rank(mk) < kBlk) br[nb + lane_rank(mk)] = a[q];
+            nb += __builtin_popcountll(mk);
         }
+        if (lane >= nb && lane < kBlk) br[lane] = 0;
         if (lane == 0) {
             VPart p;
             p.l = l;
+            p.kd = (D < K && n > D) ? kd : 0;
             p.m = fin ? FM : 0.0f;
-            p.bv = MX;
-            p.bi = bi;
+            p.top = top;
             p.fin = fin ? 1 : 0;
-            p.nk = nk;
+            p.nlist = n;
             p.pad = 0;
-            part[row * nch + ch] = p;
+            part[cid] = p;
         }
     }
 
     // ------------------------------------------------------------------ pass 2
-    // K-th largest of the nonzero keys a wave holds R per lane (at least K
-    // exist). Every search below builds its answer bit by bit from the top, a
-    // fixed number of steps.
-    template <int R>
-    MG_DEV uint64_t wave_kth_key(const uint64_t (&r)[R], int K)
+    // K-th largest key over every chunk's candidate list, read from memory
+    MG_DEV uint64_t lists_kth(const VPart *pr, const uint64_t *ls, int nch, int cap, int K)
     {
-        uint32_t hmin = 0xffffffffu, hmax = 0;
-#pragma unroll
-        for (int q = 0; q < R; ++q)
-            if (r[q]) {
-                const uint32_t h = uint32_t(r[q] >> 32);
-                hmin = h < hmin ? h : hmin;
-                hmax = h > hmax ? h : hmax;
-            }
-        hmin = wave_min_u32(hmin);
-        hmax = wave_max_u32(hmax);
-        // th: the largest h with count(hi >= h) >= K; it lies in [hmin, hmax],
-        // whose members share the bits above the highest bit where they differ
-        const uint32_t d = hmin ^ hmax;
-        const int nb = d ? 32 - __builtin_clz(d) : 0;
-        uint32_t th = nb == 32 ? 0u : (hmax & ~((1u << nb) - 1u));
-        for (int b = nb - 1; b >= 0; --b) {
-            const uint32_t t = th | (1u << b);
+        const int lane = threadIdx.x & 63;
+        auto count = [&](auto pred) {
             int c = 0;
-#pragma unroll
-            for (int q = 0; q < R; ++q) c += (r[q] && uint32_t(r[q] >> 32) >= t) ? 1 : 0;
-            if (wave_sum_i(c) >= K) th = t;
-        }
-        int gt = 0, eq = 0;
-        uint64_t emin = ~uint64_t(0);
-#pragma unroll
-        for (int q = 0; q < R; ++q)
-            if (r[q]) {
-                const uint32_t h = uint32_t(r[q] >> 32);
-                gt += h > th ? 1 : 0;
-                if (h == th) {
-                    ++eq;
-                    emin = r[q] < emin ? r[q] : emin;
+            for (int ch = 0; ch < nch; ++ch) {
+                const int nl = pr[ch].nlist < cap ? pr[ch].nlist : cap;
+                for (int p0 = 0; p0 < nl; p0 += 64) {
+                    const int p = p0 + lane;
+                    const uint64_t k = p < nl ? ls[int64_t(ch) * cap + p] : 0;
+                    c += wave_count(k != 0 && pred(k));
                 }
             }
-        const int need = K - wave_sum_i(gt); // 1 <= need <= keys with hi == th
-        if (wave_sum_i(eq) == need) {
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) {
-                const uint64_t o = __shfl_xor(emin, m, 64);
-                emin = o < emin ? o : emin;
-            }
-            return emin;
+            return c;
+        };
+        uint32_t th = 0;
+        for (int b = 31; b >= 0; --b) {
+            const uint32_t t = th | (1u << b);
+            if (count([&](uint64_t k) { return uint32_t(k >> 32) >= t; }) >= K) th = t;
         }
-        // ties on the value: the need-th largest low word among them
+        const int need = K - count([&](uint64_t k) { return uint32_t(k >> 32) > th; });
         uint32_t lw = 0;
         for (int b = 31; b >= 0; --b) {
             const uint32_t t = lw | (1u << b);
-            int c = 0;
-#pragma unroll
-            for (int q = 0; q < R; ++q) c += (r[q] && uint32_t(r[q] >> 32) == th && uint32_t(r[q]) >= t) ? 1 : 0;
-            if (wave_sum_i(c) >= need) lw = t;
+            if (count([&](uint64_t k) { return uint32_t(k >> 32) == th && uint32_t(k) >= t; }) >= need) lw = t;
         }
         return (uint64_t(th) << 32) | lw;
     }
 
-    // the same over every key of the row's full chunk lists, read from memory
-    MG_DEV uint64_t wave_kth_key_mem(const uint64_t *cr, int64_t n, int K)
-    {
-        const int lane = threadIdx.x & 63;
-        uint64_t k = 0;
-        for (int b = 63; b >= 0; --b) {
-            const uint64_t t = k | (uint64_t(1) << b);
-            int c = 0;
-            for (int64_t i = lane; i < n; i += 64) c += cr[i] >= t ? 1 : 0;
-            if (wave_sum_i(c) >= K) k = t;
-        }
-        return k;
-    }
-
     template <class SI, int SL>
     __global__ __launch_bounds__(64) void k_vocab_merge(const typename SI::raw *__restrict__ L, int64_t V, int K,
-                                                        int nch, const VPart *__restrict__ part,
-                                                        const uint64_t *__restrict__ cand, double *lse,
+                                                        int nch, int cap, const VPart *__restrict__ part,
+                                                        const uint64_t *__restrict__ blk,
+                                                        const uint64_t *__restrict__ lst, double *lse,
                                                         int64_t *amax, int64_t *top_idx, float *top_val)
     {
-        __shared__ uint64_t sl[64 * SL];
+        __shared__ uint64_t sel[64 * SL];
+        __shared__ __align__(16) uint32_t hist[256];
         const int lane = threadIdx.x;
         const int64_t row = blockIdx.x;
         const VPart *pr = part + row * nch;
-        const uint64_t *cr = cand + row * nch * int64_t(K);
+        const uint64_t *bk = blk + row * nch * int64_t(kBlk);
+        const uint64_t *ls = lst + row * nch * int64_t(cap);
+        const float x0 = float(SI::dec(L[row * V]));
+        const bool want_top = top_idx || top_val;
+        const int D = K < kBlk ? K : kBlk;
+        const bool regs = want_top && nch * D <= 64 * kMergeRegs;
 
-        // lse and argmax: fold the chunk partials (lane-strided, then a
-        // butterfly whose result every lane shares)
-        float M = -__builtin_huge_valf(), bv = 0.0f;
-        int bi = -1;
+        // the blocks' keys, loaded first so their latency overlaps the fold
+        uint64_t r[kMergeRegs];
+#pragma unroll
+        for (int q = 0; q < kMergeRegs; ++q) {
+            const int i = lane + 64 * q;
+            const int c = D == kBlk ? i / kBlk : i / D, p = D == kBlk ? i % kBlk : i - c * D;
+            r[q] = regs && c < nch ? bk[int64_t(c) * kBlk + p] : 0;
+        }
+
+        // lse and argmax: fold the chunk partials; the largest chunk key is
+        // the row's first maximum
+        float M = -__builtin_huge_valf();
+        uint64_t ak = 0;
         bool any = false;
         for (int c = lane; c < nch; c += 64) {
             const VPart p = pr[c];
@@ -467,92 +503,79 @@ namespace mg
                 M = p.m > M ? p.m : M;
                 any = true;
             }
-            if (beats(p.bv, p.bi, bv, bi)) {
-                bv = p.bv;
-                bi = p.bi;
-            }
+            ak = p.top > ak ? p.top : ak;
         }
-        M = wave_max(M);
+        M = dpp_max(M);
+        ak = dpp_reduce(ak, uint64_t(0), [](uint64_t u, uint64_t v) { return u > v ? u : v; });
         any = __builtin_amdgcn_ballot_w64(any) != 0;
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float ov = __shfl_xor(bv, m, 64);
-            const int oi = __shfl_xor(bi, m, 64);
-            if (beats(ov, oi, bv, bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
+        // sum of l_c * e^(m_c - M): the f32 difference and hardware exp2 keep
+        // each term within a few ulp of f32, far inside the lse tolerance
         double S = 0.0;
         if (any)
             for (int c = lane; c < nch; c += 64) {
                 const VPart p = pr[c];
-                if (p.fin) S += p.l * mgm::exp(double(p.m) - double(M));
+                if (p.fin) S += p.l * double(__builtin_amdgcn_exp2f((p.m - M) * 1.44269504088896341f));
             }
-        S = wave_sum(S);
+        S = dpp_sum(S);
         if (lane == 0) {
             if (lse) lse[row] = any ? double(M) + mgm::log(S) : -__builtin_huge_val();
             // the scan starts at index 0: a NaN there is never beaten
-            const float x0 = float(SI::dec(L[row * V]));
-            if (amax) amax[row] = (x0 != x0 || bi < 0) ? 0 : bi;
+            if (amax) amax[row] = (x0 != x0 || ak == 0) ? 0 : int64_t(vkey_index(ak));
         }
-        if (!top_idx && !top_val) return;
+        if (!want_top) return;
 
-        // first try: the top kDepth keys of every chunk list
-        uint64_t kap = 0;
+        // first try: the blocks alone
         bool done = false;
-        if (nch * kDepth <= 64 * kMergeRegs) {
-            uint64_t r[kMergeRegs];
+        if (regs) {
             int have = 0;
 #pragma unroll
-            for (int q = 0; q < kMergeRegs; ++q) {
-                const int i = lane + 64 * q, c = i / kDepth, p = i % kDepth;
-                r[q] = (c < nch && p < K) ? cr[int64_t(c) * K + p] : 0;
-                have += r[q] ? 1 : 0;
-            }
-            if (wave_sum_i(have) >= K) {
-                kap = wave_kth_key<kMergeRegs>(r, K);
-                // every list's first key left out must fall below kap
-                bool ok = true;
-                if (K > kDepth)
-                    for (int c = lane; c < nch; c += 64) ok &= cr[int64_t(c) * K + kDepth] < kap;
-                done = __builtin_amdgcn_ballot_w64(!ok) == 0;
+            for (int q = 0; q < kMergeRegs; ++q) have += wave_count(r[q] != 0);
+            if (have >= K) {
+                const uint64_t kap = wave_kth<kMergeRegs>(r, K, hist);
+                bool bad = false;
+                for (int c = lane; c < nch; c += 64) {
+                    const uint64_t kd = pr[c].kd;
+                    bad |= kd != 0 && kd > kap;
+                }
+                done = __builtin_amdgcn_ballot_w64(bad) == 0;
                 if (done) {
                     int n = 0;
 #pragma unroll
                     for (int q = 0; q < kMergeRegs; ++q) {
-                        const bool take = r[q] >= kap && r[q] != 0;
-                        const uint64_t mask = __builtin_amdgcn_ballot_w64(take);
-                        if (mask) {
-                            if (take) sl[n + lane_rank(mask)] = r[q];
-                            n += __builtin_popcountll(mask);
+                        const bool take = r[q] != 0 && r[q] >= kap;
+                        const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
+                        if (mk) {
+                            if (take && n + lane_rank(mk) < 64 * SL) sel[n + lane_rank(mk)] = r[q];
+                            n += __builtin_popcountll(mk);
                         }
                     }
                 }
             }
         }
         if (!done) {
-            const int64_t n_all = int64_t(nch) * K;
-            kap = wave_kth_key_mem(cr, n_all, K);
+            const uint64_t kap = lists_kth(pr, ls, nch, cap, K);
             int n = 0;
-            for (int64_t b = 0; b < n_all; b += 64) {
-                const int64_t i = b + lane;
-                const uint64_t k = i < n_all ? cr[i] : 0;
-                const bool take = k >= kap && k != 0;
-                const uint64_t mask = __builtin_amdgcn_ballot_w64(take);
-                if (mask) {
-                    if (take) sl[n + lane_rank(mask)] = k;
-                    n += __builtin_popcountll(mask);
+            for (int c = 0; c < nch; ++c) {
+                const int nl = pr[c].nlist < cap ? pr[c].nlist : cap;
+                for (int p0 = 0; p0 < nl; p0 += 64) {
+                    const int p = p0 + lane;
+                    const uint64_t k = p < nl ? ls[int64_t(c) * cap + p] : 0;
+                    const bool take = k != 0 && k >= kap;
+                    const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
+                    if (mk) {
+                        if (take && n + lane_rank(mk) < 64 * SL) sel[n + lane_rank(mk)] = k;
+                        n += __builtin_popcountll(mk);
+                    }
                 }
             }
         }
         wave_lds_sync();
-        // exactly K keys are >= kap (keys are unique)
+        // exactly K keys were selected (keys are unique)
         uint64_t a[SL];
 #pragma unroll
         for (int q = 0; q < SL; ++q) {
             const int i = SL * lane + q;
-            a[q] = i < K ? sl[i] : 0;
+            a[q] = i < K ? sel[i] : 0;
         }
         wave_sort_desc<uint64_t, SL>(a);
 #pragma unroll
@@ -582,17 +605,21 @@ namespace mg
         need(rows <= 65535, "vocab_reduce: at most 65535 rows per call");
         if (rows == 0) return;
         const int nch = int((V + kVChunk - 1) / kVChunk);
-        const int64_t need_bytes = rows * nch * int64_t(sizeof(VPart)) + rows * nch * K * int64_t(sizeof(uint64_t));
+        const bool small = K <= kFastK;
+        const int cap = small ? 128 : 256;
+        const int64_t nc = rows * nch;
+        const int64_t need_bytes = nc * int64_t(sizeof(VPart) + sizeof(uint64_t) * (kBlk + cap));
         need(need_bytes <= c->work_bytes, "vocab_reduce: partials exceed the context workspace (raise workspace_bytes at mg_open)");
         VPart *part = static_cast<VPart *>(c->work);
-        uint64_t *cand = reinterpret_cast<uint64_t *>(static_cast<char *>(c->work) + rows * nch * int64_t(sizeof(VPart)));
+        uint64_t *blk = reinterpret_cast<uint64_t *>(part + nc);
+        uint64_t *lst = blk + nc * kBlk;
         const dim3 g1{unsigned((nch + 3) / 4), unsigned(rows), 1u};
         const dim3 g2{unsigned(rows), 1u, 1u};
-        const bool small = K <= kFastK;
         auto go = [&](auto chunk, auto merge, const auto *x) {
-            hipLaunchKernelGGL(chunk, g1, dim3(256), 0, c->stream, x, V, int(K), nch, part, cand);
+            hipLaunchKernelGGL(chunk, g1, dim3(256), 0, c->stream, x, V, int(K), nch, part, blk, lst);
             check_launch("k_vocab_chunk");
-            hipLaunchKernelGGL(merge, g2, dim3(64), 0, c->stream, x, V, int(K), nch, part, cand, lse, amax, top_idx, top_val);
+            hipLaunchKernelGGL(merge, g2, dim3(64), 0, c->stream, x, V, int(K), nch, cap, part, blk, lst, lse, amax,
+                               top_idx, top_val);
             check_launch("k_vocab_merge");
         };
         if (dt_in == F32) {

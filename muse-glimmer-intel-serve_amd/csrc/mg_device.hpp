@@ -162,6 +162,93 @@ namespace mg
         return v;
     }
 
+    // DPP wave64 reductions (all 64 lanes active): swap within quads, mirror
+    // within half-rows and rows, then broadcast lane 15 of each row into the
+    // next row and lane 31 into the upper half; lane 63 ends with the result
+    // and readlane hands it to every lane as a uniform value. No LDS traffic,
+    // and a fixed combination order, so floating-point results are
+    // deterministic.
+    template <int CTRL, int ROWS, int BANKS = 0xf>
+    MG_DEV uint32_t dpp32(uint32_t old, uint32_t v)
+    {
+        return uint32_t(__builtin_amdgcn_update_dpp(int(old), int(v), CTRL, ROWS, BANKS, false));
+    }
+    // inclusive prefix sum over the lanes (all active): shifts by 1, 2, 3
+    // within rows of 16, then 4 and 8 into the upper banks, then the row
+    // broadcasts of lanes 15 and 31
+    MG_DEV int wave_prefix_sum(int v)
+    {
+        const uint32_t u = uint32_t(v);
+        uint32_t t = u;
+        t += dpp32<0x111, 0xf>(0u, u);      // row_shr:1
+        t += dpp32<0x112, 0xf>(0u, u);      // row_shr:2
+        t += dpp32<0x113, 0xf>(0u, u);      // row_shr:3
+        t += dpp32<0x114, 0xf, 0xe>(0u, t); // row_shr:4, banks 1-3
+        t += dpp32<0x118, 0xf, 0xc>(0u, t); // row_shr:8, banks 2-3
+        t += dpp32<0x142, 0xa>(0u, t);      // row_bcast:15 into rows 1, 3
+        t += dpp32<0x143, 0xc>(0u, t);      // row_bcast:31 into rows 2, 3
+        return int(t);
+    }
+    template <int CTRL, int ROWS, typename T>
+    MG_DEV T dpp_mov(T old, T v)
+    {
+        if constexpr (sizeof(T) == 4) {
+            return __builtin_bit_cast(T, dpp32<CTRL, ROWS>(__builtin_bit_cast(uint32_t, old), __builtin_bit_cast(uint32_t, v)));
+        } else {
+            using U2 = Vec<uint32_t, 2>;
+            const U2 o = __builtin_bit_cast(U2, old), x = __builtin_bit_cast(U2, v);
+            U2 r;
+            r.v[0] = dpp32<CTRL, ROWS>(o.v[0], x.v[0]);
+            r.v[1] = dpp32<CTRL, ROWS>(o.v[1], x.v[1]);
+            return __builtin_bit_cast(T, r);
+        }
+    }
+    template <typename T>
+    MG_DEV T readlane63(T v)
+    {
+        if constexpr (sizeof(T) == 4) {
+            return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+        } else {
+            using U2 = Vec<int, 2>;
+            U2 x = __builtin_bit_cast(U2, v);
+            x.v[0] = __builtin_amdgcn_readlane(x.v[0], 63);
+            x.v[1] = __builtin_amdgcn_readlane(x.v[1], 63);
+            return __builtin_bit_cast(T, x);
+        }
+    }
+    template <typename T, class OP>
+    MG_DEV T dpp_reduce(T v, T id, OP op)
+    {
+        v = op(v, dpp_mov<0xB1, 0xf>(id, v));  // quad_perm [1,0,3,2]
+        v = op(v, dpp_mov<0x4E, 0xf>(id, v));  // quad_perm [2,3,0,1]
+        v = op(v, dpp_mov<0x141, 0xf>(id, v)); // row_half_mirror
+        v = op(v, dpp_mov<0x140, 0xf>(id, v)); // row_mirror
+        v = op(v, dpp_mov<0x142, 0xa>(id, v)); // row_bcast:15 into rows 1, 3
+        v = op(v, dpp_mov<0x143, 0xc>(id, v)); // row_bcast:31 into rows 2, 3
+        return readlane63(v);
+    }
+    MG_DEV float dpp_max(float v)
+    {
+        return dpp_reduce(v, -__builtin_huge_valf(), [](float a, float b) { return __builtin_fmaxf(a, b); });
+    }
+    MG_DEV double dpp_sum(double v)
+    {
+        return dpp_reduce(v, 0.0, [](double a, double b) { return a + b; });
+    }
+    MG_DEV uint32_t dpp_min_u32(uint32_t v)
+    {
+        return dpp_reduce(v, 0xffffffffu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+    }
+    MG_DEV uint32_t dpp_max_u32(uint32_t v)
+    {
+        return dpp_reduce(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+    }
+    // number of lanes for which p holds (uniform)
+    MG_DEV int wave_count(bool p)
+    {
+        return __builtin_popcountll(__builtin_amdgcn_ballot_w64(p));
+    }
+
     // ---------------------------------------------------------------- f32 exp
     // e^(x + lo) for the f32 reductions, lo a small correction term (|lo| <=
     // ulp(x)/2): Cody–Waite reduction x = n·ln2 + r with the Cephes
