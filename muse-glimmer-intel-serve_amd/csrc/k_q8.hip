@@ -8,58 +8,65 @@
 // f16 subnormal scales decode exactly (v_cvt_f32_f16 keeps them,
 // gpu_engine.cpp:145-151 explains why that matters).
 //
-// One thread owns 16 quants (one 16-byte load; the 16 never straddle a 32-block)
-// and writes them as 32 bytes of bf16; four such groups are in flight per
-// thread; the scale read is 2 bytes per thread, coalesced across the wave.
+// A lane owns Q = 16 / sizeof(out) consecutive quants (8 for bf16/f16, 4 for
+// f32): one Q-byte load and one 16-byte store, so every load and store
+// instruction of a wave covers one contiguous span (512 B in, 1 KiB out for
+// bf16) and no cache line is written in parts. A work-group of 256 lanes
+// takes U = 4 such spans per lane in flight; the grid covers the tensor
+// exactly. The scale read is 2 bytes per lane, shared by the 32/Q lanes of
+// its block and coalesced across the wave.
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
 
 namespace mg
 {
+    template <int Q>
+    MG_DEV Vec<int8_t, Q> ld_quants(const int8_t *p)
+    {
+        if constexpr (Q == 8) {
+            const uint64_t u = __builtin_nontemporal_load(reinterpret_cast<const uint64_t *>(p));
+            return __builtin_bit_cast(Vec<int8_t, 8>, u);
+        } else {
+            const uint32_t u = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+            return __builtin_bit_cast(Vec<int8_t, 4>, u);
+        }
+    }
+
     template <class SO>
     __global__ __launch_bounds__(256) void k_dequant_q8_0(const int8_t *__restrict__ qs,
                                                           const uint16_t *__restrict__ d,
                                                           typename SO::raw *__restrict__ out,
-                                                          int64_t ngroups)
+                                                          int64_t nspans)
     {
         using raw = typename SO::raw;
-        constexpr int U = 4;
-        const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-        for (int64_t base = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; base < ngroups; base += stride * U) {
-            Vec<int8_t, 16> q[U];
-            float sc[U];
+        constexpr int Q = 16 / sizeof(raw), U = 4;
+        const int64_t base = int64_t(blockIdx.x) * (256 * U) + threadIdx.x;
+        Vec<int8_t, Q> q[U];
+        float sc[U];
 #pragma unroll
-            for (int k = 0; k < U; ++k) {
-                const int64_t g = base + k * stride;
-                if (g < ngroups) {
-                    q[k] = ld16_stream<int8_t, 16>(qs + 16 * g);
-                    // `in` is a multiple of 32, so group g's 32-block is g / 2 in
-                    // the row-major [rows, in/32] scale array
-                    sc[k] = f16_f32(d[g >> 1]);
-                }
+        for (int k = 0; k < U; ++k) {
+            const int64_t g = base + 256 * k;
+            if (g < nspans) {
+                q[k] = ld_quants<Q>(qs + Q * g);
+                // `in` is a multiple of 32, so span g lies in the row-major
+                // [rows, in/32] scale array's block g*Q/32
+                sc[k] = f16_f32(d[(g * Q) >> 5]);
             }
+        }
 #pragma unroll
-            for (int k = 0; k < U; ++k) {
-                const int64_t g = base + k * stride;
-                if (g < ngroups) {
-                    raw o[16];
-                    if (__builtin_isfinite(sc[k])) {
-                        // int8 x finite scale: finite products, no NaN to canonicalize
+        for (int k = 0; k < U; ++k) {
+            const int64_t g = base + 256 * k;
+            if (g < nspans) {
+                Vec<raw, Q> o;
+                if (__builtin_isfinite(sc[k])) {
+                    // int8 x finite scale: finite products, no NaN to canonicalize
 #pragma unroll
-                        for (int e = 0; e < 16; ++e) o[e] = SO::enc_finite(float(q[k].v[e]) * sc[k]);
-                    } else {
+                    for (int e = 0; e < Q; ++e) o.v[e] = SO::enc_finite(float(q[k].v[e]) * sc[k]);
+                } else {
 #pragma unroll
-                        for (int e = 0; e < 16; ++e) o[e] = SO::enc32(float(q[k].v[e]) * sc[k]);
-                    }
-                    constexpr int V = 16 / sizeof(raw);
-#pragma unroll
-                    for (int p = 0; p < 16 / V; ++p) {
-                        Vec<raw, V> w;
-#pragma unroll
-                        for (int e = 0; e < V; ++e) w.v[e] = o[p * V + e];
-                        st16_stream<raw, V>(out + 16 * g + p * V, w);
-                    }
+                    for (int e = 0; e < Q; ++e) o.v[e] = SO::enc32(float(q[k].v[e]) * sc[k]);
                 }
+                st16_stream<raw, Q>(out + Q * g, o);
             }
         }
     }
@@ -72,12 +79,15 @@ namespace mg
         need(qs && d && out, "dequant_q8_0: NULL tensor");
         need(aligned16(qs) && aligned16(out), "dequant_q8_0: quants and output must be 16-byte aligned");
         if (rows == 0 || in == 0) return;
-        const int64_t ngroups = rows * (in / 16);
-        const unsigned blocks = unsigned(std::min<int64_t>((ngroups + 1023) / 1024, int64_t(c->num_cus) * 32));
+        const int64_t n = rows * in;
+        const int Q = dt_out == F32 ? 4 : 8;
+        const int64_t nspans = n / Q, blocks = (nspans + 1023) / 1024;
+        need(blocks < (int64_t(1) << 31), "dequant_q8_0: tensor too large");
+        const dim3 g{unsigned(blocks), 1u, 1u};
         switch (dt_out) {
-        case BF16: hipLaunchKernelGGL(k_dequant_q8_0<SBf16>, dim3(blocks), dim3(256), 0, c->stream, qs, d, static_cast<uint16_t *>(out), ngroups); break;
-        case F16: hipLaunchKernelGGL(k_dequant_q8_0<SF16>, dim3(blocks), dim3(256), 0, c->stream, qs, d, static_cast<uint16_t *>(out), ngroups); break;
-        case F32: hipLaunchKernelGGL(k_dequant_q8_0<SF32>, dim3(blocks), dim3(256), 0, c->stream, qs, d, static_cast<float *>(out), ngroups); break;
+        case BF16: hipLaunchKernelGGL(k_dequant_q8_0<SBf16>, g, dim3(256), 0, c->stream, qs, d, static_cast<uint16_t *>(out), nspans); break;
+        case F16: hipLaunchKernelGGL(k_dequant_q8_0<SF16>, g, dim3(256), 0, c->stream, qs, d, static_cast<uint16_t *>(out), nspans); break;
+        case F32: hipLaunchKernelGGL(k_dequant_q8_0<SF32>, g, dim3(256), 0, c->stream, qs, d, static_cast<float *>(out), nspans); break;
         default: fail("dequant_q8_0: output dtype must be bf16, f16 or f32");
         }
         check_launch("k_dequant_q8_0");

@@ -358,6 +358,16 @@ namespace mg
         const int64_t row = blockIdx.y;
         const int nch = int(gridDim.x);
         const float2 *pr = part + row * nch;
+        // this chunk's scores first, so their latency overlaps the merge
+        int64_t lo, hi;
+        row_range(a, row, lo, hi);
+        const typename SI::raw *xr = x + row * a.kc;
+        typename SO::raw *yr = y + row * a.kc;
+        const int64_t base = int64_t(blockIdx.x) * kSplitChunk;
+        float s[2][8];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            load_scores<SI, CAP>(a, xr, base + int64_t(threadIdx.x + 256 * c) * 8, lo, hi, vec, s[c]);
         float M = kNegInf;
         for (int i = threadIdx.x; i < nch; i += blockDim.x) M = pr[i].x > M ? pr[i].x : M;
         M = block_max_f32(M, red);
@@ -367,19 +377,12 @@ namespace mg
                 if (pr[i].x != kNegInf) L += double(pr[i].y) * mgm::exp(double(pr[i].x) - double(M));
         L = block_sum_f64(L, redd);
         const float inv = M == kNegInf ? 0.0f : float(1.0 / L);
-        int64_t lo, hi;
-        row_range(a, row, lo, hi);
-        const typename SI::raw *xr = x + row * a.kc;
-        typename SO::raw *yr = y + row * a.kc;
-        const int64_t base = int64_t(blockIdx.x) * kSplitChunk;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const int64_t j0 = base + int64_t(threadIdx.x + 256 * c) * 8;
-            float s[8];
-            load_scores<SI, CAP>(a, xr, j0, lo, hi, vec, s);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s[e] = s[e] == kNegInf ? 0.0f : exp_diff(s[e], M) * inv;
-            store_probs<SO>(a, yr, j0, vec, s);
+            for (int e = 0; e < 8; ++e) s[c][e] = s[c][e] == kNegInf ? 0.0f : exp_diff(s[c][e], M) * inv;
+            store_probs<SO>(a, yr, j0, vec, s[c]);
         }
     }
 
