@@ -386,6 +386,110 @@ namespace mg
         }
     }
 
+    // Long rows of f32 scores to 16-bit probabilities without softcap: the
+    // log2-domain math of k_softmax_fast over 4096-key chunks (f32 partial
+    // sums, merged as sum_c l_c * 2^(m_c - M)), with DPP reductions. A row
+    // with NaN or +inf scores gets NaN sums and so NaN probabilities, as on
+    // the accurate path; masked keys stay exactly 0.
+    MG_DEV void load_t8(const float *xr, int64_t j0, int64_t lo, int64_t hi, int64_t kc, bool vec, float c2,
+                        float *t)
+    {
+        if (vec && j0 >= lo && j0 + 7 <= hi && j0 + 8 <= kc) {
+            float v[8];
+            load8_stream(xr + j0, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) t[e] = v[e] * c2;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t j = j0 + e;
+                t[e] = (j >= lo && j <= hi && j < kc) ? xr[j] * c2 : kNegInf;
+            }
+        }
+    }
+    MG_DEV float block_max_dpp(float v, float *red)
+    {
+        v = dpp_max(v);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        const float t = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+        __syncthreads();
+        return t;
+    }
+    MG_DEV float block_sum_dpp(float v, float *red)
+    {
+        v = float(dpp_sum(double(v)));
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        const float t = (red[0] + red[1]) + (red[2] + red[3]);
+        __syncthreads();
+        return t;
+    }
+
+    __global__ __launch_bounds__(256) void k_softmax_partial_fast(const float *__restrict__ x, SmArgs a, float c2,
+                                                                  bool vec, float2 *__restrict__ part)
+    {
+        __shared__ float red[4];
+        const int64_t row = blockIdx.y;
+        int64_t lo, hi;
+        row_range(a, row, lo, hi);
+        const float *xr = x + row * a.kc;
+        const int64_t base = int64_t(blockIdx.x) * kSplitChunk;
+        float t[2][8];
+        float m = kNegInf;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            load_t8(xr, base + int64_t(threadIdx.x + 256 * c) * 8, lo, hi, a.kc, vec, c2, t[c]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = t[c][e] > m ? t[c][e] : m;
+        }
+        m = block_max_dpp(m, red);
+        float sum = 0.0f;
+        if (m != kNegInf)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sum += __builtin_amdgcn_exp2f(t[c][e] - m); // exp2(-inf) = 0
+        sum = block_sum_dpp(sum, red);
+        if (threadIdx.x == 0) part[row * gridDim.x + blockIdx.x] = make_float2(m, sum);
+    }
+
+    template <class SO>
+    __global__ __launch_bounds__(256) void k_softmax_finish_fast(const float *__restrict__ x,
+                                                                 typename SO::raw *__restrict__ y, SmArgs a,
+                                                                 float c2, bool vec,
+                                                                 const float2 *__restrict__ part)
+    {
+        __shared__ float red[4];
+        const int64_t row = blockIdx.y;
+        const int nch = int(gridDim.x);
+        const float2 *pr = part + row * nch;
+        int64_t lo, hi;
+        row_range(a, row, lo, hi);
+        const float *xr = x + row * a.kc;
+        typename SO::raw *yr = y + row * a.kc;
+        const int64_t base = int64_t(blockIdx.x) * kSplitChunk;
+        // this chunk's scores first, so their latency overlaps the merge
+        float t[2][8];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) load_t8(xr, base + int64_t(threadIdx.x + 256 * c) * 8, lo, hi, a.kc, vec, c2, t[c]);
+        float M = kNegInf;
+        for (int i = threadIdx.x; i < nch; i += blockDim.x) M = pr[i].x > M ? pr[i].x : M;
+        M = block_max_dpp(M, red);
+        float L = 0.0f;
+        if (M != kNegInf)
+            for (int i = threadIdx.x; i < nch; i += blockDim.x)
+                if (pr[i].x != kNegInf) L += pr[i].y * __builtin_amdgcn_exp2f(pr[i].x - M);
+        L = block_sum_dpp(L, red);
+        const float inv = M == kNegInf ? 0.0f : 1.0f / L;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) t[c][e] = t[c][e] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(t[c][e] - M) * inv;
+            store_probs<SO>(a, yr, base + int64_t(threadIdx.x + 256 * c) * 8, vec, t[c]);
+        }
+    }
+
     template <class SI, class SO, bool CAP>
     void launch_softmax_t(mg_ctx *c, const void *x, void *y, const SmArgs &a)
     {
@@ -423,6 +527,14 @@ namespace mg
              "softmax: partials exceed the context workspace (raise workspace_bytes at mg_open)");
         float2 *part = static_cast<float2 *>(c->work);
         const dim3 grid{unsigned(nch), unsigned(a.nrows), 1u};
+        if constexpr (SI::dt == F32 && sizeof(ro) == 2 && !CAP) {
+            const float c2 = float(double(a.scale) * 1.4426950408889634);
+            hipLaunchKernelGGL(k_softmax_partial_fast, grid, dim3(256), 0, c->stream, xi, a, c2, vec, part);
+            check_launch("k_softmax_partial_fast");
+            hipLaunchKernelGGL(k_softmax_finish_fast<SO>, grid, dim3(256), 0, c->stream, xi, yo, a, c2, vec, part);
+            check_launch("k_softmax_finish_fast");
+            return;
+        }
         hipLaunchKernelGGL((k_softmax_partial<SI, CAP>), grid, dim3(256), 0, c->stream, xi, a, vec, part);
         check_launch("k_softmax_partial");
         hipLaunchKernelGGL((k_softmax_finish<SI, SO, CAP>), grid, dim3(256), 0, c->stream, xi, yo, a, vec, part);

@@ -114,6 +114,34 @@ def test_split_ragged_and_masked(prims):
     check(y, ref, F32, visible(2, 3, 20000, O.MASK_WINDOW, 7000, 15000))
 
 
+def test_split_two_kernel_path(prims):
+    """more split work-groups than can be resident at once (1024 rows x 2
+    chunks): the two-kernel path instead of the one-read cooperative one"""
+    y, ref = run(prims, 8, 128, 6000, q_pos0=5872)
+    check(y, ref, BF16, visible(8, 128, 6000, O.MASK_CAUSAL, 0, 5872))
+
+
+def test_split_two_kernel_nonfinite(prims):
+    """split rows with a NaN or +inf score: NaN probabilities where the twin
+    has them (canonical bits), exact zeros where masked, the rest untouched"""
+    heads, q, kc = 3, 2, 9000
+    xs, x = storage(9, (heads, q, kc), F32, 0.0, 3.0)
+    x = x.copy()
+    x[0, 0, 4321] = np.nan
+    x[1, 1, 77] = np.inf
+    xs = O.from_f64(x, F32)
+    dx = to_dev(xs, F32)
+    dy = to_dev(np.zeros((heads, q, kc), np.uint16), BF16)
+    prims.softmax_rows(dx, dy, SCALE, O.MASK_CAUSAL, 0, 8990, 0.0)
+    y = from_dev(dy, BF16)
+    ref = O.from_f64(O.softmax_rows(x, SCALE, O.MASK_CAUSAL, 0, 8990, 0.0, F32, O.F64), BF16)
+    bad = np.zeros((heads, q), bool)
+    bad[0, 0] = bad[1, 1] = True
+    assert np.array_equal(y[bad], ref[bad])
+    d = ulp_diff16(y[~bad], ref[~bad])
+    assert d.max() <= 1
+
+
 def test_all_masked_row_is_zero(prims):
     """window rows with q_pos0 < 0 see no key at all: zeros, not NaN"""
     y, ref = run(prims, 1, 4, 64, mask=O.MASK_WINDOW, window=2, q_pos0=-10)
