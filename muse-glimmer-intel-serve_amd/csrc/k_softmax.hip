@@ -200,93 +200,86 @@ namespace mg
 
     // Lean row for f32 scores and 16-bit probabilities without softcap (the
     // attention-score configuration). Scores are taken in the log2 domain,
-    // t = x * (scale*log2 e), and p = 2^(t - max t) / sum on the hardware exp2:
-    // about 7 instructions per key instead of ~30, with a relative error of a
-    // few 1e-7 (well inside the 16-bit output's half-ulp of 2e-3, so outputs
-    // stay within 1 ulp of the twin). Chunks entirely visible skip the
-    // per-key mask; chunks entirely masked skip the arithmetic. A row whose
-    // sum is not finite (NaN or infinite scores) is redone on the accurate path.
+    // p = 2^(x*c2 - max*c2) / sum on the hardware exp2, c2 = scale*log2 e > 0:
+    // the max is taken over the raw scores (multiplying by c2 > 0 keeps the
+    // order) and each key costs one fma, one exp2 and one add before the
+    // normalisation; relative error a few 1e-7, well inside the 16-bit
+    // output's half-ulp of 2e-3, so outputs stay within 1 ulp of the twin.
+    // Key indices are 32-bit (rows of at most 2048 keys); chunks entirely
+    // visible skip the per-key mask, chunks entirely masked skip the
+    // arithmetic and store zeros. A row whose sum is not finite (NaN or
+    // infinite scores) is redone on the accurate path.
     template <class SO, int CH>
     __global__ __launch_bounds__(256) void k_softmax_fast(const float *__restrict__ x,
                                                           typename SO::raw *__restrict__ y, SmArgs a,
                                                           float c2, bool vec)
     {
+        using ro = typename SO::raw;
         const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
         const int lane = threadIdx.x & 63;
         if (row >= a.nrows) return;
-        int64_t lo, hi;
-        row_range(a, row, lo, hi);
+        int64_t lo64, hi64;
+        row_range(a, row, lo64, hi64);
+        const int kc = int(a.kc);
+        const int lo = int(lo64 < 0 ? 0 : lo64), hi = int(hi64 >= kc ? kc - 1 : hi64); // visible: lo..hi
         const float *xr = x + row * a.kc;
-        typename SO::raw *yr = y + row * a.kc;
-        float t[CH][8];
+        ro *yr = y + row * a.kc;
+        float v[CH][8];
         float m = kNegInf;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            const int64_t cb = int64_t(c) * 512, ce = cb + 511; // the wave's keys in chunk c
-            const int64_t j0 = cb + lane * 8;
-            if (cb > hi || ce < lo || cb >= a.kc) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) t[c][e] = kNegInf;
-            } else if (vec && cb >= lo && ce <= hi) { // every key of the chunk visible
-                float v[8];
-                load8_stream(xr + j0, v);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    t[c][e] = v[e] * c2;
-                    m = t[c][e] > m ? t[c][e] : m;
-                }
+            const int cb = c * 512, j0 = cb + lane * 8;
+            if (cb > hi || cb + 511 < lo) continue; // nothing of this chunk visible
+            if (vec && cb >= lo && cb + 511 <= hi) {
+                load8_stream(xr + j0, v[c]);
             } else {
-                float v[8];
-                if (vec && j0 + 8 <= a.kc && j0 <= hi && j0 + 7 >= lo)
-                    load8_stream(xr + j0, v);
+                if (vec && j0 + 8 <= kc && j0 <= hi && j0 + 7 >= lo)
+                    load8_stream(xr + j0, v[c]);
                 else
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = (j0 + e < a.kc && j0 + e <= hi && j0 + e >= lo) ? xr[j0 + e] : 0.0f;
+                    for (int e = 0; e < 8; ++e) v[c][e] = (j0 + e >= lo && j0 + e <= hi) ? xr[j0 + e] : 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    v[c][e] = unsigned(j0 + e - lo) <= unsigned(hi - lo) ? v[c][e] : kNegInf;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = __builtin_fmaxf(m, v[c][e]);
+        }
+        m = dpp_max(m);
+        float sum = 0.0f;
+        if (m != kNegInf) {
+            const float mc = m * c2;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int cb = c * 512;
+                if (cb > hi || cb + 511 < lo) continue;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const int64_t j = j0 + e;
-                    t[c][e] = (j >= lo && j <= hi && j < a.kc) ? v[e] * c2 : kNegInf;
-                    m = t[c][e] > m ? t[c][e] : m;
+                    v[c][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[c][e], c2, -mc)); // masked: exp2(-inf) = 0
+                    sum += v[c][e];
                 }
             }
         }
-        m = wave_max(m);
-        float sum = 0.0f;
-        if (m != kNegInf)
-#pragma unroll
-            for (int c = 0; c < CH; ++c) {
-                const int64_t cb = int64_t(c) * 512;
-                if (cb > hi || cb + 511 < lo || cb >= a.kc) continue;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    t[c][e] = __builtin_amdgcn_exp2f(t[c][e] - m); // exp2(-inf) = 0
-                    sum += t[c][e];
-                }
-            }
-        sum = wave_sum(sum);
+        sum = dpp_sum_f32(sum);
         if (m != kNegInf && !(sum < __builtin_huge_valf())) { // NaN / infinite scores
-            softmax_row_accurate<SF32, SO, CH, false>(a, xr, yr, lo, hi, vec, lane);
+            softmax_row_accurate<SF32, SO, CH, false>(a, xr, yr, lo64, hi64, vec, lane);
             return;
         }
         const float inv = m == kNegInf ? 0.0f : __builtin_amdgcn_rcpf(sum);
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            const int64_t cb = int64_t(c) * 512;
-            const int64_t j0 = cb + lane * 8;
-            if (j0 >= a.kc) continue;
+            const int cb = c * 512, j0 = cb + lane * 8;
+            if (j0 >= kc) continue;
             const bool none = m == kNegInf || cb > hi || cb + 511 < lo;
-            typename SO::raw o[8];
+            Vec<ro, 8> o;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = none ? typename SO::raw(0) : SO::enc_finite(t[c][e] * inv);
-            if (vec && j0 + 8 <= a.kc) {
-                Vec<typename SO::raw, 8> w;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) w.v[e] = o[e];
-                st16_stream<typename SO::raw, 8>(yr + j0, w);
+            for (int e = 0; e < 8; ++e) o.v[e] = none ? ro(0) : SO::enc_finite(v[c][e] * inv);
+            if (vec && j0 + 8 <= kc) {
+                st16_stream<ro, 8>(yr + j0, o);
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    if (j0 + e < a.kc) yr[j0 + e] = o[e];
+                    if (j0 + e < kc) yr[j0 + e] = o.v[e];
             }
         }
     }
@@ -501,7 +494,7 @@ namespace mg
         if (a.kc <= 2048) {
             const unsigned blocks = unsigned((a.nrows + 3) / 4);
             need((a.nrows + 3) / 4 < (int64_t(1) << 31), "softmax: too many rows");
-            if constexpr (SI::dt == F32 && sizeof(ro) == 2 && !CAP) {
+            if constexpr (SI::dt == F32 && sizeof(ro) == 2 && !CAP) if (a.scale > 0.0) {
                 const float c2 = float(double(a.scale) * 1.4426950408889634);
                 if (a.kc <= 512)
                     hipLaunchKernelGGL((k_softmax_fast<SO, 1>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, c2, vec);

@@ -235,6 +235,10 @@ namespace mg
     {
         return dpp_reduce(v, 0.0, [](double a, double b) { return a + b; });
     }
+    MG_DEV float dpp_sum_f32(float v)
+    {
+        return dpp_reduce(v, 0.0f, [](float a, float b) { return a + b; });
+    }
     MG_DEV uint32_t dpp_min_u32(uint32_t v)
     {
         return dpp_reduce(v, 0xffffffffu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
