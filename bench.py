@@ -57,6 +57,9 @@ BYTES = {
     "softmax_decode": SM_H * DEC_K * (4 + 2),
     "dequant_q8_0": Q8_R * Q8_C + Q8_R * (Q8_C // 32) * 2 + Q8_R * Q8_C * 2,
     "vocab_lse_argmax_top64": V_ROWS * VOCAB * 4 + V_ROWS * (8 + 8) + V_ROWS * TOPK * (8 + 4),
+    # q, k read + written, v read, k/v cache rows written, cos/sin read
+    "qk_norm_rope_kv": 2 * (2 * T * Q_H * HD + 2 * T * K_H * HD) + 2 * T * K_H * HD + 2 * 2 * T * K_H * HD
+                       + 2 * 2 * T * (HD // 2),
 }
 STEP_OPS = ("residual_rmsnorm", "swiglu", "softmax_causal")
 KERNEL_OF = {
@@ -67,6 +70,7 @@ KERNEL_OF = {
     "softmax_decode": "k_softmax_partial + k_softmax_finish",
     "dequant_q8_0": "k_dequant_q8_0",
     "vocab_lse_argmax_top64": "k_vocab_chunk + k_vocab_merge",
+    "qk_norm_rope_kv": "k_qk_norm_rope",
 }
 
 
@@ -119,6 +123,9 @@ def make_inputs(torch, P):
     I["amax"] = torch.empty(V_ROWS, dtype=torch.int64, device=dev)
     I["tidx"] = torch.empty((V_ROWS, TOPK), dtype=torch.int64, device=dev)
     I["tval"] = torch.empty((V_ROWS, TOPK), dtype=torch.float32, device=dev)
+    I["v"] = randn((T, K_H, HD))
+    I["kcache"] = torch.empty((T, K_H, HD), dtype=bf, device=dev)
+    I["vcache"] = torch.empty((T, K_H, HD), dtype=bf, device=dev)
     I["hdec"] = randn((64, D))
     I["xdec"] = randn((64, D))
     I["ydec"] = torch.empty((64, D), dtype=bf, device=dev)
@@ -133,6 +140,8 @@ def make_inputs(torch, P):
         "softmax_decode": lambda: P.softmax_rows(I["dscores"], I["dprobs"], scale, M.MASK_CAUSAL, 0, DEC_K - 1),
         "dequant_q8_0": lambda: P.dequant_q8_0(I["qs"], I["qd"], I["deq"]),
         "vocab_lse_argmax_top64": lambda: P.vocab_reduce(I["logits"], TOPK, I["lse"], I["amax"], I["tidx"], I["tval"]),
+        "qk_norm_rope_kv": lambda: P.qk_norm_rope(I["q"], I["k"], 1e-6, 3.87, I["cos"], I["sin"], None, 0, I["v"],
+                                                  I["kcache"], I["vcache"]),
     }
     for t in (1, 4, 16, 64):
         ops[f"residual_rmsnorm_T{t}"] = (lambda t=t: P.residual_rmsnorm(

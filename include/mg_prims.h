@@ -109,6 +109,26 @@ int mg_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k, int64_t
             int64_t ldk, int64_t tokens, int64_t head_dim, const void *cos_t, const void *sin_t,
             int64_t table_rows, const int64_t *positions, int64_t pos0, int dtype);
 
+/* The caller sequence around RoPE in one pass (src/muse_glimmer.hpp:799-819;
+ * GPU src/gpu/gpu_engine.cpp:4339-4350 and k_kv_append 481-492), in place on
+ * q [tokens, q_heads, head_dim] and k [tokens, k_heads, head_dim]:
+ *   weight-less RMSNorm of every head row over head_dim (eps),
+ *   q = rnd(q * qk_scale) (q only; qk_scale taken as an f32 value outside f64),
+ *   rotate-half RoPE with table row positions[t] or pos0 + t, when cos_t/sin_t
+ *   are given (NULL for NoPE layers; rows outside the table stay unrotated),
+ *   and, when k_cache is given, k_cache[p % cache_slots, g, :] = k and (with
+ *   v/v_cache) v_cache[p % cache_slots, g, :] = v for token position p >= 0;
+ *   the caches are [cache_slots, k_heads, head_dim] (the ring of k_kv_append);
+ *   two tokens of one call that map to one slot race, as in the reference.
+ * Each step rounds to `dtype` exactly as mg_rmsnorm_rows, mg_scale and mg_rope
+ * do, so the result is bit-identical to running them in sequence.
+ * ldq/ldk/ldv: token strides in elements (0 = heads*head_dim). */
+int mg_qk_norm_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k, int64_t k_heads,
+                    int64_t ldk, int64_t tokens, int64_t head_dim, double eps, double qk_scale,
+                    const void *cos_t, const void *sin_t, int64_t table_rows, const int64_t *positions,
+                    int64_t pos0, const void *v, int64_t ldv, void *k_cache, void *v_cache,
+                    int64_t cache_slots, int dtype);
+
 /* Scaled, masked row softmax over a contiguous [heads, q, k] score block — the
  * softmax of attention_forward (src/muse_glimmer.hpp:828-885) as a row operator:
  * s = x*scale (f32 opmath), optional tanh softcap s = cap*tanh(s/cap) in

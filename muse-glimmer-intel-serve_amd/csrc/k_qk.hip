@@ -1,0 +1,175 @@
+// Fused QK-norm + qk-scale + RoPE + KV-cache append for gfx950: the caller
+// sequence around RoPE, one pass over q and k.
+//
+// Reference sequence (src/muse_glimmer.hpp:799-819; GPU engine
+// src/gpu/gpu_engine.cpp:4339-4350 and k_kv_append 481-492):
+//   q[t,h,:] = rnd(q * rs)            weight-less rmsnorm_rows over head_dim
+//   k[t,g,:] = rnd(k * rs)            (rs = 1/sqrt(mean_sq + eps) per head row)
+//   q        = rnd(q * qk_scale)      q only; qk_scale an f32 value outside f64
+//   q, k     = apply_rope(., table row pos)   when a table is given
+//   k_cache[pos % slots, g, :] = k,  v_cache[pos % slots, g, :] = v
+// Each step materializes at storage exactly as the separate primitives do, so
+// the result is bit-identical to running mg_rmsnorm_rows, mg_scale, mg_rope and
+// the two cache copies one after the other.
+//
+// A work-group takes 32 head rows (of q and k alike) staged in LDS with
+// 16-byte loads; eight lanes per row run mean_sq's eight interleaved f64
+// accumulators in the reference order and its fixed tree (bit-identical rs);
+// then every thread takes (lo, hi) pairs of a row: normalize, scale, rotate,
+// store back and append to the caches.
+#include "mg_device.hpp"
+#include "mg_internal.hpp"
+
+namespace mg
+{
+    constexpr int kQkRows = 32;
+
+    struct QkArgs
+    {
+        int64_t nq, nkv, ldq, ldk, ldv, T, table_rows, pos0, slots;
+        int D;
+        double eps;
+    };
+
+    template <class S, int VEC>
+    __global__ __launch_bounds__(256) void k_qk_norm_rope(typename S::raw *q, typename S::raw *k,
+                                                          const typename S::raw *__restrict__ v, QkArgs a,
+                                                          typename S::comp qs,
+                                                          const typename S::raw *__restrict__ co,
+                                                          const typename S::raw *__restrict__ si,
+                                                          const int64_t *__restrict__ pos,
+                                                          typename S::raw *kc, typename S::raw *vc)
+    {
+        using raw = typename S::raw;
+        extern __shared__ double smem_d[];
+        double *rsq = smem_d;                                 // [kQkRows]
+        raw *st = reinterpret_cast<raw *>(smem_d + kQkRows); // [kQkRows][D]
+        const int D = a.D, half = D / 2;
+        const int64_t heads = a.nq + a.nkv, rows = a.T * heads;
+        const int64_t r0 = int64_t(blockIdx.x) * kQkRows;
+        const int nr = int(rows - r0 < kQkRows ? rows - r0 : kQkRows);
+        auto row_ptr = [&](int64_t r) -> raw * {
+            const int64_t t = r / heads, hh = r - t * heads;
+            return hh < a.nq ? q + t * a.ldq + hh * D : k + t * a.ldk + (hh - a.nq) * D;
+        };
+
+        // stage the head rows
+        const int vpr = D / VEC;
+        for (int idx = threadIdx.x; idx < nr * vpr; idx += blockDim.x) {
+            const int rr = idx / vpr, i = (idx - rr * vpr) * VEC;
+            *reinterpret_cast<Vec<raw, VEC> *>(st + rr * D + i) = *reinterpret_cast<const Vec<raw, VEC> *>(row_ptr(r0 + rr) + i);
+        }
+        __syncthreads();
+
+        // mean_sq (src/muse_glimmer.hpp:509-527): lane l of a row's 8-lane
+        // group owns accumulator a_l
+        {
+            const int rr = threadIdx.x >> 3, l = threadIdx.x & 7;
+            const int full = D & ~7;
+            double acc = 0.0;
+            if (rr < nr)
+                for (int i = l; i < full; i += 8) {
+                    const double x = double(S::dec(st[rr * D + i]));
+                    acc += x * x;
+                }
+            const double s1 = acc + __shfl_xor(acc, 1, 64);
+            const double s2 = s1 + __shfl_xor(s1, 2, 64);
+            const double s3 = s2 + __shfl_xor(s2, 4, 64);
+            if (rr < nr && l == 0) {
+                double tail = 0.0;
+                for (int i = full; i < D; ++i) {
+                    const double x = double(S::dec(st[rr * D + i]));
+                    tail += x * x;
+                }
+                rsq[rr] = 1.0 / __builtin_sqrt((s3 + tail) / double(D) + a.eps);
+            }
+        }
+        __syncthreads();
+
+        // (lo, hi) pairs: normalize, scale q, rotate, store, append
+        for (int idx = threadIdx.x; idx < nr * half; idx += blockDim.x) {
+            const int rr = idx / half, j = idx - rr * half;
+            const int64_t r = r0 + rr, t = r / heads, hh = r - t * heads;
+            const bool isq = hh < a.nq;
+            const double rs = rsq[rr];
+            raw lo = S::enc64(double(S::dec(st[rr * D + j])) * rs);
+            raw hi = S::enc64(double(S::dec(st[rr * D + j + half])) * rs);
+            if (isq) {
+                lo = S::enc(S::dec(lo) * qs);
+                hi = S::enc(S::dec(hi) * qs);
+            }
+            const int64_t p = pos ? pos[t] : a.pos0 + t;
+            if (co && p >= 0 && p < a.table_rows) rope_pair<S>(lo, hi, co[p * half + j], si[p * half + j]);
+            raw *dst = row_ptr(r);
+            dst[j] = lo;
+            dst[j + half] = hi;
+            if (!isq && kc && p >= 0) {
+                const int64_t g = hh - a.nq;
+                const int64_t o = (p % a.slots) * (a.nkv * D) + g * D;
+                kc[o + j] = lo;
+                kc[o + j + half] = hi;
+                if (vc) {
+                    const raw *vr = v + t * a.ldv + g * D;
+                    vc[o + j] = vr[j];
+                    vc[o + j + half] = vr[j + half];
+                }
+            }
+        }
+    }
+
+    template <class S>
+    void launch_qk_t(mg_ctx *c, void *q, void *k, const void *v, const QkArgs &a, double qk_scale, const void *co,
+                     const void *si, const int64_t *pos, void *kc, void *vc)
+    {
+        using raw = typename S::raw;
+        using comp = typename S::comp;
+        constexpr int V16 = 16 / sizeof(raw);
+        const bool vec = a.D % V16 == 0 && a.ldq % V16 == 0 && (a.nkv == 0 || a.ldk % V16 == 0) &&
+                         aligned16(q) && (a.nkv == 0 || aligned16(k));
+        const int64_t rows = a.T * (a.nq + a.nkv);
+        const unsigned blocks = unsigned((rows + kQkRows - 1) / kQkRows);
+        const size_t smem = kQkRows * sizeof(double) + size_t(kQkRows) * a.D * sizeof(raw);
+        // python-float scalar: an f32 value outside f64 (src/muse_glimmer.hpp:772)
+        const comp qs = comp(S::dt == F64 ? qk_scale : double(float(qk_scale)));
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), smem, c->stream, static_cast<raw *>(q),
+                               static_cast<raw *>(k), static_cast<const raw *>(v), a, qs,
+                               static_cast<const raw *>(co), static_cast<const raw *>(si), pos,
+                               static_cast<raw *>(kc), static_cast<raw *>(vc));
+        };
+        if (vec)
+            go(k_qk_norm_rope<S, V16>);
+        else
+            go(k_qk_norm_rope<S, 1>);
+        check_launch("k_qk_norm_rope");
+    }
+
+    void launch_qk_norm_rope(mg_ctx *c, void *q, int64_t nq, int64_t ldq, void *k, int64_t nkv, int64_t ldk,
+                             int64_t T, int64_t D, double eps, double qk_scale, const void *co, const void *si,
+                             int64_t table_rows, const int64_t *pos, int64_t pos0, const void *v, int64_t ldv,
+                             void *kc, void *vc, int64_t slots, int dt)
+    {
+        need(D > 0 && D % 2 == 0 && D <= 512, "qk_norm_rope: head_dim must be even and <= 512");
+        need(T >= 0 && nq >= 0 && nkv >= 0, "qk_norm_rope: bad shape");
+        need(q != nullptr || nq == 0, "qk_norm_rope: q is NULL");
+        need(k != nullptr || nkv == 0, "qk_norm_rope: k is NULL");
+        need((co == nullptr) == (si == nullptr), "qk_norm_rope: give both cos and sin, or neither");
+        need(co == nullptr || table_rows > 0, "qk_norm_rope: empty rope table");
+        need(vc == nullptr || (kc != nullptr && v != nullptr), "qk_norm_rope: v_cache needs k_cache and v");
+        need(kc == nullptr || slots > 0, "qk_norm_rope: cache_slots must be > 0");
+        if (ldq == 0) ldq = nq * D;
+        if (ldk == 0) ldk = nkv * D;
+        if (ldv == 0) ldv = nkv * D;
+        need(ldq >= nq * D && ldk >= nkv * D && (v == nullptr || ldv >= nkv * D),
+             "qk_norm_rope: token stride smaller than heads*head_dim");
+        if (T == 0 || nq + nkv == 0) return;
+        QkArgs a{nq, nkv, ldq, ldk, ldv, T, table_rows, pos0, slots > 0 ? slots : 1, int(D), eps};
+        switch (dt) {
+        case BF16: launch_qk_t<SBf16>(c, q, k, v, a, qk_scale, co, si, pos, kc, vc); break;
+        case F16: launch_qk_t<SF16>(c, q, k, v, a, qk_scale, co, si, pos, kc, vc); break;
+        case F32: launch_qk_t<SF32>(c, q, k, v, a, qk_scale, co, si, pos, kc, vc); break;
+        case F64: launch_qk_t<SF64>(c, q, k, v, a, qk_scale, co, si, pos, kc, vc); break;
+        default: fail("qk_norm_rope: unknown dtype " + std::to_string(dt));
+        }
+    }
+} // namespace mg

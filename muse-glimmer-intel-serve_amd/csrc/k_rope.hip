@@ -66,24 +66,6 @@ namespace mg
         check_launch("k_rope_table");
     }
 
-    template <class S>
-    MG_DEV void rope_pair(typename S::raw &lo, typename S::raw &hi, typename S::raw c, typename S::raw s)
-    {
-        if (S::dt == F64) {
-            const double l = double(S::dec(lo)), h = double(S::dec(hi));
-            const double cc = double(S::dec(c)), ss = double(S::dec(s));
-            lo = S::enc64(l * cc - h * ss);
-            hi = S::enc64(h * cc + l * ss);
-        } else {
-            const float l = float(S::dec(lo)), h = float(S::dec(hi));
-            const float cc = float(S::dec(c)), ss = float(S::dec(s));
-            const float a = float(S::dec(S::enc32(l * cc))), b = float(S::dec(S::enc32(-(h * ss))));
-            const float d = float(S::dec(S::enc32(h * cc))), e = float(S::dec(S::enc32(l * ss)));
-            lo = S::enc32(a + b);
-            hi = S::enc32(d + e);
-        }
-    }
-
     // One thread per VEC consecutive j of one (token, head). Positions outside
     // [0, table_rows) leave that head unchanged (no out-of-table read).
     template <class S, int VEC>

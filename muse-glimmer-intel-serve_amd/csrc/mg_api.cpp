@@ -189,6 +189,20 @@ int mg_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k, int64_t
     });
 }
 
+int mg_qk_norm_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k, int64_t k_heads,
+                    int64_t ldk, int64_t tokens, int64_t head_dim, double eps, double qk_scale,
+                    const void *cos_t, const void *sin_t, int64_t table_rows, const int64_t *positions,
+                    int64_t pos0, const void *v, int64_t ldv, void *k_cache, void *v_cache,
+                    int64_t cache_slots, int dtype)
+{
+    MG_GUARD(-1, {
+        mg::launch_qk_norm_rope(ctx_of(ctx), q, q_heads, ldq, k, k_heads, ldk, tokens, head_dim, eps, qk_scale,
+                                cos_t, sin_t, table_rows, positions, pos0, v, ldv, k_cache, v_cache,
+                                cache_slots, dtype);
+        return 0;
+    });
+}
+
 int mg_softmax_rows(mg_ctx *ctx, const void *x, void *y, int64_t heads, int64_t q_rows,
                     int64_t k_cols, double scale, int mask, int64_t window, int64_t q_pos0,
                     double softcap, int dtype_in, int dtype_out)

@@ -143,6 +143,29 @@ namespace mg
             *reinterpret_cast<Vec<T, N> *>(p) = v;
     }
 
+    // RoPE rotate-half of one (lo, hi) pair (reference apply_rope,
+    // src/muse_glimmer.hpp:681-705): x[j] = rnd(rnd(lo*c) + rnd(-hi*s)),
+    // x[j+half] = rnd(rnd(hi*c) + rnd(lo*s)); for 16-bit and f32 storage the
+    // products and sums of stored values in f32 equal the twin's f64 ones
+    // rounded to storage, for f64 the plain f64 expression.
+    template <class S>
+    MG_DEV void rope_pair(typename S::raw &lo, typename S::raw &hi, typename S::raw c, typename S::raw s)
+    {
+        if (S::dt == F64) {
+            const double l = double(S::dec(lo)), h = double(S::dec(hi));
+            const double cc = double(S::dec(c)), ss = double(S::dec(s));
+            lo = S::enc64(l * cc - h * ss);
+            hi = S::enc64(h * cc + l * ss);
+        } else {
+            const float l = float(S::dec(lo)), h = float(S::dec(hi));
+            const float cc = float(S::dec(c)), ss = float(S::dec(s));
+            const float a = float(S::dec(S::enc32(l * cc))), b = float(S::dec(S::enc32(-(h * ss))));
+            const float d = float(S::dec(S::enc32(h * cc))), e = float(S::dec(S::enc32(l * ss)));
+            lo = S::enc32(a + b);
+            hi = S::enc32(d + e);
+        }
+    }
+
     // -------------------------------------------------------- wave64 reductions
     template <typename T>
     MG_DEV T wave_sum(T v)

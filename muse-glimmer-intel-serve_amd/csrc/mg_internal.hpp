@@ -60,6 +60,10 @@ namespace mg
     // k_rope.hip
     void launch_rope_table(mg_ctx *c, double theta, int64_t dim, int64_t T, int dt, void *co,
                            void *si);
+    void launch_qk_norm_rope(mg_ctx *c, void *q, int64_t nq, int64_t ldq, void *k, int64_t nkv, int64_t ldk,
+                             int64_t T, int64_t D, double eps, double qk_scale, const void *co, const void *si,
+                             int64_t table_rows, const int64_t *pos, int64_t pos0, const void *v, int64_t ldv,
+                             void *kc, void *vc, int64_t slots, int dt);
     void launch_rope(mg_ctx *c, void *q, int64_t qh, int64_t ldq, void *k, int64_t kh,
                      int64_t ldk, int64_t tokens, int64_t dim, const void *co, const void *si,
                      int64_t table_rows, const int64_t *pos, int64_t pos0, int dt);

@@ -49,6 +49,8 @@ _SIGS = {
     "mg_scale": ([_P, _P, _I, _D, _INT], _INT),
     "mg_rope_table": ([_P, _D, _I, _I, _INT, _P, _P], _INT),
     "mg_rope": ([_P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _INT], _INT),
+    "mg_qk_norm_rope": ([_P, _P, _I, _I, _P, _I, _I, _I, _I, _D, _D, _P, _P, _I, _P, _I, _P, _I, _P, _P, _I, _INT],
+                        _INT),
     "mg_softmax_rows": ([_P, _P, _P, _I, _I, _I, _D, _INT, _I, _I, _D, _INT, _INT], _INT),
     "mg_softcap": ([_P, _P, _I, _D, _D, _INT], _INT),
     "mg_dequant_q8_0": ([_P, _P, _P, _P, _I, _I, _INT], _INT),
@@ -173,6 +175,19 @@ class Prims:
         self._check(self.lib.mg_rope(self.h, _ptr(q), qh, q.stride(0), _ptr(k), kh,
                                      k.stride(0) if k is not None else 0, T, D, _ptr(cos), _ptr(sin),
                                      cos.shape[0], _ptr(positions), pos0, _dtype_code(q)))
+
+    def qk_norm_rope(self, q, k, eps, qk_scale, cos=None, sin=None, positions=None, pos0=0, v=None,
+                     k_cache=None, v_cache=None):
+        """The sequence around RoPE in one pass (src/muse_glimmer.hpp:799-819): weight-less
+        QK-norm over head_dim, q *= qk_scale, RoPE (when a table is given), and the KV-cache
+        append k_cache/v_cache [slots, Hk, D] at row position % slots (k_kv_append)."""
+        T, qh, D = q.shape
+        kh = k.shape[1] if k is not None else 0
+        slots = k_cache.shape[0] if k_cache is not None else 0
+        self._check(self.lib.mg_qk_norm_rope(
+            self.h, _ptr(q), qh, q.stride(0), _ptr(k), kh, k.stride(0) if k is not None else 0, T, D, eps,
+            qk_scale, _ptr(cos), _ptr(sin), cos.shape[0] if cos is not None else 0, _ptr(positions), pos0,
+            _ptr(v), v.stride(0) if v is not None else 0, _ptr(k_cache), _ptr(v_cache), slots, _dtype_code(q)))
 
     # ------------------------------------------------------------ softmax
     def softmax_rows(self, x, y, scale, mask=MASK_NONE, window=0, q_pos0=0, softcap=0.0):

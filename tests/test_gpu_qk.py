@@ -1,0 +1,110 @@
+"""GPU parity: fused QK-norm + qk-scale + RoPE + KV-cache append.
+
+Reference: the sequence of src/muse_glimmer.hpp:799-819 (weight-less
+rmsnorm_rows over head_dim for q and k, q *= qk_scale, apply_rope over
+(t, head)) and the cache append of k_kv_append (src/gpu/gpu_engine.cpp:481-492,
+slot = position % slots). The oracle runs the same steps one after another;
+the fused kernel must match it bit for bit in every dtype.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from util import BF16, F16, F32, F64, from_dev, same_bits, storage, to_dev
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+QK = 3.87
+
+
+def oracle_seq(q, k, dt, theta, dim, table_T, pos, use_rope):
+    T, qh, _ = q.shape
+    kh = k.shape[1]
+    rq = O.rmsnorm_rows(O.WEIGHTLESS, q.reshape(T * qh, dim), None, EPS, dt).reshape(q.shape)
+    rk = O.rmsnorm_rows(O.WEIGHTLESS, k.reshape(T * kh, dim), None, EPS, dt).reshape(k.shape)
+    rq = O.scale(rq, QK, dt)
+    if use_rope:
+        rc, rs = O.rope_table(theta, dim, table_T, dt)
+        rq = O.apply_rope(rq, rc, rs, pos, dt)
+        rk = O.apply_rope(rk, rc, rs, pos, dt)
+    return rq, rk
+
+
+def run_case(prims, dt, T, qh, kh, dim, theta=1e6, pos0=0, positions=None, table_T=None, use_rope=True,
+             slots=0, with_v=True):
+    import torch
+    table_T = table_T or (pos0 + T)
+    qs, q = storage(31, (T, qh, dim), dt)
+    ks, k = storage(32, (T, kh, dim), dt)
+    vs, v = storage(33, (T, kh, dim), dt)
+    dq, dk, dv = to_dev(qs, dt), to_dev(ks, dt), to_dev(vs, dt)
+    dco = dsi = None
+    if use_rope:
+        rc, rs = O.rope_table(theta, dim, table_T, dt)
+        dco, dsi = to_dev(O.from_f64(rc, dt), dt), to_dev(O.from_f64(rs, dt), dt)
+    dpos = None
+    if positions is not None:
+        pos = np.asarray(positions, np.int64)
+        dpos = torch.from_numpy(pos).to("cuda:0")
+    else:
+        pos = np.arange(pos0, pos0 + T, dtype=np.int64)
+    kc = vc = None
+    cache0 = None
+    if slots:
+        cache0 = O.from_f64(np.full((slots, kh, dim), 0.25), dt)
+        kc, vc = to_dev(cache0, dt), to_dev(cache0, dt)
+        if not with_v:
+            vc = None
+    prims.qk_norm_rope(dq, dk, EPS, QK, dco, dsi, dpos, pos0, dv if with_v else None, kc, vc)
+    rq, rk = oracle_seq(q, k, dt, theta, dim, table_T, pos, use_rope)
+    assert same_bits(from_dev(dq, dt), O.from_f64(rq, dt))
+    assert same_bits(from_dev(dk, dt), O.from_f64(rk, dt))
+    if slots:
+        ek = O.to_f64(cache0, dt).copy()
+        ev = O.to_f64(cache0, dt).copy()
+        for t in range(T):  # later tokens overwrite earlier ones in the ring, as sequential appends do
+            if pos[t] >= 0:
+                ek[pos[t] % slots] = rk[t]
+                ev[pos[t] % slots] = v[t]
+        assert same_bits(from_dev(kc, dt), O.from_f64(ek, dt))
+        if with_v:
+            assert same_bits(from_dev(vc, dt), O.from_f64(ev, dt))
+
+
+@pytest.mark.parametrize("dt", (BF16, F16, F32, F64))
+def test_sequence_bitwise(prims, dt):
+    run_case(prims, dt, 65, 40, 8, 128, pos0=7, slots=128)
+
+
+def test_prefill_shape_bf16(prims):
+    """config-3 shapes: q [4096, 40, 128], k [4096, 8, 128], theta 1e6, positions 0..4095"""
+    run_case(prims, BF16, 4096, 40, 8, 128, slots=4096)
+
+
+def test_nope_layer_and_no_cache(prims):
+    run_case(prims, BF16, 33, 40, 8, 128, use_rope=False)
+
+
+def test_positions_array_ring_wrap(prims):
+    """explicit positions wrapping a ring of 16 slots (distinct slots: two
+    tokens of one call on one slot would race, as in the reference), no v"""
+    pos = [3, 40, 17, 1002, 2, 31, 604, 5]
+    run_case(prims, BF16, len(pos), 32, 4, 128, theta=5e5, positions=pos, table_T=2048, slots=16,
+             with_v=False)
+
+
+def test_odd_shapes(prims):
+    """head_dim 64 (theta 1e4), one kv head, a single token"""
+    run_case(prims, BF16, 1, 3, 1, 64, theta=1e4, pos0=99, slots=8)
+    run_case(prims, F32, 5, 2, 2, 18, theta=1e4, pos0=3, slots=7)  # half = 9, scalar staging
+
+
+def test_errors(prims):
+    import torch
+    q = torch.zeros((2, 4, 128), dtype=torch.bfloat16, device="cuda:0")
+    k = torch.zeros((2, 1, 128), dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(Exception, match="head_dim"):
+        prims.qk_norm_rope(q[:, :, :127], k[:, :, :127], EPS, QK)
+    with pytest.raises(Exception, match="v_cache"):
+        prims.qk_norm_rope(q, k, EPS, QK, v_cache=k)
