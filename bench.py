@@ -57,6 +57,7 @@ BYTES = {
     "softmax_decode": SM_H * DEC_K * (4 + 2),
     "dequant_q8_0": Q8_R * Q8_C + Q8_R * (Q8_C // 32) * 2 + Q8_R * Q8_C * 2,
     "vocab_lse_argmax_top64": V_ROWS * VOCAB * 4 + V_ROWS * (8 + 8) + V_ROWS * TOPK * (8 + 4),
+    "vocab_tail_top64_dist": V_ROWS * VOCAB * 4 + V_ROWS * (8 + 8) + V_ROWS * TOPK * (8 + 4) * 2,
     # q, k read + written, v read, k/v cache rows written, cos/sin read
     "qk_norm_rope_kv": 2 * (2 * T * Q_H * HD + 2 * T * K_H * HD) + 2 * T * K_H * HD + 2 * 2 * T * K_H * HD
                        + 2 * 2 * T * (HD // 2),
@@ -67,10 +68,11 @@ KERNEL_OF = {
     "swiglu": "k_gate_lut",
     "softmax_causal": "k_softmax_fast",
     "rope": "k_rope",
-    "softmax_decode": "k_softmax_partial + k_softmax_finish",
+    "softmax_decode": "k_softmax_partial_fast + k_softmax_finish_fast",
     "dequant_q8_0": "k_dequant_q8_0",
     "vocab_lse_argmax_top64": "k_vocab_chunk + k_vocab_merge",
     "qk_norm_rope_kv": "k_qk_norm_rope",
+    "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
 }
 
 
@@ -132,6 +134,12 @@ def make_inputs(torch, P):
     torch.cuda.synchronize()
 
     scale = 1.0 / math.sqrt(HD)
+
+    def tail_dist():
+        # output tail (cap 30) fused into the vocab pass, then the sampler's distribution
+        _, am, ti, tv = P.vocab_reduce_tail(I["logits"], 1.0, 30.0, TOPK)
+        return P.sample_dist(ti, tv, am, 0.7, 0.95, 0.0)
+
     ops = {
         "residual_rmsnorm": lambda: P.residual_rmsnorm(M.PLAIN, I["h"], I["x"], I["w"], 1e-6, I["y"]),
         "swiglu": lambda: P.swiglu(I["gate"], I["up"], I["act"]),
@@ -140,6 +148,7 @@ def make_inputs(torch, P):
         "softmax_decode": lambda: P.softmax_rows(I["dscores"], I["dprobs"], scale, M.MASK_CAUSAL, 0, DEC_K - 1),
         "dequant_q8_0": lambda: P.dequant_q8_0(I["qs"], I["qd"], I["deq"]),
         "vocab_lse_argmax_top64": lambda: P.vocab_reduce(I["logits"], TOPK, I["lse"], I["amax"], I["tidx"], I["tval"]),
+        "vocab_tail_top64_dist": lambda: tail_dist(),
         "qk_norm_rope_kv": lambda: P.qk_norm_rope(I["q"], I["k"], 1e-6, 3.87, I["cos"], I["sin"], None, 0, I["v"],
                                                   I["kcache"], I["vcache"]),
     }

@@ -166,6 +166,31 @@ int mg_dequant_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, void *out,
 int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, int dtype_in,
                     int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val);
 
+/* The output tail fused into the vocab pass: every logit first becomes
+ * apply_output_tail's value (z = rnd(z*mult); z = rnd(cap*rnd(tanh(rnd(z/cap)))),
+ * rounded to dtype_in at each step, FDLIBM tanh; src/muse_glimmer.hpp:920-943,
+ * GPU k_softcap src/gpu/gpu_engine.cpp:1906-1919), then lse / argmax / top-K are
+ * taken over the transformed logits exactly as mg_vocab_reduce does; top_val
+ * holds transformed values. logits_out (optional, [rows, V] at dtype_in)
+ * receives the transformed logits; the input is not modified. */
+int mg_vocab_reduce_tail(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, int dtype_in, double mult,
+                         double cap, int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val,
+                         void *logits_out);
+
+/* The sampler's final candidate distribution from a vocab pass's output
+ * (serve/sampler.py:43-112, Sampler._transformed / dist after the logit edits):
+ * top_idx/top_val [rows, K] sorted as mg_vocab_reduce writes them (K = the
+ * sampler's top_k, 1..256), argmax [rows]. Per row: -inf candidates dropped;
+ * none left, or temperature <= 0, gives the point mass on argmax; otherwise
+ * probs = softmax(values), top_p < 1 keeps the first searchsorted(cumsum, top_p)+1,
+ * min_p > 0 keeps probs >= min_p*max(probs), and the kept candidates get
+ * softmax(values / temperature). Writes cand_count[r] candidates, in order, to
+ * cand_ids/cand_probs [rows, K]. Probabilities match the reference's numpy
+ * float32 arithmetic to a few ulp (f32 exp, f64 sums). */
+int mg_sample_dist(mg_ctx *ctx, const int64_t *top_idx, const float *top_val, const int64_t *argmax, int64_t rows,
+                   int64_t K, double temperature, double top_p, double min_p, int64_t *cand_ids, float *cand_probs,
+                   int64_t *cand_count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,8 +43,9 @@ namespace mg
         using raw = typename S::raw;
         extern __shared__ double smem_d[];
         double *rsq = smem_d;                                 // [kQkRows]
-        raw *st = reinterpret_cast<raw *>(smem_d + kQkRows); // [kQkRows][D]
+        raw *st = reinterpret_cast<raw *>(smem_d + kQkRows); // [kQkRows][SD]
         const int D = a.D, half = D / 2;
+        const int SD = D + 16 / int(sizeof(raw)); // row stride: 16 bytes of padding against bank conflicts
         const int64_t heads = a.nq + a.nkv, rows = a.T * heads;
         const int64_t r0 = int64_t(blockIdx.x) * kQkRows;
         const int nr = int(rows - r0 < kQkRows ? rows - r0 : kQkRows);
@@ -57,7 +58,7 @@ namespace mg
         const int vpr = D / VEC;
         for (int idx = threadIdx.x; idx < nr * vpr; idx += blockDim.x) {
             const int rr = idx / vpr, i = (idx - rr * vpr) * VEC;
-            *reinterpret_cast<Vec<raw, VEC> *>(st + rr * D + i) = *reinterpret_cast<const Vec<raw, VEC> *>(row_ptr(r0 + rr) + i);
+            *reinterpret_cast<Vec<raw, VEC> *>(st + rr * SD + i) = *reinterpret_cast<const Vec<raw, VEC> *>(row_ptr(r0 + rr) + i);
         }
         __syncthreads();
 
@@ -69,7 +70,7 @@ namespace mg
             double acc = 0.0;
             if (rr < nr)
                 for (int i = l; i < full; i += 8) {
-                    const double x = double(S::dec(st[rr * D + i]));
+                    const double x = double(S::dec(st[rr * SD + i]));
                     acc += x * x;
                 }
             const double s1 = acc + __shfl_xor(acc, 1, 64);
@@ -78,7 +79,7 @@ namespace mg
             if (rr < nr && l == 0) {
                 double tail = 0.0;
                 for (int i = full; i < D; ++i) {
-                    const double x = double(S::dec(st[rr * D + i]));
+                    const double x = double(S::dec(st[rr * SD + i]));
                     tail += x * x;
                 }
                 rsq[rr] = 1.0 / __builtin_sqrt((s3 + tail) / double(D) + a.eps);
@@ -86,14 +87,61 @@ namespace mg
         }
         __syncthreads();
 
-        // (lo, hi) pairs: normalize, scale q, rotate, store, append
+        // (lo, hi) pairs, VEC at a time when the halves allow 16-byte
+        // accesses: normalize, scale q, rotate, store, append
+        constexpr int PV = VEC;
+        const int npv = half % PV == 0 ? half / PV : 0;
+        if (npv) {
+            for (int idx = threadIdx.x; idx < nr * npv; idx += blockDim.x) {
+                const int rr = idx / npv, j = (idx - rr * npv) * PV;
+                const int64_t r = r0 + rr, t = r / heads, hh = r - t * heads;
+                const bool isq = hh < a.nq;
+                const double rs = rsq[rr];
+                Vec<raw, PV> lo = *reinterpret_cast<const Vec<raw, PV> *>(st + rr * SD + j);
+                Vec<raw, PV> hi = *reinterpret_cast<const Vec<raw, PV> *>(st + rr * SD + j + half);
+                const int64_t p = pos ? pos[t] : a.pos0 + t;
+                const bool rot = co && p >= 0 && p < a.table_rows;
+                Vec<raw, PV> cv, sv;
+                if (rot) {
+                    cv = *reinterpret_cast<const Vec<raw, PV> *>(co + p * half + j);
+                    sv = *reinterpret_cast<const Vec<raw, PV> *>(si + p * half + j);
+                }
+#pragma unroll
+                for (int e = 0; e < PV; ++e) {
+                    raw l = S::enc64(double(S::dec(lo.v[e])) * rs);
+                    raw h = S::enc64(double(S::dec(hi.v[e])) * rs);
+                    if (isq) {
+                        l = S::enc(S::dec(l) * qs);
+                        h = S::enc(S::dec(h) * qs);
+                    }
+                    if (rot) rope_pair<S>(l, h, cv.v[e], sv.v[e]);
+                    lo.v[e] = l;
+                    hi.v[e] = h;
+                }
+                raw *dst = row_ptr(r);
+                stv<raw, PV>(dst + j, lo);
+                stv<raw, PV>(dst + j + half, hi);
+                if (!isq && kc && p >= 0) {
+                    const int64_t g = hh - a.nq;
+                    const int64_t o = (p % a.slots) * (a.nkv * D) + g * D;
+                    stv<raw, PV>(kc + o + j, lo);
+                    stv<raw, PV>(kc + o + j + half, hi);
+                    if (vc) {
+                        const raw *vr = v + t * a.ldv + g * D;
+                        stv<raw, PV>(vc + o + j, ldv<raw, PV>(vr + j));
+                        stv<raw, PV>(vc + o + j + half, ldv<raw, PV>(vr + j + half));
+                    }
+                }
+            }
+            return;
+        }
         for (int idx = threadIdx.x; idx < nr * half; idx += blockDim.x) {
             const int rr = idx / half, j = idx - rr * half;
             const int64_t r = r0 + rr, t = r / heads, hh = r - t * heads;
             const bool isq = hh < a.nq;
             const double rs = rsq[rr];
-            raw lo = S::enc64(double(S::dec(st[rr * D + j])) * rs);
-            raw hi = S::enc64(double(S::dec(st[rr * D + j + half])) * rs);
+            raw lo = S::enc64(double(S::dec(st[rr * SD + j])) * rs);
+            raw hi = S::enc64(double(S::dec(st[rr * SD + j + half])) * rs);
             if (isq) {
                 lo = S::enc(S::dec(lo) * qs);
                 hi = S::enc(S::dec(hi) * qs);
@@ -125,10 +173,11 @@ namespace mg
         using comp = typename S::comp;
         constexpr int V16 = 16 / sizeof(raw);
         const bool vec = a.D % V16 == 0 && a.ldq % V16 == 0 && (a.nkv == 0 || a.ldk % V16 == 0) &&
-                         aligned16(q) && (a.nkv == 0 || aligned16(k));
+                         aligned16(q) && (a.nkv == 0 || aligned16(k)) && (!co || (aligned16(co) && aligned16(si))) &&
+                         (!kc || aligned16(kc)) && (!vc || (aligned16(vc) && aligned16(v) && a.ldv % V16 == 0));
         const int64_t rows = a.T * (a.nq + a.nkv);
         const unsigned blocks = unsigned((rows + kQkRows - 1) / kQkRows);
-        const size_t smem = kQkRows * sizeof(double) + size_t(kQkRows) * a.D * sizeof(raw);
+        const size_t smem = kQkRows * sizeof(double) + size_t(kQkRows) * (a.D * sizeof(raw) + 16);
         // python-float scalar: an f32 value outside f64 (src/muse_glimmer.hpp:772)
         const comp qs = comp(S::dt == F64 ? qk_scale : double(float(qk_scale)));
         auto go = [&](auto kern) {

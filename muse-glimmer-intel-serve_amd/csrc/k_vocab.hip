@@ -58,6 +58,28 @@ namespace mg
         int32_t pad;
     };
 
+    // apply_output_tail (src/muse_glimmer.hpp:920-943) on one stored logit:
+    // z*mult, z/cap, tanh, z*cap, each rounded to the logits' storage format,
+    // FDLIBM tanh in f64 — the twin's values, bit for bit (mult 1 / cap 0 skip
+    // their steps). Optionally written back in storage format.
+    struct VTail
+    {
+        double mult, cap;
+        void *out;
+    };
+    template <class SI>
+    MG_DEV float vtail(float x, const VTail &t)
+    {
+        double v = double(x);
+        if (t.mult != 1.0) v = double(SI::dec(SI::enc64(v * t.mult)));
+        if (t.cap != 0.0) {
+            v = double(SI::dec(SI::enc64(v / t.cap)));
+            v = double(SI::dec(SI::enc64(mgm::tanh(v))));
+            v = double(SI::dec(SI::enc64(v * t.cap)));
+        }
+        return float(v);
+    }
+
     // order-preserving 32-bit image of a logit: NaN lowest (1, below -inf's
     // 0x007fffff), -0 == +0; 0 marks an empty slot
     MG_DEV uint32_t vhi(float x)
@@ -226,10 +248,11 @@ namespace mg
         return (uint64_t(th) << 32) | lw;
     }
 
-    template <class SI, int VW, int SL>
+    template <class SI, int VW, int SL, bool TAIL>
     __global__ __launch_bounds__(256) void k_vocab_chunk(const typename SI::raw *__restrict__ L, int64_t V, int K,
                                                          int nch, VPart *__restrict__ part,
-                                                         uint64_t *__restrict__ blk, uint64_t *__restrict__ lst)
+                                                         uint64_t *__restrict__ blk, uint64_t *__restrict__ lst,
+                                                         VTail tail)
     {
         using raw = typename SI::raw;
         constexpr int CAP = 64 * SL; // list capacity
@@ -269,6 +292,35 @@ namespace mg
             for (int s = 0; s < kVLane; ++s) {
                 const int o = voff<VW>(lane, s);
                 xb[s] = __builtin_bit_cast(uint32_t, o < nvalid ? float(SI::dec(xr[o])) : -__builtin_huge_valf());
+            }
+        }
+
+        if constexpr (TAIL) {
+#pragma unroll
+            for (int s = 0; s < kVLane; ++s)
+                if (full || voff<VW>(lane, s) < nvalid) xb[s] = __builtin_bit_cast(uint32_t, vtail<SI>(x(s), tail));
+            if (tail.out) {
+                raw *orow = static_cast<raw *>(tail.out) + row * V + cb;
+                bool stored = false;
+                if constexpr (VW > 1) {
+                    if (full) {
+#pragma unroll
+                        for (int i = 0; i < kVLane / VW; ++i) {
+                            Vec<raw, VW> w;
+#pragma unroll
+                            for (int e = 0; e < VW; ++e) w.v[e] = SI::enc32(x(VW * i + e));
+                            st16_stream<raw, VW>(orow + VW * lane + 64 * VW * i, w);
+                        }
+                        stored = true;
+                    }
+                }
+                if (!stored) {
+#pragma unroll
+                    for (int s = 0; s < kVLane; ++s) {
+                        const int o = voff<VW>(lane, s);
+                        if (o < nvalid) orow[o] = SI::enc32(x(s));
+                    }
+                }
             }
         }
 
@@ -464,12 +516,12 @@ namespace mg
         return (uint64_t(th) << 32) | lw;
     }
 
-    template <class SI, int SL>
+    template <class SI, int SL, bool TAIL>
     __global__ __launch_bounds__(64) void k_vocab_merge(const typename SI::raw *__restrict__ L, int64_t V, int K,
                                                         int nch, int cap, const VPart *__restrict__ part,
                                                         const uint64_t *__restrict__ blk,
                                                         const uint64_t *__restrict__ lst, double *lse,
-                                                        int64_t *amax, int64_t *top_idx, float *top_val)
+                                                        int64_t *amax, int64_t *top_idx, float *top_val, VTail tail)
     {
         __shared__ uint64_t sel[64 * SL];
         __shared__ __align__(16) uint32_t hist[256];
@@ -478,7 +530,8 @@ namespace mg
         const VPart *pr = part + row * nch;
         const uint64_t *bk = blk + row * nch * int64_t(kBlk);
         const uint64_t *ls = lst + row * nch * int64_t(cap);
-        const float x0 = float(SI::dec(L[row * V]));
+        float x0 = float(SI::dec(L[row * V]));
+        if constexpr (TAIL) x0 = vtail<SI>(x0, tail);
         const bool want_top = top_idx || top_val;
         const int D = K < kBlk ? K : kBlk;
         const bool regs = want_top && nch * D <= 64 * kMergeRegs;
@@ -587,13 +640,19 @@ namespace mg
                 const uint32_t j = vkey_index(a[q]);
                 const bool ok = a[q] != 0 && int64_t(j) < V;
                 if (top_idx) top_idx[row * K + i] = ok ? int64_t(j) : -1;
-                if (top_val) top_val[row * K + i] = ok ? float(SI::dec(L[row * V + j])) : -__builtin_huge_valf();
+                float tv = -__builtin_huge_valf();
+                if (ok) {
+                    tv = float(SI::dec(L[row * V + j]));
+                    if constexpr (TAIL) tv = vtail<SI>(tv, tail);
+                }
+                if (top_val) top_val[row * K + i] = tv;
             }
         }
     }
 
     void launch_vocab(mg_ctx *c, const void *logits, int64_t rows, int64_t V, int dt_in, int64_t K,
-                      double *lse, int64_t *amax, int64_t *top_idx, float *top_val)
+                      double *lse, int64_t *amax, int64_t *top_idx, float *top_val, bool tail_on, double mult,
+                      double cap, void *logits_out)
     {
         need(rows >= 0 && V > 0, "vocab_reduce: bad shape");
         need(V < (int64_t(1) << 31), "vocab_reduce: V must be < 2^31");
@@ -606,36 +665,44 @@ namespace mg
         if (rows == 0) return;
         const int nch = int((V + kVChunk - 1) / kVChunk);
         const bool small = K <= kFastK;
-        const int cap = small ? 128 : 256;
+        const int lcap = small ? 128 : 256; // list capacity per chunk
         const int64_t nc = rows * nch;
-        const int64_t need_bytes = nc * int64_t(sizeof(VPart) + sizeof(uint64_t) * (kBlk + cap));
+        const int64_t need_bytes = nc * int64_t(sizeof(VPart) + sizeof(uint64_t) * (kBlk + lcap));
         need(need_bytes <= c->work_bytes, "vocab_reduce: partials exceed the context workspace (raise workspace_bytes at mg_open)");
         VPart *part = static_cast<VPart *>(c->work);
         uint64_t *blk = reinterpret_cast<uint64_t *>(part + nc);
         uint64_t *lst = blk + nc * kBlk;
         const dim3 g1{unsigned((nch + 3) / 4), unsigned(rows), 1u};
         const dim3 g2{unsigned(rows), 1u, 1u};
+        // python-float scalars are f32 opmath values outside f64 (src/muse_glimmer.hpp:924-926)
+        const VTail tail{double(float(mult)), double(float(cap)), logits_out};
         auto go = [&](auto chunk, auto merge, const auto *x) {
-            hipLaunchKernelGGL(chunk, g1, dim3(256), 0, c->stream, x, V, int(K), nch, part, blk, lst);
+            hipLaunchKernelGGL(chunk, g1, dim3(256), 0, c->stream, x, V, int(K), nch, part, blk, lst, tail);
             check_launch("k_vocab_chunk");
-            hipLaunchKernelGGL(merge, g2, dim3(64), 0, c->stream, x, V, int(K), nch, cap, part, blk, lst, lse, amax,
-                               top_idx, top_val);
+            hipLaunchKernelGGL(merge, g2, dim3(64), 0, c->stream, x, V, int(K), nch, lcap, part, blk, lst, lse, amax,
+                               top_idx, top_val, tail);
             check_launch("k_vocab_merge");
+        };
+        auto pick = [&](auto si, auto vw, const auto *x) {
+            using SI = decltype(si);
+            constexpr int VW = decltype(vw)::value;
+            if (small && tail_on) go(k_vocab_chunk<SI, VW, 2, true>, k_vocab_merge<SI, 1, true>, x);
+            else if (small) go(k_vocab_chunk<SI, VW, 2, false>, k_vocab_merge<SI, 1, false>, x);
+            else if (tail_on) go(k_vocab_chunk<SI, VW, 4, true>, k_vocab_merge<SI, 4, true>, x);
+            else go(k_vocab_chunk<SI, VW, 4, false>, k_vocab_merge<SI, 4, false>, x);
         };
         if (dt_in == F32) {
             const float *x = static_cast<const float *>(logits);
-            const bool vec = V % 4 == 0 && aligned16(x);
-            if (small && vec) go(k_vocab_chunk<SF32, 4, 2>, k_vocab_merge<SF32, 1>, x);
-            else if (small) go(k_vocab_chunk<SF32, 1, 2>, k_vocab_merge<SF32, 1>, x);
-            else if (vec) go(k_vocab_chunk<SF32, 4, 4>, k_vocab_merge<SF32, 4>, x);
-            else go(k_vocab_chunk<SF32, 1, 4>, k_vocab_merge<SF32, 4>, x);
+            if (V % 4 == 0 && aligned16(x) && (!logits_out || aligned16(logits_out)))
+                pick(SF32{}, std::integral_constant<int, 4>{}, x);
+            else
+                pick(SF32{}, std::integral_constant<int, 1>{}, x);
         } else if (dt_in == BF16) {
             const uint16_t *x = static_cast<const uint16_t *>(logits);
-            const bool vec = V % 8 == 0 && aligned16(x);
-            if (small && vec) go(k_vocab_chunk<SBf16, 8, 2>, k_vocab_merge<SBf16, 1>, x);
-            else if (small) go(k_vocab_chunk<SBf16, 1, 2>, k_vocab_merge<SBf16, 1>, x);
-            else if (vec) go(k_vocab_chunk<SBf16, 8, 4>, k_vocab_merge<SBf16, 4>, x);
-            else go(k_vocab_chunk<SBf16, 1, 4>, k_vocab_merge<SBf16, 4>, x);
+            if (V % 8 == 0 && aligned16(x) && (!logits_out || aligned16(logits_out)))
+                pick(SBf16{}, std::integral_constant<int, 8>{}, x);
+            else
+                pick(SBf16{}, std::integral_constant<int, 1>{}, x);
         } else {
             fail("vocab_reduce: input dtype must be f32 or bf16");
         }

@@ -235,9 +235,32 @@ int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, in
                     int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val)
 {
     MG_GUARD(-1, {
-        mg::launch_vocab(ctx_of(ctx), logits, rows, V, dtype_in, K, lse, argmax, top_idx, top_val);
+        mg::launch_vocab(ctx_of(ctx), logits, rows, V, dtype_in, K, lse, argmax, top_idx, top_val, false, 1.0, 0.0,
+                         nullptr);
+        return 0;
+    });
+}
+
+int mg_vocab_reduce_tail(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, int dtype_in, double mult,
+                         double cap, int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val,
+                         void *logits_out)
+{
+    MG_GUARD(-1, {
+        mg::launch_vocab(ctx_of(ctx), logits, rows, V, dtype_in, K, lse, argmax, top_idx, top_val, true, mult, cap,
+                         logits_out);
         return 0;
     });
 }
 
 } // extern "C"
+
+int mg_sample_dist(mg_ctx *ctx, const int64_t *top_idx, const float *top_val, const int64_t *argmax, int64_t rows,
+                   int64_t K, double temperature, double top_p, double min_p, int64_t *cand_ids, float *cand_probs,
+                   int64_t *cand_count)
+{
+    MG_GUARD(-1, {
+        mg::launch_sample_dist(ctx_of(ctx), top_idx, top_val, argmax, rows, K, temperature, top_p, min_p, cand_ids,
+                               cand_probs, cand_count);
+        return 0;
+    });
+}

@@ -75,6 +75,10 @@ namespace mg
     void launch_dequant_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, void *out,
                              int64_t rows, int64_t in, int dt_out);
     // k_vocab.hip
-    void launch_vocab(mg_ctx *c, const void *logits, int64_t rows, int64_t V, int dt_in,
-                      int64_t K, double *lse, int64_t *amax, int64_t *top_idx, float *top_val);
+    void launch_sample_dist(mg_ctx *c, const int64_t *top_idx, const float *top_val, const int64_t *amax,
+                            int64_t rows, int64_t K, double temperature, double top_p, double min_p,
+                            int64_t *out_ids, float *out_p, int64_t *out_n);
+    void launch_vocab(mg_ctx *c, const void *logits, int64_t rows, int64_t V, int dt_in, int64_t K,
+                      double *lse, int64_t *amax, int64_t *top_idx, float *top_val, bool tail_on, double mult,
+                      double cap, void *logits_out);
 } // namespace mg

@@ -55,6 +55,8 @@ _SIGS = {
     "mg_softcap": ([_P, _P, _I, _D, _D, _INT], _INT),
     "mg_dequant_q8_0": ([_P, _P, _P, _P, _I, _I, _INT], _INT),
     "mg_vocab_reduce": ([_P, _P, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
+    "mg_sample_dist": ([_P, _P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P], _INT),
+    "mg_vocab_reduce_tail": ([_P, _P, _I, _I, _INT, _D, _D, _I, _P, _P, _P, _P, _P], _INT),
 }
 
 _lib = None
@@ -224,4 +226,31 @@ class Prims:
         self._check(self.lib.mg_vocab_reduce(self.h, _ptr(logits), rows, V, _dtype_code(logits), K, _ptr(lse),
                                              _ptr(argmax), _ptr(top_idx) if K > 0 else None,
                                              _ptr(top_val) if K > 0 else None))
+        return lse, argmax, top_idx, top_val
+
+    def sample_dist(self, top_idx, top_val, argmax, temperature, top_p, min_p):
+        """serve/sampler.py's candidate distribution (ids, probs, count per row) from a vocab pass."""
+        import torch
+        rows, K = top_idx.shape
+        ids = torch.full((rows, K), -1, dtype=torch.int64, device=top_idx.device)
+        probs = torch.zeros((rows, K), dtype=torch.float32, device=top_idx.device)
+        n = torch.empty(rows, dtype=torch.int64, device=top_idx.device)
+        self._check(self.lib.mg_sample_dist(self.h, _ptr(top_idx), _ptr(top_val), _ptr(argmax), rows, K, temperature,
+                                            top_p, min_p, _ptr(ids), _ptr(probs), _ptr(n)))
+        return ids, probs, n
+
+    def vocab_reduce_tail(self, logits, mult, cap, K, logits_out=None):
+        """apply_output_tail (src/muse_glimmer.hpp:920-943) fused into the vocab pass:
+        lse / first argmax / top-K over the transformed logits; logits_out, when given,
+        receives them (the input is left as it is)."""
+        import torch
+        rows, V = logits.shape
+        dev = logits.device
+        lse = torch.empty(rows, dtype=torch.float64, device=dev)
+        argmax = torch.empty(rows, dtype=torch.int64, device=dev)
+        top_idx = torch.empty((rows, K), dtype=torch.int64, device=dev)
+        top_val = torch.empty((rows, K), dtype=torch.float32, device=dev)
+        self._check(self.lib.mg_vocab_reduce_tail(self.h, _ptr(logits), rows, V, _dtype_code(logits), mult, cap, K,
+                                                  _ptr(lse), _ptr(argmax), _ptr(top_idx), _ptr(top_val),
+                                                  _ptr(logits_out)))
         return lse, argmax, top_idx, top_val

@@ -205,3 +205,26 @@ def test_vocab_short_tails(prims):
     """last chunk holding 1, 63, 100 and 2047 entries"""
     for V in (2048 * 3 + 1, 2048 + 63, 2048 * 5 + 100, 2048 * 2 + 2047):
         vocab_check(prims, O.normal(23, (3, V), 0.0, 4.0, F32), F32, 64)
+
+
+# ------------------------------------------------------- output tail fused
+@pytest.mark.parametrize("dt,mult,cap,std", ((F32, 1.0, 30.0, 4.0), (F32, 0.5, 30.0, 4.0), (BF16, 1.0, 30.0, 4.0),
+                                             (F32, 1.0, 30.0, 300.0), (BF16, 2.0, 0.0, 4.0)))
+def test_vocab_tail_fused(prims, dt, mult, cap, std):
+    """apply_output_tail in the vocab pass == softcap then vocab_reduce; std 300
+    saturates many logits to cap, so ties (lower index first) decide the top-K"""
+    import torch
+    Ls = O.normal(24, (6, 50000), 0.0, std, dt)
+    L = O.to_f64(Ls, dt)
+    Z = O.softcap(L, mult, cap, dt)
+    dL = to_dev(Ls, dt)
+    out = torch.empty_like(dL)
+    lse, am, ti, tv = prims.vocab_reduce_tail(dL, mult, cap, 64, out)
+    assert same_bits(from_dev(out, dt), O.from_f64(Z, dt))
+    assert same_bits(from_dev(dL, dt), Ls)  # input untouched
+    r_lse, r_am, r_ti, r_tv = O.vocab_reduce(Z, 64)
+    rel = np.abs(lse.cpu().numpy() - r_lse) / np.abs(r_lse)
+    assert rel.max() <= 1e-6
+    assert np.array_equal(am.cpu().numpy(), r_am)
+    assert np.array_equal(ti.cpu().numpy(), r_ti)
+    assert np.array_equal(tv.cpu().numpy().astype(np.float64), r_tv)
