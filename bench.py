@@ -58,6 +58,8 @@ BYTES = {
     "dequant_q8_0": Q8_R * Q8_C + Q8_R * (Q8_C // 32) * 2 + Q8_R * Q8_C * 2,
     "vocab_lse_argmax_top64": V_ROWS * VOCAB * 4 + V_ROWS * (8 + 8) + V_ROWS * TOPK * (8 + 4),
     "vocab_tail_top64_dist": V_ROWS * VOCAB * 4 + V_ROWS * (8 + 8) + V_ROWS * TOPK * (8 + 4) * 2,
+    "quantize_q8_0": Q8_R * Q8_C * 2 + Q8_R * Q8_C + Q8_R * (Q8_C // 32) * 2,
+    "gemv_q8_0_decode": Q8_R * Q8_C + Q8_R * (Q8_C // 32) * 2 + Q8_C * 2 + Q8_R * 4,
     # q, k read + written, v read, k/v cache rows written, cos/sin read
     "qk_norm_rope_kv": 2 * (2 * T * Q_H * HD + 2 * T * K_H * HD) + 2 * T * K_H * HD + 2 * 2 * T * K_H * HD
                        + 2 * 2 * T * (HD // 2),
@@ -72,6 +74,8 @@ KERNEL_OF = {
     "dequant_q8_0": "k_dequant_q8_0",
     "vocab_lse_argmax_top64": "k_vocab_chunk + k_vocab_merge",
     "qk_norm_rope_kv": "k_qk_norm_rope",
+    "quantize_q8_0": "k_quantize_q8_0",
+    "gemv_q8_0_decode": "k_gemv_q8_0<1>",
     "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
 }
 
@@ -125,6 +129,11 @@ def make_inputs(torch, P):
     I["amax"] = torch.empty(V_ROWS, dtype=torch.int64, device=dev)
     I["tidx"] = torch.empty((V_ROWS, TOPK), dtype=torch.int64, device=dev)
     I["tval"] = torch.empty((V_ROWS, TOPK), dtype=torch.float32, device=dev)
+    I["wq"] = randn((Q8_R, Q8_C), 0.0, 0.05)
+    I["qs2"] = torch.empty((Q8_R, Q8_C), dtype=torch.int8, device=dev)
+    I["qd2"] = torch.empty((Q8_R, Q8_C // 32), dtype=torch.int16, device=dev)
+    I["xg"] = randn((1, Q8_C))
+    I["yg"] = torch.empty((1, Q8_R), dtype=torch.float32, device=dev)
     I["v"] = randn((T, K_H, HD))
     I["kcache"] = torch.empty((T, K_H, HD), dtype=bf, device=dev)
     I["vcache"] = torch.empty((T, K_H, HD), dtype=bf, device=dev)
@@ -149,6 +158,8 @@ def make_inputs(torch, P):
         "dequant_q8_0": lambda: P.dequant_q8_0(I["qs"], I["qd"], I["deq"]),
         "vocab_lse_argmax_top64": lambda: P.vocab_reduce(I["logits"], TOPK, I["lse"], I["amax"], I["tidx"], I["tval"]),
         "vocab_tail_top64_dist": lambda: tail_dist(),
+        "quantize_q8_0": lambda: P.quantize_q8_0(I["wq"], I["qs2"], I["qd2"]),
+        "gemv_q8_0_decode": lambda: P.gemv_q8_0(I["qs"], I["qd"], I["xg"], I["yg"]),
         "qk_norm_rope_kv": lambda: P.qk_norm_rope(I["q"], I["k"], 1e-6, 3.87, I["cos"], I["sin"], None, 0, I["v"],
                                                   I["kcache"], I["vcache"]),
     }

@@ -154,6 +154,21 @@ int mg_softcap(mg_ctx *ctx, void *z, int64_t n, double mult, double cap, int dty
 int mg_dequant_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, void *out, int64_t rows,
                     int64_t in, int dtype_out);
 
+/* Q8_0 quantizer, the step before dequant — up_w (src/gpu/gpu_engine.cpp:2722-2755,
+ * llama.cpp's quantize_row_q8_0 rule): w bf16 bits [rows, in] (in % 32 == 0) ->
+ * qs int8 [rows, in] and d f16 bits [rows, in/32]; per 32-block d = amax/127 in
+ * f32 stored as f16 (RNE, subnormals kept), q = lround(x * (d ? 1/d : 0)). */
+int mg_quantize_q8_0(mg_ctx *ctx, const uint16_t *w, int64_t rows, int64_t in, int8_t *qs, uint16_t *d);
+
+/* Q8_0 GEMV, the step after — k_gemv_q8 (src/gpu/gpu_engine.cpp:815-889):
+ * y[b, o] = sum_i w[o, i] * x[b, i] for b < batch (1..8), x bf16 bits
+ * [batch, in] (row stride ldx, 0 = in), y f32 [batch, rows] (row stride ldy,
+ * 0 = rows). blockdot = 0: every weight is bf16(q * d) first (the engine's
+ * default, consistent with a prefill that dequantizes); blockdot = 1:
+ * sum over blocks of d * sum(q * x) (llama.cpp's dot). f32 accumulation. */
+int mg_gemv_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, const uint16_t *x, int64_t batch, int64_t rows,
+                 int64_t in, int64_t ldx, float *y, int64_t ldy, int blockdot);
+
 /* Per row of logits [rows, V] (dtype_in f32 or bf16), one fused pass:
  *   lse[r]     = m + log(sum exp(x - m)) over finite entries, m their max
  *                (serve/sampler.py:168-171); -inf for a row with none

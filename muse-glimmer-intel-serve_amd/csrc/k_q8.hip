@@ -71,6 +71,170 @@ namespace mg
         }
     }
 
+    // ------------------------------------------------------------ quantizer
+    // up_w (src/gpu/gpu_engine.cpp:2722-2755), the llama.cpp quantize_row_q8_0
+    // rule: per 32-block, amax = max |x| over the bf16 values, d = amax / 127
+    // (f32), id = d ? 1/d : 0, the scale stored as f16 (RNE, subnormals kept,
+    // f32_to_f16 at 152-158), q = lround(x * id) (half away from zero). One
+    // lane per block.
+    __global__ __launch_bounds__(256) void k_quantize_q8_0(const uint16_t *__restrict__ w, int8_t *__restrict__ qs,
+                                                           uint16_t *__restrict__ d, int64_t nblk)
+    {
+        const int64_t b = int64_t(blockIdx.x) * 256 + threadIdx.x;
+        if (b >= nblk) return;
+        const uint16_t *src = w + b * 32;
+        float x[32];
+        float amax = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const Vec<uint16_t, 8> v = ld16_stream<uint16_t, 8>(src + 8 * k);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                x[8 * k + e] = bf16_f32(v.v[e]);
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(x[8 * k + e]));
+            }
+        }
+        const float dd = amax / 127.0f;
+        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+        d[b] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(dd));
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            Vec<int8_t, 16> q;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) q.v[e] = int8_t(int(__builtin_roundf(x[16 * k + e] * id)));
+            st16_stream<int8_t, 16>(qs + b * 32 + 16 * k, q);
+        }
+    }
+
+    void launch_quantize_q8_0(mg_ctx *c, const uint16_t *w, int64_t rows, int64_t in, int8_t *qs, uint16_t *d)
+    {
+        need(rows >= 0 && in >= 0, "quantize_q8_0: bad shape");
+        need(in % 32 == 0, "quantize_q8_0: input dim must be a multiple of 32 (got " + std::to_string(in) + ")");
+        need(w && qs && d, "quantize_q8_0: NULL tensor");
+        need(aligned16(w) && aligned16(qs), "quantize_q8_0: weights and quants must be 16-byte aligned");
+        const int64_t nblk = rows * (in / 32);
+        if (nblk == 0) return;
+        hipLaunchKernelGGL(k_quantize_q8_0, dim3(unsigned((nblk + 255) / 256)), dim3(256), 0, c->stream, w, qs, d,
+                           nblk);
+        check_launch("k_quantize_q8_0");
+    }
+
+    // ----------------------------------------------------------- Q8_0 GEMV
+    // y[b, o] = sum_i w[o, i] * x[b, i] over a Q8_0 weight, as k_gemv_q8
+    // (src/gpu/gpu_engine.cpp:815-889) defines it: by default every weight is
+    // first materialized as bf16(q * d) (so decode agrees with a prefill that
+    // dequantizes), with the BLOCKDOT form sum_blocks d * sum(q * x) behind a
+    // flag (llama.cpp's Q8_0 dot). f32 accumulation in both.
+    // One wave per output row, 16 quants (one 16-byte load) per lane and step.
+    // q * d is formed as fma(u, d, -128 d) on the biased byte u = q + 128
+    // (exact, the same rounding as the product), rounded to bf16 in pairs, and
+    // dotted with the bf16 activations by v_dot2_f32_bf16.
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+    template <int B, bool BLOCKDOT>
+    __global__ __launch_bounds__(256) void k_gemv_q8_0(const int8_t *__restrict__ W, const uint16_t *__restrict__ D,
+                                                       const uint16_t *__restrict__ X, float *__restrict__ Y,
+                                                       int64_t in, int64_t out, int64_t ldx, int64_t ldy)
+    {
+        const int64_t o = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+        const int lane = threadIdx.x & 63;
+        if (o >= out) return;
+        const int8_t *w = W + o * in;
+        const uint16_t *dd = D + o * (in / 32);
+        float part[B];
+#pragma unroll
+        for (int bb = 0; bb < B; ++bb) part[bb] = 0.0f;
+        const int64_t nc = in / 16;
+        for (int64_t c = lane; c < nc; c += 64) {
+            const Vec<uint32_t, 4> qv = ld16_stream<uint32_t, 4>(reinterpret_cast<const uint32_t *>(w + 16 * c));
+            const float sc = f16_f32(dd[c >> 1]);
+            if constexpr (!BLOCKDOT) {
+                const float nsc = -128.0f * sc;
+                uint32_t wb[8]; // bf16(q * d) in pairs
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t u = qv.v[k] ^ 0x80808080u; // q + 128 in each byte
+                    const float f0 = __builtin_fmaf(float(u & 0xffu), sc, nsc);
+                    const float f1 = __builtin_fmaf(float((u >> 8) & 0xffu), sc, nsc);
+                    const float f2 = __builtin_fmaf(float((u >> 16) & 0xffu), sc, nsc);
+                    const float f3 = __builtin_fmaf(float(u >> 24), sc, nsc);
+                    wb[2 * k] = uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f0))) |
+                                (uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f1))) << 16);
+                    wb[2 * k + 1] = uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f2))) |
+                                    (uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f3))) << 16);
+                }
+#pragma unroll
+                for (int bb = 0; bb < B; ++bb) {
+                    const uint32_t *xr = reinterpret_cast<const uint32_t *>(X + bb * ldx + 16 * c);
+                    const Vec<uint32_t, 4> x0 = *reinterpret_cast<const Vec<uint32_t, 4> *>(xr);
+                    const Vec<uint32_t, 4> x1 = *reinterpret_cast<const Vec<uint32_t, 4> *>(xr + 4);
+                    float acc = part[bb];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wb[k]),
+                                                              __builtin_bit_cast(bf16x2, x0.v[k]), acc, false);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wb[4 + k]),
+                                                              __builtin_bit_cast(bf16x2, x1.v[k]), acc, false);
+                    part[bb] = acc;
+                }
+            } else {
+                const Vec<int8_t, 16> q = __builtin_bit_cast(Vec<int8_t, 16>, qv);
+#pragma unroll
+                for (int bb = 0; bb < B; ++bb) {
+                    const Vec<uint16_t, 8> x0 = *reinterpret_cast<const Vec<uint16_t, 8> *>(X + bb * ldx + 16 * c);
+                    const Vec<uint16_t, 8> x1 = *reinterpret_cast<const Vec<uint16_t, 8> *>(X + bb * ldx + 16 * c + 8);
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(float(q.v[e]), bf16_f32(x0.v[e]), acc);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(float(q.v[8 + e]), bf16_f32(x1.v[e]), acc);
+                    part[bb] = __builtin_fmaf(acc, sc, part[bb]);
+                }
+            }
+        }
+#pragma unroll
+        for (int bb = 0; bb < B; ++bb) {
+            const float s = dpp_sum_f32(part[bb]);
+            if (lane == 0) Y[bb * ldy + o] = s;
+        }
+    }
+
+    void launch_gemv_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, const uint16_t *x, int64_t batch,
+                          int64_t rows, int64_t in, int64_t ldx, float *y, int64_t ldy, bool blockdot)
+    {
+        need(rows >= 0 && in >= 0 && batch >= 1 && batch <= 8, "gemv_q8_0: batch must be in [1, 8]");
+        need(in % 32 == 0, "gemv_q8_0: input dim must be a multiple of 32 (got " + std::to_string(in) + ")");
+        need(qs && d && x && y, "gemv_q8_0: NULL tensor");
+        if (ldx == 0) ldx = in;
+        if (ldy == 0) ldy = rows;
+        need(ldx >= in && ldy >= rows, "gemv_q8_0: leading dimension too small");
+        need(aligned16(qs) && aligned16(x) && ldx % 8 == 0, "gemv_q8_0: quants and activations must be 16-byte aligned");
+        if (rows == 0) return;
+        const dim3 g{unsigned((rows + 3) / 4), 1u, 1u};
+        // up to four activation rows per pass over the weights
+        for (int64_t b0 = 0; b0 < batch; b0 += 4) {
+            const int nb = int(batch - b0 < 4 ? batch - b0 : 4);
+            const uint16_t *xb = x + b0 * ldx;
+            float *yb = y + b0 * ldy;
+            auto go = [&](auto kern) {
+                hipLaunchKernelGGL(kern, g, dim3(256), 0, c->stream, qs, d, xb, yb, in, rows, ldx, ldy);
+            };
+            switch (nb * 2 + (blockdot ? 1 : 0)) {
+            case 2: go(k_gemv_q8_0<1, false>); break;
+            case 3: go(k_gemv_q8_0<1, true>); break;
+            case 4: go(k_gemv_q8_0<2, false>); break;
+            case 5: go(k_gemv_q8_0<2, true>); break;
+            case 6: go(k_gemv_q8_0<3, false>); break;
+            case 7: go(k_gemv_q8_0<3, true>); break;
+            case 8: go(k_gemv_q8_0<4, false>); break;
+            default: go(k_gemv_q8_0<4, true>); break;
+            }
+        }
+        check_launch("k_gemv_q8_0");
+    }
+
     void launch_dequant_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, void *out,
                              int64_t rows, int64_t in, int dt_out)
     {

@@ -264,3 +264,20 @@ int mg_sample_dist(mg_ctx *ctx, const int64_t *top_idx, const float *top_val, co
         return 0;
     });
 }
+
+int mg_quantize_q8_0(mg_ctx *ctx, const uint16_t *w, int64_t rows, int64_t in, int8_t *qs, uint16_t *d)
+{
+    MG_GUARD(-1, {
+        mg::launch_quantize_q8_0(ctx_of(ctx), w, rows, in, qs, d);
+        return 0;
+    });
+}
+
+int mg_gemv_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, const uint16_t *x, int64_t batch, int64_t rows,
+                 int64_t in, int64_t ldx, float *y, int64_t ldy, int blockdot)
+{
+    MG_GUARD(-1, {
+        mg::launch_gemv_q8_0(ctx_of(ctx), qs, d, x, batch, rows, in, ldx, y, ldy, blockdot != 0);
+        return 0;
+    });
+}

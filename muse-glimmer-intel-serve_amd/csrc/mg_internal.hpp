@@ -78,6 +78,9 @@ namespace mg
     void launch_sample_dist(mg_ctx *c, const int64_t *top_idx, const float *top_val, const int64_t *amax,
                             int64_t rows, int64_t K, double temperature, double top_p, double min_p,
                             int64_t *out_ids, float *out_p, int64_t *out_n);
+    void launch_quantize_q8_0(mg_ctx *c, const uint16_t *w, int64_t rows, int64_t in, int8_t *qs, uint16_t *d);
+    void launch_gemv_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, const uint16_t *x, int64_t batch,
+                          int64_t rows, int64_t in, int64_t ldx, float *y, int64_t ldy, bool blockdot);
     void launch_vocab(mg_ctx *c, const void *logits, int64_t rows, int64_t V, int dt_in, int64_t K,
                       double *lse, int64_t *amax, int64_t *top_idx, float *top_val, bool tail_on, double mult,
                       double cap, void *logits_out);

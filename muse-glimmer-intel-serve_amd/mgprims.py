@@ -55,6 +55,8 @@ _SIGS = {
     "mg_softcap": ([_P, _P, _I, _D, _D, _INT], _INT),
     "mg_dequant_q8_0": ([_P, _P, _P, _P, _I, _I, _INT], _INT),
     "mg_vocab_reduce": ([_P, _P, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
+    "mg_quantize_q8_0": ([_P, _P, _I, _I, _P, _P], _INT),
+    "mg_gemv_q8_0": ([_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _INT], _INT),
     "mg_sample_dist": ([_P, _P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P], _INT),
     "mg_vocab_reduce_tail": ([_P, _P, _I, _I, _INT, _D, _D, _I, _P, _P, _P, _P, _P], _INT),
 }
@@ -208,6 +210,18 @@ class Prims:
         """qs int8 [rows, in], d f16 scales [rows, in/32] -> out [rows, in] (k_dequant_q8)."""
         rows, n_in = qs.shape
         self._check(self.lib.mg_dequant_q8_0(self.h, _ptr(qs), _ptr(d), _ptr(out), rows, n_in, _dtype_code(out)))
+
+    def quantize_q8_0(self, w, qs, d):
+        """w bf16 [rows, in] -> qs int8 [rows, in], d f16 [rows, in/32] (up_w, llama.cpp Q8_0 rule)."""
+        rows, n_in = w.shape
+        self._check(self.lib.mg_quantize_q8_0(self.h, _ptr(w), rows, n_in, _ptr(qs), _ptr(d)))
+
+    def gemv_q8_0(self, qs, d, x, y, blockdot=False):
+        """y[b, o] = sum_i W[o, i] x[b, i] over a Q8_0 weight (k_gemv_q8); x bf16 [B, in], y f32 [B, rows]."""
+        rows, n_in = qs.shape
+        B = x.shape[0]
+        self._check(self.lib.mg_gemv_q8_0(self.h, _ptr(qs), _ptr(d), _ptr(x), B, rows, n_in, x.stride(0), _ptr(y),
+                                          y.stride(0), int(blockdot)))
 
     # -------------------------------------------------------------- vocab
     def vocab_reduce(self, logits, K, lse=None, argmax=None, top_idx=None, top_val=None):
