@@ -60,6 +60,7 @@ BYTES = {
     "vocab_tail_top64_dist": V_ROWS * VOCAB * 4 + V_ROWS * (8 + 8) + V_ROWS * TOPK * (8 + 4) * 2,
     "quantize_q8_0": Q8_R * Q8_C * 2 + Q8_R * Q8_C + Q8_R * (Q8_C // 32) * 2,
     "gemv_q8_0_decode": Q8_R * Q8_C + Q8_R * (Q8_C // 32) * 2 + Q8_C * 2 + Q8_R * 4,
+    "attn_decode_131072": 2 * DEC_K * K_H * HD * 2 + Q_H * HD * 2 + Q_H * HD * 4,
     # q, k read + written, v read, k/v cache rows written, cos/sin read
     "qk_norm_rope_kv": 2 * (2 * T * Q_H * HD + 2 * T * K_H * HD) + 2 * T * K_H * HD + 2 * 2 * T * K_H * HD
                        + 2 * 2 * T * (HD // 2),
@@ -75,6 +76,7 @@ KERNEL_OF = {
     "vocab_lse_argmax_top64": "k_vocab_chunk + k_vocab_merge",
     "qk_norm_rope_kv": "k_qk_norm_rope",
     "quantize_q8_0": "k_quantize_q8_0",
+    "attn_decode_131072": "k_attn_split<5,64> + k_attn_combine",
     "gemv_q8_0_decode": "k_gemv_q8_0<1>",
     "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
 }
@@ -134,6 +136,10 @@ def make_inputs(torch, P):
     I["qd2"] = torch.empty((Q8_R, Q8_C // 32), dtype=torch.int16, device=dev)
     I["xg"] = randn((1, Q8_C))
     I["yg"] = torch.empty((1, Q8_R), dtype=torch.float32, device=dev)
+    I["qd1"] = randn((Q_H, HD))
+    I["kring"] = randn((DEC_K, K_H, HD))
+    I["vring"] = randn((DEC_K, K_H, HD))
+    I["attn_out"] = torch.empty((Q_H, HD), dtype=torch.float32, device=dev)
     I["v"] = randn((T, K_H, HD))
     I["kcache"] = torch.empty((T, K_H, HD), dtype=bf, device=dev)
     I["vcache"] = torch.empty((T, K_H, HD), dtype=bf, device=dev)
@@ -159,6 +165,7 @@ def make_inputs(torch, P):
         "vocab_lse_argmax_top64": lambda: P.vocab_reduce(I["logits"], TOPK, I["lse"], I["amax"], I["tidx"], I["tval"]),
         "vocab_tail_top64_dist": lambda: tail_dist(),
         "quantize_q8_0": lambda: P.quantize_q8_0(I["wq"], I["qs2"], I["qd2"]),
+        "attn_decode_131072": lambda: P.attn_decode(I["qd1"], I["kring"], I["vring"], DEC_K - 1, scale, 0, I["attn_out"]),
         "gemv_q8_0_decode": lambda: P.gemv_q8_0(I["qs"], I["qd"], I["xg"], I["yg"]),
         "qk_norm_rope_kv": lambda: P.qk_norm_rope(I["q"], I["k"], 1e-6, 3.87, I["cos"], I["sin"], None, 0, I["v"],
                                                   I["kcache"], I["vcache"]),

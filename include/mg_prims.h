@@ -154,6 +154,20 @@ int mg_softcap(mg_ctx *ctx, void *z, int64_t n, double mult, double cap, int dty
 int mg_dequant_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, void *out, int64_t rows,
                     int64_t in, int dtype_out);
 
+/* Decode attention, the softmax's caller at one query token — the GPU
+ * engine's split-K flash decode (k_attn_decode_split + k_attn_decode_combine,
+ * src/gpu/gpu_engine.cpp:1690-1857) over the KV ring of k_kv_append:
+ * q bf16 [q_heads, head_dim] (after QK-norm, scale and RoPE), caches bf16
+ * [cache_slots, kv_heads, head_dim] with key position j in slot j % cache_slots;
+ * keys lo..q_pos, lo = window > 0 ? max(0, q_pos - window + 1) : 0 (at most
+ * cache_slots of them); query head h reads kv head h / (q_heads / kv_heads).
+ * out f32 [q_heads, head_dim] = softmax(q.k * scaling) v. head_dim 64 or 128,
+ * at most 8 query heads per kv head. Like the reference's split-K path, a
+ * numerical envelope rather than bits (f32 online softmax, split merge). */
+int mg_attn_decode(mg_ctx *ctx, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache, int64_t q_heads,
+                   int64_t kv_heads, int64_t head_dim, int64_t cache_slots, int64_t q_pos, int64_t window,
+                   double scaling, float *out);
+
 /* Q8_0 quantizer, the step before dequant — up_w (src/gpu/gpu_engine.cpp:2722-2755,
  * llama.cpp's quantize_row_q8_0 rule): w bf16 bits [rows, in] (in % 32 == 0) ->
  * qs int8 [rows, in] and d f16 bits [rows, in/32]; per 32-block d = amax/127 in

@@ -134,19 +134,6 @@ namespace mg
         }
     }
 
-    // LDS writes of one wave made visible to the same wave's later reads
-    MG_DEV void wave_lds_sync()
-    {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-
-    MG_DEV int lane_rank(uint64_t mask)
-    {
-        return int(__builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u)));
-    }
-
     // ------------------------------------------------------------------ pass 1
     // lane element s sits at chunk offset VW*lane + 64*VW*(s/VW) + s%VW: VW
     // consecutive elements per 16-byte load, a wave covering 1 KiB per load

@@ -281,3 +281,14 @@ int mg_gemv_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, const uint16_
         return 0;
     });
 }
+
+int mg_attn_decode(mg_ctx *ctx, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache, int64_t q_heads,
+                   int64_t kv_heads, int64_t head_dim, int64_t cache_slots, int64_t q_pos, int64_t window,
+                   double scaling, float *out)
+{
+    MG_GUARD(-1, {
+        mg::launch_attn_decode(ctx_of(ctx), q, k_cache, v_cache, q_heads, kv_heads, head_dim, cache_slots, q_pos,
+                               window, scaling, out);
+        return 0;
+    });
+}

@@ -276,6 +276,19 @@ namespace mg
         return __builtin_popcountll(__builtin_amdgcn_ballot_w64(p));
     }
 
+    // LDS writes of one wave made visible to the same wave's later reads
+    MG_DEV void wave_lds_sync()
+    {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    MG_DEV int lane_rank(uint64_t mask)
+    {
+        return int(__builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u)));
+    }
+
     // ---------------------------------------------------------------- f32 exp
     // e^(x + lo) for the f32 reductions, lo a small correction term (|lo| <=
     // ulp(x)/2): Cody–Waite reduction x = n·ln2 + r with the Cephes

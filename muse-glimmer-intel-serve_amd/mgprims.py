@@ -57,6 +57,7 @@ _SIGS = {
     "mg_vocab_reduce": ([_P, _P, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
     "mg_quantize_q8_0": ([_P, _P, _I, _I, _P, _P], _INT),
     "mg_gemv_q8_0": ([_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _INT], _INT),
+    "mg_attn_decode": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _D, _P], _INT),
     "mg_sample_dist": ([_P, _P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P], _INT),
     "mg_vocab_reduce_tail": ([_P, _P, _I, _I, _INT, _D, _D, _I, _P, _P, _P, _P, _P], _INT),
 }
@@ -192,6 +193,18 @@ class Prims:
             self.h, _ptr(q), qh, q.stride(0), _ptr(k), kh, k.stride(0) if k is not None else 0, T, D, eps,
             qk_scale, _ptr(cos), _ptr(sin), cos.shape[0] if cos is not None else 0, _ptr(positions), pos0,
             _ptr(v), v.stride(0) if v is not None else 0, _ptr(k_cache), _ptr(v_cache), slots, _dtype_code(q)))
+
+    def attn_decode(self, q, k_cache, v_cache, q_pos, scaling, window=0, out=None):
+        """One query token's attention over the KV ring (split-K flash decode):
+        q [Hq, D] bf16, caches [slots, Hk, D] bf16 -> out [Hq, D] f32."""
+        import torch
+        hq, D = q.shape
+        slots, hk, _ = k_cache.shape
+        if out is None:
+            out = torch.empty((hq, D), dtype=torch.float32, device=q.device)
+        self._check(self.lib.mg_attn_decode(self.h, _ptr(q), _ptr(k_cache), _ptr(v_cache), hq, hk, D, slots, q_pos,
+                                            window, scaling, _ptr(out)))
+        return out
 
     # ------------------------------------------------------------ softmax
     def softmax_rows(self, x, y, scale, mask=MASK_NONE, window=0, q_pos0=0, softcap=0.0):
