@@ -75,35 +75,57 @@ namespace mg
     // up_w (src/gpu/gpu_engine.cpp:2722-2755), the llama.cpp quantize_row_q8_0
     // rule: per 32-block, amax = max |x| over the bf16 values, d = amax / 127
     // (f32), id = d ? 1/d : 0, the scale stored as f16 (RNE, subnormals kept,
-    // f32_to_f16 at 152-158), q = lround(x * id) (half away from zero). One
-    // lane per block.
+    // f32_to_f16 at 152-158), q = lround(x * id) (half away from zero).
+    // A wave takes 64 consecutive blocks (2048 weights): in step k, lane L
+    // holds weights 512k + 8L .. +7, so the four lanes of a quad hold one
+    // block and amax is a quad reduction; every load instruction reads 1 KiB
+    // and every store instruction writes 512 contiguous bytes of quants, and
+    // the wave's 64 scales go out in one 128-byte store.
+    MG_DEV float quad_max(float v)
+    {
+        v = __builtin_fmaxf(v, dpp_mov<0xB1, 0xf>(v, v)); // quad_perm [1,0,3,2]
+        v = __builtin_fmaxf(v, dpp_mov<0x4E, 0xf>(v, v)); // quad_perm [2,3,0,1]
+        return v;
+    }
+
     __global__ __launch_bounds__(256) void k_quantize_q8_0(const uint16_t *__restrict__ w, int8_t *__restrict__ qs,
                                                            uint16_t *__restrict__ d, int64_t nblk)
     {
-        const int64_t b = int64_t(blockIdx.x) * 256 + threadIdx.x;
-        if (b >= nblk) return;
-        const uint16_t *src = w + b * 32;
-        float x[32];
-        float amax = 0.0f;
+        const int lane = threadIdx.x & 63;
+        const int64_t b0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 64; // the wave's first block
+        if (b0 >= nblk) return;
+        Vec<uint16_t, 8> v[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const Vec<uint16_t, 8> v = ld16_stream<uint16_t, 8>(src + 8 * k);
+            v[k] = Vec<uint16_t, 8>{};
+            if (b0 + 16 * k + (lane >> 2) < nblk) v[k] = ld16_stream<uint16_t, 8>(w + b0 * 32 + 512 * k + 8 * lane);
+        }
+        uint16_t my_scale = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t b = b0 + 16 * k + (lane >> 2);
+            float x[8], amax = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                x[8 * k + e] = bf16_f32(v.v[e]);
-                amax = __builtin_fmaxf(amax, __builtin_fabsf(x[8 * k + e]));
+                x[e] = bf16_f32(v[k].v[e]);
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(x[e]));
+            }
+            amax = quad_max(amax);
+            const float dd = amax / 127.0f;
+            const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+            const uint16_t dh = __builtin_bit_cast(uint16_t, static_cast<_Float16>(dd));
+            // gather the scales so that lane j holds block b0 + j's
+            const uint16_t s = uint16_t(__shfl(int(dh), 4 * (lane & 15), 64));
+            if ((lane >> 4) == k) my_scale = s;
+            if (b < nblk) {
+                uint64_t q = 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    q |= uint64_t(uint8_t(int8_t(int(__builtin_roundf(x[e] * id))))) << (8 * e);
+                __builtin_nontemporal_store(q, reinterpret_cast<uint64_t *>(qs + b0 * 32 + 512 * k + 8 * lane));
             }
         }
-        const float dd = amax / 127.0f;
-        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
-        d[b] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(dd));
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            Vec<int8_t, 16> q;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) q.v[e] = int8_t(int(__builtin_roundf(x[16 * k + e] * id)));
-            st16_stream<int8_t, 16>(qs + b * 32 + 16 * k, q);
-        }
+        if (b0 + lane < nblk) d[b0 + lane] = my_scale;
     }
 
     void launch_quantize_q8_0(mg_ctx *c, const uint16_t *w, int64_t rows, int64_t in, int8_t *qs, uint16_t *d)
@@ -114,8 +136,9 @@ namespace mg
         need(aligned16(w) && aligned16(qs), "quantize_q8_0: weights and quants must be 16-byte aligned");
         const int64_t nblk = rows * (in / 32);
         if (nblk == 0) return;
-        hipLaunchKernelGGL(k_quantize_q8_0, dim3(unsigned((nblk + 255) / 256)), dim3(256), 0, c->stream, w, qs, d,
-                           nblk);
+        const int64_t waves = (nblk + 63) / 64;
+        need((waves + 3) / 4 <= int64_t(0x7fffffff), "quantize_q8_0: tensor too large");
+        hipLaunchKernelGGL(k_quantize_q8_0, dim3(unsigned((waves + 3) / 4)), dim3(256), 0, c->stream, w, qs, d, nblk);
         check_launch("k_quantize_q8_0");
     }
 

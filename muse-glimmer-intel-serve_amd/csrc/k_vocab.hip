@@ -36,6 +36,7 @@
 // smaller still). Otherwise the selection runs over the full lists.
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
+#include "mg_tanh_fast.hpp"
 
 namespace mg
 {
@@ -59,25 +60,47 @@ namespace mg
     };
 
     // apply_output_tail (src/muse_glimmer.hpp:920-943) on one stored logit:
-    // z*mult, z/cap, tanh, z*cap, each rounded to the logits' storage format,
-    // FDLIBM tanh in f64 — the twin's values, bit for bit (mult 1 / cap 0 skip
-    // their steps). Optionally written back in storage format.
+    // z*mult, z/cap, tanh, z*cap, each rounded to the logits' storage format —
+    // the twin's values, bit for bit (mult 1 / cap 0 skip their steps).
+    // Optionally written back in storage format. mult and cap are f32 values
+    // (the twin's opmath, src/muse_glimmer.hpp:924-926) and z is stored, so
+    // the product and quotient of two floats rounded once in f32 equal the
+    // twin's f64 result rounded f64 -> f32 (products are exact in f64; for
+    // the quotient, 53 >= 2*24 + 2 makes the double rounding innocuous).
+    // tanh is the fast f64 evaluation of mg_tanh_fast.hpp, accepted when its
+    // error interval rounds to one stored value, else FDLIBM (an out-of-line
+    // call, so the unrolled per-key code stays small).
     struct VTail
     {
-        double mult, cap;
+        float mult, cap;
         void *out;
     };
+    __attribute__((noinline)) __device__ double tanh_fdlibm(double x)
+    {
+        return mgm::tanh(x);
+    }
+    template <class SI>
+    MG_DEV float tail_tanh(float v)
+    {
+        const double a = __builtin_fabs(double(v));
+        if (a == a) {
+            const double t = mgm::tanh_fast_abs(a);
+            const auto lo = SI::enc64(t - t * mgm::kTanhFastMargin), hi = SI::enc64(t + t * mgm::kTanhFastMargin);
+            if (lo == hi) return __builtin_copysignf(SI::dec(lo), v);
+        }
+        return SI::dec(SI::enc64(tanh_fdlibm(double(v))));
+    }
     template <class SI>
     MG_DEV float vtail(float x, const VTail &t)
     {
-        double v = double(x);
-        if (t.mult != 1.0) v = double(SI::dec(SI::enc64(v * t.mult)));
-        if (t.cap != 0.0) {
-            v = double(SI::dec(SI::enc64(v / t.cap)));
-            v = double(SI::dec(SI::enc64(mgm::tanh(v))));
-            v = double(SI::dec(SI::enc64(v * t.cap)));
+        float v = x;
+        if (t.mult != 1.0f) v = SI::dec(SI::enc32(v * t.mult));
+        if (t.cap != 0.0f) {
+            v = SI::dec(SI::enc32(v / t.cap));
+            v = tail_tanh<SI>(v);
+            v = SI::dec(SI::enc32(v * t.cap));
         }
-        return float(v);
+        return v;
     }
 
     // order-preserving 32-bit image of a logit: NaN lowest (1, below -inf's
@@ -662,7 +685,7 @@ namespace mg
         const dim3 g1{unsigned((nch + 3) / 4), unsigned(rows), 1u};
         const dim3 g2{unsigned(rows), 1u, 1u};
         // python-float scalars are f32 opmath values outside f64 (src/muse_glimmer.hpp:924-926)
-        const VTail tail{double(float(mult)), double(float(cap)), logits_out};
+        const VTail tail{float(mult), float(cap), logits_out};
         auto go = [&](auto chunk, auto merge, const auto *x) {
             hipLaunchKernelGGL(chunk, g1, dim3(256), 0, c->stream, x, V, int(K), nch, part, blk, lst, tail);
             check_launch("k_vocab_chunk");
