@@ -11,23 +11,37 @@
 // from the sequential recurrence, so its contract is a numerical envelope,
 // not bits.
 //
-// MI355X layout of the work: one wave per (KV head, 256-key split) runs ALL
-// the query heads of its GQA group (5 for the 30B), so every K and V row is
-// read from HBM once. For q.k each lane owns one key and forms the dot from
-// bf16 pairs with v_dot2_f32_bf16 against the group's q rows held in LDS
-// (broadcast reads); for p.v the weights go to LDS and each lane takes 8 of
-// the head's dimensions (one 16-byte load of V) for every 4th key, the four
-// lane groups summed once per split. Online softmax per head in f32
-// (hardware exp2 on log2-scaled scores). A second kernel, four waves per
-// query head, merges the splits: global max, split weights, then the weighted
-// sum of the split accumulators (16-byte loads, the waves' sums added in LDS).
+// MI355X layout of the work: one wave per (KV head, split) runs ALL the
+// query heads of its GQA group (5 for the 30B), so every K and V row is read
+// from HBM once, and both products run on the matrix cores
+// (v_mfma_f32_16x16x32_bf16; lane l = 16c + n holds row/column n and
+// k-elements 8c..8c+7 of an operand, and C rows 4c..4c+3 of column n).
+// Per step of 32 keys:
+//   staging         coalesced 16-byte streaming loads (each instruction reads
+//                   whole 256-byte key rows), requested one step ahead, then
+//                   written to LDS (padded rows);
+//   S^T = K Q^T     A = 16 keys x 32 dims of K read from LDS, B = the group's q
+//                   rows (zero-padded to 16): C lane (head n, c) holds the
+//                   scores of keys 4c..4c+3 of the tile for head n;
+//   O += P V        A = P (heads x 32 keys, two tiles) straight from the S^T
+//                   layout; B = V read from LDS with the transposing
+//                   ds_read_b64_tr_b16 (lane (dim n, c) gets keys 4c..4c+3 of
+//                   dim n). P enters as bf16(p) + bf16(p - bf16(p)) in two
+//                   products, so the weights keep about 17 bits (relative
+//                   error < 2^-17).
+// Online softmax per head in f32 (hardware exp2 on log2-scaled scores), the
+// running sums and O rows rescaled only in steps where a head's maximum
+// moved. Splits are at least 256 keys and long contexts get about one wave
+// per SIMD (1024 waves), each streaming its keys. A second kernel, one
+// work-group per (query head, 16 dims), merges the splits: global max, split
+// weights, the weighted sum of the split accumulators.
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
 
 namespace mg
 {
-    constexpr int kAttnSplit = 256; // keys per split
-    typedef __bf16 bf16x2a __attribute__((ext_vector_type(2)));
+    constexpr int kAttnSplit = 256;    // shortest split (keys)
+    constexpr int kAttnWaves = 1024;   // splits x kv heads aimed at for long contexts
 
     struct AttnArgs
     {
@@ -36,160 +50,213 @@ namespace mg
         float scale2; // scaling * log2(e)
     };
 
-    template <int HPG, int ND> // ND = head_dim / 2 (bf16 pairs per row), <= 64
+    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+    MG_DEV f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c)
+    {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    MG_DEV bf16x8 ld_bf16x8(const uint16_t *p)
+    {
+        return __builtin_bit_cast(bf16x8, *reinterpret_cast<const Vec<uint32_t, 4> *>(p));
+    }
+    typedef short i16x4 __attribute__((ext_vector_type(4)));
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+    // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+    // i % 4 of the 8-byte pieces addressed by lanes 4j + i / 4, j = 0..3
+    MG_DEV bf16x4 lds_read_tr(const uint16_t *p)
+    {
+        typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+        return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p)));
+    }
+
+    template <int HPG, int KB> // KB = head_dim / 32
     __global__ __launch_bounds__(256) void k_attn_split(const uint16_t *__restrict__ q,
                                                         const uint16_t *__restrict__ kc,
                                                         const uint16_t *__restrict__ vc, AttnArgs a,
                                                         float *__restrict__ pm, float *__restrict__ pl,
                                                         float *__restrict__ pa)
     {
-        constexpr int D = 2 * ND;
-        __shared__ __align__(16) uint32_t sq[4][HPG][64];
-        __shared__ __align__(16) float spw[4][HPG][64];
+        constexpr int D = 32 * KB, NT = 2 * KB; // NT output tiles of 16 dims
+        constexpr int LPR = D / 8;              // lanes per 16-byte-piece row of a key
+        constexpr int NLD = D / 16;             // coalesced 16-byte loads per lane per 32 keys
+        constexpr int SK = D + 8, SV = D + 16;  // LDS row strides (elements): conflict-free reads
+        __shared__ __align__(16) uint16_t lk[4][32 * SK];
+        __shared__ __align__(16) uint16_t lv[4][32 * SV];
         const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
         const int64_t w = int64_t(blockIdx.x) * 4 + wv;
-        if (w >= a.nkv * a.nsplit) return; // whole wave
-        const int64_t g = w / a.nsplit;
-        const int sp = int(w - g * a.nsplit);
+        if (w >= a.nkv * a.nsplit) return; // whole wave; nothing below syncs the block
+        // the kv heads of one split are neighbours: they read the same ring rows
+        const int sp = int(w / a.nkv);
+        const int64_t g = w - int64_t(sp) * a.nkv;
         const int64_t j0 = a.lo + int64_t(sp) * a.per;
         const int64_t j1 = j0 + a.per - 1 < a.qpos ? j0 + a.per - 1 : a.qpos;
+        const int n = lane & 15, c = lane >> 4;
+        const bf16x8 zero8 = {};
+        uint16_t *sk = lk[wv], *sv = lv[wv];
 
-        // the group's q rows as bf16 pairs
+        // B of S^T: lane (head n, c) holds q[n][32 kb + 8c ..], zero for padding heads
+        bf16x8 qop[KB];
 #pragma unroll
-        for (int hh = 0; hh < HPG; ++hh)
-            sq[wv][hh][lane] = lane < ND ? reinterpret_cast<const uint32_t *>(q + (g * HPG + hh) * D)[lane] : 0u;
-        wave_lds_sync();
+        for (int kb = 0; kb < KB; ++kb)
+            qop[kb] = n < HPG ? ld_bf16x8(q + (g * HPG + n) * D + 32 * kb + 8 * c) : zero8;
 
-        // p.v: lane = 16 * kk + dg owns dims 8*dg..8*dg+7 for keys u = kk (mod 4)
-        const int kk = lane >> 4, dg = lane & 15;
-        const bool dim_on = 8 * dg < D;
-        float m[HPG], l[HPG], acc[HPG][8];
+        f32x4 o[NT];
 #pragma unroll
-        for (int hh = 0; hh < HPG; ++hh) {
-            m[hh] = -__builtin_huge_valf();
-            l[hh] = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[hh][e] = 0.0f;
-        }
+        for (int t = 0; t < NT; ++t) o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float m = -__builtin_huge_valf(), l = 0.0f; // head n (replicated over c)
         const int64_t rowstride = a.nkv * D;
-        const uint32_t *vbase = reinterpret_cast<const uint32_t *>(vc + g * D);
-        for (int64_t jb = j0; jb <= j1; jb += 64) {
-            // ring slots without a division per key: keys jb.. are consecutive
-            const int64_t sb = jb % a.slots;
-            const int64_t j = jb + lane;
-            const bool valid = j <= j1;
-            int64_t sj = sb + lane;
-            sj = sj >= a.slots ? sj - a.slots : sj;
-            float s[HPG];
+        // coalesced staging: lane l loads the 16-byte piece l % LPR of keys
+        // l / LPR + (64 / LPR) i of the step
+        const int pc = lane % LPR, pr = lane / LPR;
+        const uint16_t *kg = kc + g * D + 8 * pc, *vg = vc + g * D + 8 * pc;
+        Vec<uint32_t, 4> stk[NLD], stv[NLD];
+        auto stage = [&](int64_t sb, int rem) {
+            if (rem >= 31 && sb + 32 <= a.slots) {
+                // the whole step, no ring wrap: one base, constant row steps
+                const int64_t step = (64 / LPR) * rowstride;
+                const uint16_t *pk = kg + (sb + pr) * rowstride, *pv = vg + (sb + pr) * rowstride;
 #pragma unroll
-            for (int hh = 0; hh < HPG; ++hh) s[hh] = 0.0f;
-            if (valid) {
-                const uint32_t *kr = reinterpret_cast<const uint32_t *>(kc + sj * rowstride + g * D);
-                Vec<uint32_t, 4> kv[ND / 4];
+                for (int i = 0; i < NLD; ++i) {
+                    stk[i] = ld16_stream<uint32_t, 4>(reinterpret_cast<const uint32_t *>(pk + i * step));
+                    stv[i] = ld16_stream<uint32_t, 4>(reinterpret_cast<const uint32_t *>(pv + i * step));
+                }
+                return;
+            }
 #pragma unroll
-                for (int p = 0; p < ND / 4; ++p) kv[p] = ld16<uint32_t, 4>(kr + 4 * p); // cached: 16-byte pieces of each line
-#pragma unroll
-                for (int p = 0; p < ND / 4; ++p) {
-#pragma unroll
-                    for (int hh = 0; hh < HPG; ++hh) {
-                        const Vec<uint32_t, 4> qv = *reinterpret_cast<const Vec<uint32_t, 4> *>(&sq[wv][hh][4 * p]);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            s[hh] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2a, qv.v[e]),
-                                                                    __builtin_bit_cast(bf16x2a, kv[p].v[e]), s[hh], false);
-                    }
+            for (int i = 0; i < NLD; ++i) {
+                const int key = pr + (64 / LPR) * i;
+                int64_t sl = sb + key;
+                sl = sl >= a.slots ? sl - a.slots : sl;
+                if (key <= rem) {
+                    stk[i] = ld16_stream<uint32_t, 4>(reinterpret_cast<const uint32_t *>(kg + sl * rowstride));
+                    stv[i] = ld16_stream<uint32_t, 4>(reinterpret_cast<const uint32_t *>(vg + sl * rowstride));
+                } else {
+                    stk[i] = Vec<uint32_t, 4>{{0u, 0u, 0u, 0u}};
+                    stv[i] = stk[i];
                 }
             }
-            // online softmax, log2 domain; the key weights go to LDS
+        };
+        int64_t sb = j0 % a.slots; // ring slot of key jb
+        if (j0 <= j1) stage(sb, int(j1 - j0 < 64 ? j1 - j0 : 64));
+        for (int64_t jb = j0; jb <= j1; jb += 32) {
+            const int rem = int(j1 - jb < 64 ? j1 - jb : 64); // keys jb + i, i <= rem, are attended
 #pragma unroll
-            for (int hh = 0; hh < HPG; ++hh) {
-                const float t = valid ? s[hh] * a.scale2 : -__builtin_huge_valf();
-                const float mn = __builtin_fmaxf(m[hh], dpp_max(t));
-                const float corr = __builtin_amdgcn_exp2f(m[hh] - mn); // first step: 2^-inf = 0
-                const float pw = __builtin_amdgcn_exp2f(t - mn);
-                spw[wv][hh][lane] = pw;
-                l[hh] = l[hh] * corr + dpp_sum_f32(pw);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[hh][e] *= corr;
-                m[hh] = mn;
+            for (int i = 0; i < NLD; ++i) {
+                const int key = pr + (64 / LPR) * i;
+                *reinterpret_cast<Vec<uint32_t, 4> *>(sk + key * SK + 8 * pc) = stk[i];
+                *reinterpret_cast<Vec<uint32_t, 4> *>(sv + key * SV + 8 * pc) = stv[i];
             }
             wave_lds_sync();
-            // p . v over this step's keys: 4 keys at a time, one per lane group
-            const int nk = int(j1 - jb + 1 < 64 ? j1 - jb + 1 : 64);
-            for (int u0 = 0; u0 < nk; u0 += 16) {
-                Vec<uint32_t, 4> vv[4];
+            // K as A of S^T: lane (key n, c) holds dims 32 kb + 8c.. of key 16 t + n
+            bf16x8 kt[2][KB];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int u = u0 + 4 * r + kk;
-                    int64_t su = sb + u;
-                    su = su >= a.slots ? su - a.slots : su;
-                    if (u < nk && dim_on)
-                        vv[r] = ld16_stream<uint32_t, 4>(vbase + su * (rowstride / 2) + 4 * dg);
-                    else
-                        vv[r] = Vec<uint32_t, 4>{{0u, 0u, 0u, 0u}};
-                }
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int u = u0 + 4 * r + kk;
-                    if (u < nk) {
-                        float v[8];
+                for (int kb = 0; kb < KB; ++kb)
+                    kt[t][kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const Vec<uint32_t, 4> *>(
+                                                               sk + (16 * t + n) * SK + 32 * kb + 8 * c));
+            // the next step's K and V are requested now
+            int64_t sn = sb + 32;
+            sn = sn >= a.slots ? sn - a.slots : sn;
+            if (jb + 32 <= j1) stage(sn, int(j1 - jb - 32 < 64 ? j1 - jb - 32 : 64));
+            // scores of keys jb + 16 t + 4c + r for head n
+            float sc[2][4];
+            float mx = -__builtin_huge_valf();
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            v[2 * e] = bf16_f32(vv[r].v[e] & 0xffffu);
-                            v[2 * e + 1] = bf16_f32(vv[r].v[e] >> 16);
-                        }
+            for (int t = 0; t < 2; ++t) {
+                f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                        for (int hh = 0; hh < HPG; ++hh) {
-                            const float wgt = spw[wv][hh][u];
+                for (int kb = 0; kb < KB; ++kb) st = mfma_bf16(kt[t][kb], qop[kb], st);
 #pragma unroll
-                            for (int e = 0; e < 8; ++e) acc[hh][e] = __builtin_fmaf(wgt, v[e], acc[hh][e]);
-                        }
-                    }
-                }
+                for (int r = 0; r < 4; ++r) sc[t][r] = st[r] * a.scale2;
+                if (rem < 31)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        sc[t][r] = 16 * t + 4 * c + r <= rem ? sc[t][r] : -__builtin_huge_valf();
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mx = __builtin_fmaxf(mx, sc[t][r]);
             }
-            wave_lds_sync(); // the next step rewrites spw
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = __builtin_fmaxf(m, mx);
+            // P as A of the P V product: element 4t + r of lane (head n, c) is key 16 t + 4c + r
+            bf16x8 phi, plo;
+            float ps = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float p = __builtin_amdgcn_exp2f(sc[t][r] - mn);
+                    ps += p;
+                    const __bf16 hi = __bf16(p);
+                    phi[4 * t + r] = hi;
+                    plo[4 * t + r] = __bf16(p - float(hi));
+                }
+            if (__builtin_amdgcn_ballot_w64(mn != m) != 0) {
+                // some head's running max moved: rescale its sum and its O row
+                // (rows are heads 4c + r; their factors come from lanes 4c + r)
+                const float corr = __builtin_amdgcn_exp2f(m - mn); // first step: 2^-inf = 0
+                l *= corr;
+                float cr[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * c + r, 64);
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) o[t][r] *= cr[r];
+            }
+            l += ps;
+            m = mn;
+            // V as B of P V: lane (dim n, c) needs keys 4c + r and 16 + 4c + r
+            // of dim 16 s + n; the transposing read gives it from lanes 4j + q
+            // addressing key 4c + j (+16), dims 16 s + 4q..
+            const uint16_t *vr = sv + (4 * c + (n >> 2)) * SV + 4 * (n & 3);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const bf16x4 v0 = lds_read_tr(vr + 16 * t);
+                const bf16x4 v1 = lds_read_tr(vr + 16 * SV + 16 * t);
+                const bf16x8 vb = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[t] = mfma_bf16(phi, vb, o[t]);
+                o[t] = mfma_bf16(plo, vb, o[t]);
+            }
+            wave_lds_sync(); // this step's reads are done before the next step's writes
+            sb = sn;
         }
-        // the four lane groups' partial sums
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const bool empty = j0 > j1;
+        if (c == 0 && n < HPG) {
+            const int64_t base = (g * HPG + n) * a.nsplit + sp;
+            pm[base] = empty ? -__builtin_huge_valf() : m;
+            pl[base] = empty ? 0.0f : l;
+        }
 #pragma unroll
-        for (int hh = 0; hh < HPG; ++hh)
+        for (int r = 0; r < 4; ++r) {
+            const int hh = 4 * c + r;
+            if (hh < HPG) {
+                float *dst = pa + ((g * HPG + hh) * a.nsplit + sp) * D + n;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                acc[hh][e] += __shfl_xor(acc[hh][e], 16, 64);
-                acc[hh][e] += __shfl_xor(acc[hh][e], 32, 64);
-            }
-#pragma unroll
-        for (int hh = 0; hh < HPG; ++hh) {
-            const int64_t h = g * HPG + hh, base = h * a.nsplit + sp;
-            if (lane == 0) {
-                pm[base] = j0 > j1 ? -__builtin_huge_valf() : m[hh];
-                pl[base] = j0 > j1 ? 0.0f : l[hh];
-            }
-            if (kk == 0 && dim_on) {
-                Vec<float, 4> lo, hi;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    lo.v[e] = acc[hh][e];
-                    hi.v[e] = acc[hh][4 + e];
-                }
-                *reinterpret_cast<Vec<float, 4> *>(pa + base * D + 8 * dg) = lo;
-                *reinterpret_cast<Vec<float, 4> *>(pa + base * D + 8 * dg + 4) = hi;
+                for (int t = 0; t < NT; ++t) dst[16 * t] = o[t][r];
             }
         }
     }
 
-    // merge the splits of one query head (four waves): M = max m_s, weights
-    // 2^(m_s - M), out = sum_s w_s acc_s / sum_s w_s l_s. Lane 16*kk + dg of
-    // wave w takes dims 8*dg.. of splits s = 4*(4*i + w) + kk ... i.e. every
-    // 16th split from 4*w + kk; the 16 partial vectors are added in LDS.
+    // merge the splits of one query head for 16 of its dims (one work-group
+    // per (head, 16 dims)): M = max m_s, weights 2^(m_s - M),
+    // out = sum_s w_s acc_s / sum_s w_s l_s. Thread 16 sg + d takes dim d of
+    // splits sg, sg + 16, ...; the 16 partial sums are added in LDS.
     __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ pm, const float *__restrict__ pl,
                                                           const float *__restrict__ pa, float *__restrict__ out,
                                                           int64_t D, int nsplit)
     {
-        __shared__ float wsp[1024];
         __shared__ double redl[4];
         __shared__ float redm[4];
-        __shared__ __align__(16) float part[16][128];
+        __shared__ float part[16][17];
         const int64_t h = blockIdx.x;
+        const int d0 = 16 * int(blockIdx.y);
         const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
         const float *mh = pm + h * nsplit, *lh = pl + h * nsplit;
         float M = -__builtin_huge_valf();
@@ -199,39 +266,26 @@ namespace mg
         __syncthreads();
         M = __builtin_fmaxf(__builtin_fmaxf(redm[0], redm[1]), __builtin_fmaxf(redm[2], redm[3]));
         double L = 0.0;
-        for (int s = tid; s < nsplit; s += 256) {
-            const float wgt = mh[s] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(mh[s] - M);
-            wsp[s] = wgt;
-            L += double(wgt) * double(lh[s]);
-        }
+        for (int s = tid; s < nsplit; s += 256)
+            if (mh[s] != -__builtin_huge_valf()) L += double(__builtin_amdgcn_exp2f(mh[s] - M)) * double(lh[s]);
         L = dpp_sum(L);
         if (lane == 0) redl[wv] = L;
+        const int sg = tid >> 4, d = tid & 15;
+        float o = 0.0f;
+        for (int s = sg; s < nsplit; s += 16) {
+            const float ms = mh[s];
+            if (ms != -__builtin_huge_valf())
+                o = __builtin_fmaf(__builtin_amdgcn_exp2f(ms - M), pa[(h * nsplit + s) * D + d0 + d], o);
+        }
+        part[sg][d] = o;
         __syncthreads();
-        L = (redl[0] + redl[1]) + (redl[2] + redl[3]);
-        const int kk = lane >> 4, dg = lane & 15, grp = 4 * wv + kk; // 16 groups
-        float o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        if (8 * dg < D)
-            for (int s = grp; s < nsplit; s += 16) {
-                const float w = wsp[s];
-                const float *src = pa + (h * nsplit + s) * D + 8 * dg;
-                const Vec<float, 4> a0 = *reinterpret_cast<const Vec<float, 4> *>(src);
-                const Vec<float, 4> a1 = *reinterpret_cast<const Vec<float, 4> *>(src + 4);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    o[e] = __builtin_fmaf(w, a0.v[e], o[e]);
-                    o[4 + e] = __builtin_fmaf(w, a1.v[e], o[4 + e]);
-                }
-            }
-        if (8 * dg < D)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) part[grp][8 * dg + e] = o[e];
-        __syncthreads();
-        const float inv = L > 0.0 ? float(1.0 / L) : 0.0f;
-        for (int64_t d = tid; d < D; d += 256) {
+        if (tid < 16) {
+            L = (redl[0] + redl[1]) + (redl[2] + redl[3]);
+            const float inv = L > 0.0 ? float(1.0 / L) : 0.0f;
             float t = 0.0f;
 #pragma unroll
-            for (int g2 = 0; g2 < 16; ++g2) t += part[g2][d];
-            out[h * D + d] = t * inv;
+            for (int g2 = 0; g2 < 16; ++g2) t += part[g2][tid];
+            out[h * D + d0 + tid] = t * inv;
         }
     }
 
@@ -249,20 +303,27 @@ namespace mg
         const int64_t lo = window > 0 ? (qpos - window + 1 > 0 ? qpos - window + 1 : 0) : 0;
         const int64_t total = qpos - lo + 1;
         need(total <= slots, "attn_decode: the attended keys do not fit the cache ring (qpos - lo + 1 > cache_slots)");
-        const int nsplit = int((total + kAttnSplit - 1) / kAttnSplit);
-        need(nsplit <= 1024, "attn_decode: context longer than 1024 splits of 256 keys");
+        // splits of at least 256 keys, few enough that a long context runs as
+        // about one wave per SIMD, each streaming its keys with the next step's
+        // loads in flight; a multiple of 32 keys (one step)
+        int64_t ns = (total + kAttnSplit - 1) / kAttnSplit;
+        const int64_t ns_cap = kAttnWaves / nkv > 1 ? kAttnWaves / nkv : 1;
+        ns = ns < ns_cap ? ns : ns_cap;
+        int64_t per = (total + ns - 1) / ns;
+        per = (per + 31) / 32 * 32;
+        const int nsplit = int((total + per - 1) / per);
         const int64_t need_bytes = nq * nsplit * int64_t(sizeof(float)) * (D + 2);
         need(need_bytes <= c->work_bytes, "attn_decode: partials exceed the context workspace (raise workspace_bytes at mg_open)");
         float *pm = static_cast<float *>(c->work);
         float *pl = pm + nq * nsplit;
         float *pa = pl + nq * nsplit;
-        const AttnArgs a{nq, nkv, slots, qpos, lo, kAttnSplit, nsplit, float(double(float(scaling)) * 1.4426950408889634)};
+        const AttnArgs a{nq, nkv, slots, qpos, lo, per, nsplit, float(double(float(scaling)) * 1.4426950408889634)};
         const dim3 g1{unsigned((nkv * nsplit + 3) / 4), 1u, 1u};
         auto go = [&](auto kern) {
             hipLaunchKernelGGL(kern, g1, dim3(256), 0, c->stream, q, kc, vc, a, pm, pl, pa);
         };
 #define MG_ATTN_CASE(H)                                                                                             \
-    case H: D == 128 ? go(k_attn_split<H, 64>) : go(k_attn_split<H, 32>); break;
+    case H: D == 128 ? go(k_attn_split<H, 4>) : go(k_attn_split<H, 2>); break;
         switch (hpg) {
             MG_ATTN_CASE(1)
             MG_ATTN_CASE(2)
@@ -276,7 +337,8 @@ namespace mg
         }
 #undef MG_ATTN_CASE
         check_launch("k_attn_split");
-        hipLaunchKernelGGL(k_attn_combine, dim3(unsigned(nq)), dim3(256), 0, c->stream, pm, pl, pa, out, D, nsplit);
+        hipLaunchKernelGGL(k_attn_combine, dim3(unsigned(nq), unsigned(D / 16)), dim3(256), 0, c->stream, pm, pl, pa,
+                           out, D, nsplit);
         check_launch("k_attn_combine");
     }
 } // namespace mg
