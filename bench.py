@@ -76,7 +76,7 @@ KERNEL_OF = {
     "vocab_lse_argmax_top64": "k_vocab_chunk + k_vocab_merge",
     "qk_norm_rope_kv": "k_qk_norm_rope",
     "quantize_q8_0": "k_quantize_q8_0",
-    "attn_decode_131072": "k_attn_split<5,64> + k_attn_combine",
+    "attn_decode_131072": "k_attn_split<5,4> + k_attn_combine",
     "gemv_q8_0_decode": "k_gemv_q8_0<1>",
     "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
 }

@@ -49,16 +49,29 @@ namespace mg
         const int64_t heads = a.nq + a.nkv, rows = a.T * heads;
         const int64_t r0 = int64_t(blockIdx.x) * kQkRows;
         const int nr = int(rows - r0 < kQkRows ? rows - r0 : kQkRows);
-        auto row_ptr = [&](int64_t r) -> raw * {
-            const int64_t t = r / heads, hh = r - t * heads;
-            return hh < a.nq ? q + t * a.ldq + hh * D : k + t * a.ldk + (hh - a.nq) * D;
-        };
+        // per row, once: its address, table position, and the cache row it
+        // appends to (k rows with a cache and a position >= 0), or -1
+        __shared__ raw *rptr[kQkRows];
+        __shared__ const raw *vptr[kQkRows];
+        __shared__ int64_t rpos[kQkRows], rcache[kQkRows];
+        __shared__ int risq[kQkRows];
+        if (threadIdx.x < nr) {
+            const int64_t r = r0 + threadIdx.x, t = r / heads, hh = r - t * heads;
+            const int64_t p = pos ? pos[t] : a.pos0 + t;
+            const bool isq = hh < a.nq;
+            rptr[threadIdx.x] = isq ? q + t * a.ldq + hh * D : k + t * a.ldk + (hh - a.nq) * D;
+            vptr[threadIdx.x] = isq || !v ? nullptr : v + t * a.ldv + (hh - a.nq) * D;
+            rpos[threadIdx.x] = p;
+            risq[threadIdx.x] = isq;
+            rcache[threadIdx.x] = !isq && kc && p >= 0 ? (p % a.slots) * (a.nkv * D) + (hh - a.nq) * D : -1;
+        }
+        __syncthreads();
 
         // stage the head rows
         const int vpr = D / VEC;
         for (int idx = threadIdx.x; idx < nr * vpr; idx += blockDim.x) {
             const int rr = idx / vpr, i = (idx - rr * vpr) * VEC;
-            *reinterpret_cast<Vec<raw, VEC> *>(st + rr * SD + i) = *reinterpret_cast<const Vec<raw, VEC> *>(row_ptr(r0 + rr) + i);
+            *reinterpret_cast<Vec<raw, VEC> *>(st + rr * SD + i) = *reinterpret_cast<const Vec<raw, VEC> *>(rptr[rr] + i);
         }
         __syncthreads();
 
@@ -94,12 +107,11 @@ namespace mg
         if (npv) {
             for (int idx = threadIdx.x; idx < nr * npv; idx += blockDim.x) {
                 const int rr = idx / npv, j = (idx - rr * npv) * PV;
-                const int64_t r = r0 + rr, t = r / heads, hh = r - t * heads;
-                const bool isq = hh < a.nq;
+                const bool isq = risq[rr] != 0;
                 const double rs = rsq[rr];
                 Vec<raw, PV> lo = *reinterpret_cast<const Vec<raw, PV> *>(st + rr * SD + j);
                 Vec<raw, PV> hi = *reinterpret_cast<const Vec<raw, PV> *>(st + rr * SD + j + half);
-                const int64_t p = pos ? pos[t] : a.pos0 + t;
+                const int64_t p = rpos[rr];
                 const bool rot = co && p >= 0 && p < a.table_rows;
                 Vec<raw, PV> cv, sv;
                 if (rot) {
@@ -118,16 +130,15 @@ namespace mg
                     lo.v[e] = l;
                     hi.v[e] = h;
                 }
-                raw *dst = row_ptr(r);
+                raw *dst = rptr[rr];
                 stv<raw, PV>(dst + j, lo);
                 stv<raw, PV>(dst + j + half, hi);
-                if (!isq && kc && p >= 0) {
-                    const int64_t g = hh - a.nq;
-                    const int64_t o = (p % a.slots) * (a.nkv * D) + g * D;
+                const int64_t o = rcache[rr];
+                if (o >= 0) {
                     stv<raw, PV>(kc + o + j, lo);
                     stv<raw, PV>(kc + o + j + half, hi);
                     if (vc) {
-                        const raw *vr = v + t * a.ldv + g * D;
+                        const raw *vr = vptr[rr];
                         stv<raw, PV>(vc + o + j, ldv<raw, PV>(vr + j));
                         stv<raw, PV>(vc + o + j + half, ldv<raw, PV>(vr + j + half));
                     }
@@ -137,8 +148,7 @@ namespace mg
         }
         for (int idx = threadIdx.x; idx < nr * half; idx += blockDim.x) {
             const int rr = idx / half, j = idx - rr * half;
-            const int64_t r = r0 + rr, t = r / heads, hh = r - t * heads;
-            const bool isq = hh < a.nq;
+            const bool isq = risq[rr] != 0;
             const double rs = rsq[rr];
             raw lo = S::enc64(double(S::dec(st[rr * SD + j])) * rs);
             raw hi = S::enc64(double(S::dec(st[rr * SD + j + half])) * rs);
@@ -146,18 +156,17 @@ namespace mg
                 lo = S::enc(S::dec(lo) * qs);
                 hi = S::enc(S::dec(hi) * qs);
             }
-            const int64_t p = pos ? pos[t] : a.pos0 + t;
+            const int64_t p = rpos[rr];
             if (co && p >= 0 && p < a.table_rows) rope_pair<S>(lo, hi, co[p * half + j], si[p * half + j]);
-            raw *dst = row_ptr(r);
+            raw *dst = rptr[rr];
             dst[j] = lo;
             dst[j + half] = hi;
-            if (!isq && kc && p >= 0) {
-                const int64_t g = hh - a.nq;
-                const int64_t o = (p % a.slots) * (a.nkv * D) + g * D;
+            const int64_t o = rcache[rr];
+            if (o >= 0) {
                 kc[o + j] = lo;
                 kc[o + j + half] = hi;
                 if (vc) {
-                    const raw *vr = v + t * a.ldv + g * D;
+                    const raw *vr = vptr[rr];
                     vc[o + j] = vr[j];
                     vc[o + j + half] = vr[j + half];
                 }
