@@ -58,23 +58,38 @@ namespace mg
                                                        uint16_t *__restrict__ out, int64_t n)
     {
         __shared__ uint16_t lut[kLutEntries];
-        for (int i = threadIdx.x; i < kLutEntries / 8; i += blockDim.x)
-            reinterpret_cast<Vec<uint32_t, 4> *>(lut)[i] = reinterpret_cast<const Vec<uint32_t, 4> *>(table)[i];
-        __syncthreads();
-
         constexpr int U = 4;
         const int64_t nvec = n / 8;
         const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-        for (int64_t base = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; base < nvec; base += stride * U) {
-            Vec<uint16_t, 8> av[U], bv[U];
+        int64_t base = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+        Vec<uint16_t, 8> av[U], bv[U];
+        auto fetch = [&](int64_t b0) {
 #pragma unroll
             for (int k = 0; k < U; ++k) {
-                const int64_t i = base + k * stride;
+                const int64_t i = b0 + k * stride;
                 if (i < nvec) {
                     av[k] = ld16_stream<uint16_t, 8>(a + 8 * i);
                     bv[k] = ld16_stream<uint16_t, 8>(b + 8 * i);
                 }
             }
+        };
+        // the first operands are requested before the table, whose copy into
+        // LDS (all of a thread's pieces in flight at once) overlaps them
+        fetch(base);
+        {
+            static_assert(kLutEntries / 8 == 8 * 1024, "table copy assumes 8 pieces per thread");
+            const Vec<uint32_t, 4> *src = reinterpret_cast<const Vec<uint32_t, 4> *>(table);
+            Vec<uint32_t, 4> *dst = reinterpret_cast<Vec<uint32_t, 4> *>(lut);
+            Vec<uint32_t, 4> tv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) tv[u] = src[threadIdx.x + 1024 * u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) dst[threadIdx.x + 1024 * u] = tv[u];
+        }
+        __syncthreads();
+
+        for (; base < nvec; base += stride * U) {
+            if (base != int64_t(blockIdx.x) * blockDim.x + threadIdx.x) fetch(base);
 #pragma unroll
             for (int k = 0; k < U; ++k) {
                 const int64_t i = base + k * stride;
