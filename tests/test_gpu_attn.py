@@ -19,11 +19,11 @@ from util import BF16, to_dev
 pytestmark = pytest.mark.gpu
 
 
-def attn_case(prims, nq, nkv, D, slots, qpos, window=0, seed=61):
+def attn_case(prims, nq, nkv, D, slots, qpos, window=0, seed=61, scaling=None):
     q = O.normal(seed, (nq, D), 0.0, 1.0, BF16)
     kc = O.normal(seed + 1, (slots, nkv, D), 0.0, 1.0, BF16)
     vc = O.normal(seed + 2, (slots, nkv, D), 0.0, 1.0, BF16)
-    scaling = 1.0 / math.sqrt(D)
+    scaling = 1.0 / math.sqrt(D) if scaling is None else scaling
     out = prims.attn_decode(to_dev(q, BF16), to_dev(kc, BF16), to_dev(vc, BF16), qpos, scaling, window)
     out = out.cpu().numpy().astype(np.float64)
     lo = max(0, qpos - window + 1) if window > 0 else 0
@@ -47,6 +47,26 @@ def attn_case(prims, nq, nkv, D, slots, qpos, window=0, seed=61):
 @pytest.mark.parametrize("nq,nkv,D", ((40, 8, 128), (8, 8, 128), (16, 2, 64), (7, 7, 64)))
 def test_shapes(prims, nq, nkv, D):
     attn_case(prims, nq, nkv, D, 5000, 4999)
+
+
+@pytest.mark.parametrize("hpg", (1, 2, 3, 4, 6, 8))
+@pytest.mark.parametrize("D", (64, 128))
+def test_group_sizes(prims, hpg, D):
+    """every query-head count per KV head the matrix-core tiles pad to 16"""
+    attn_case(prims, 2 * hpg, 2, D, 3000, 2999, seed=80 + hpg)
+
+
+def test_peaked_scores(prims):
+    """scaling 1: scores spread over tens of units, so the running maxima move
+    late in the splits and the lazy rescale runs"""
+    attn_case(prims, 40, 8, 128, 8192, 8191, scaling=1.0, seed=91)
+
+
+def test_long_unaligned(prims):
+    """a context that is not a multiple of the step or split length (longer
+    splits for long contexts), ending part-way through a step"""
+    attn_case(prims, 40, 8, 128, 40960, 39999 - 7, seed=92)
+    attn_case(prims, 40, 8, 128, 70000, 65536 + 17, window=60001, seed=93)
 
 
 def test_window_and_ring(prims):

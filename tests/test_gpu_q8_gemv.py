@@ -28,8 +28,9 @@ def bf16_weights(seed, rows, n_in):
     return O.from_f64(wf, BF16)
 
 
-@pytest.mark.parametrize("rows,n_in", ((64, 4096), (300, 160)))
+@pytest.mark.parametrize("rows,n_in", ((64, 4096), (300, 160), (4, 32), (5, 96)))
 def test_quantize_bitwise(prims, rows, n_in):
+    """whole and partial 64-block waves (a wave quantizes 64 consecutive blocks)"""
     import torch
     w = bf16_weights(51, rows, n_in)
     rq, rd = O.quantize_q8_0(w)
