@@ -154,6 +154,23 @@ int mg_softcap(mg_ctx *ctx, void *z, int64_t n, double mult, double cap, int dty
 int mg_dequant_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, void *out, int64_t rows,
                     int64_t in, int dtype_out);
 
+/* Prefill attention over the KV ring — the GPU engine's --flash-prefill tier
+ * (attention_flash with k_flash_softmax and k_flash_finish,
+ * src/gpu/gpu_engine.cpp:3292-3372, 1481-1560): q bf16 [tokens, q_heads,
+ * head_dim] (token stride ldq, 0 = q_heads*head_dim) after QK-norm, scale and
+ * RoPE; row t, at position pos0 + t, attends keys lo_t..pos0 + t (lo_t =
+ * window > 0 ? max(0, pos0 + t - window + 1) : 0) of the caches bf16
+ * [cache_slots, kv_heads, head_dim] (key j in slot j % cache_slots, all of
+ * them appended before the call); query head h reads kv head
+ * h / (q_heads / kv_heads). out f32 [tokens, q_heads, head_dim] (token stride
+ * ldo, 0 = q_heads*head_dim). Tile-wise online softmax with bf16
+ * probabilities in the p.v product, the reference tier's contract: a
+ * numerical envelope, not bits. head_dim 64 or 128, at most 8 query heads per
+ * kv head. */
+int mg_attn_prefill(mg_ctx *ctx, const uint16_t *q, int64_t ldq, const uint16_t *k_cache, const uint16_t *v_cache,
+                    int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t cache_slots,
+                    int64_t pos0, int64_t window, double scaling, float *out, int64_t ldo);
+
 /* Decode attention, the softmax's caller at one query token — the GPU
  * engine's split-K flash decode (k_attn_decode_split + k_attn_decode_combine,
  * src/gpu/gpu_engine.cpp:1690-1857) over the KV ring of k_kv_append:

@@ -27,8 +27,8 @@
 //                   layout; B = V read from LDS with the transposing
 //                   ds_read_b64_tr_b16 (lane (dim n, c) gets keys 4c..4c+3 of
 //                   dim n). P enters as bf16(p) + bf16(p - bf16(p)) in two
-//                   products, so the weights keep about 17 bits (relative
-//                   error < 2^-17).
+//                   products, so each weight is within 2^-16 of p
+//                   (relative; bf16 carries 8 significant bits).
 // Online softmax per head in f32 (hardware exp2 on log2-scaled scores), the
 // running sums and O rows rescaled only in steps where a head's maximum
 // moved. Splits are at least 256 keys and long contexts get about one wave
@@ -49,28 +49,6 @@ namespace mg
         int nsplit;
         float scale2; // scaling * log2(e)
     };
-
-    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-    typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-    MG_DEV f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c)
-    {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-    }
-    MG_DEV bf16x8 ld_bf16x8(const uint16_t *p)
-    {
-        return __builtin_bit_cast(bf16x8, *reinterpret_cast<const Vec<uint32_t, 4> *>(p));
-    }
-    typedef short i16x4 __attribute__((ext_vector_type(4)));
-    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-
-    // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
-    // i % 4 of the 8-byte pieces addressed by lanes 4j + i / 4, j = 0..3
-    MG_DEV bf16x4 lds_read_tr(const uint16_t *p)
-    {
-        typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-        return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p)));
-    }
 
     template <int HPG, int KB> // KB = head_dim / 32
     __global__ __launch_bounds__(256) void k_attn_split(const uint16_t *__restrict__ q,

@@ -1,0 +1,286 @@
+// Tiled prefill attention for gfx950: the softmax's caller over a whole
+// prompt chunk, on the matrix cores.
+//
+// Reference: the GPU engine's --flash-prefill tier (attention_flash,
+// src/gpu/gpu_engine.cpp:3292-3372, with k_flash_softmax 1481-1545 and
+// k_flash_finish 1547-1560) over the KV ring of k_kv_append (481-492): query
+// row t (position pos0 + t) of head h attends keys j in [lo_t, pos0 + t],
+// lo_t = window > 0 ? max(0, pos0 + t - window + 1) : 0, key j in slot
+// j % slots of kv head h / (q_heads / kv_heads);
+//   S = q.k * scaling, masked keys excluded; per key tile the running
+//   (max, sumexp) fold, the accumulator rescale, and P = bf16(e) for the p.v
+//   product (e summed in f32); out = acc / sumexp (f32).
+// The same numerical contract as the reference's tier: a tile-wise summation
+// schedule with bf16 probabilities in the second product, gated on an
+// envelope rather than bits.
+//
+// Layout of the work: a work-group of HPG waves serves one KV head and 32
+// query rows; wave w runs query head g * HPG + w, so every K/V tile staged in
+// LDS is used by the whole GQA group. Per 32-key step:
+//   staging   coalesced 16-byte loads of the next step's K and V (whole 256-
+//             byte key rows per instruction), held in registers while this
+//             step computes, then written to the other LDS buffer (padded
+//             rows, conflict-free reads); one barrier per step;
+//   S^T       A = 16 keys x 32 dims of K from LDS, B = 16 query rows
+//             (registers): C lane (query n, c) holds keys 4c..4c+3 of the tile,
+//             two key tiles x two query tiles per step;
+//   softmax   per query row in f32 (hardware exp2 on log2-scaled scores), the
+//             row max across the four lane groups by two shuffles;
+//   P V       A = P of two key tiles, straight from the S^T layout, B = V from
+//             LDS through the transposing ds_read_b64_tr_b16.
+// Work-groups of the last query tiles (the most keys) start first.
+#include "mg_device.hpp"
+#include "mg_internal.hpp"
+
+namespace mg
+{
+    constexpr int kPfQ = 32; // query rows per work-group (two 16-row tiles per wave)
+    constexpr int kPfK = 32; // keys per step
+
+    struct PfArgs
+    {
+        int64_t T, nkv, ldq, ldo, slots, pos0, window, nqt;
+        float scale2; // scaling * log2(e)
+    };
+
+    template <int HPG, int KB> // KB = head_dim / 32
+    __global__ __launch_bounds__(64 * HPG) void k_attn_prefill(const uint16_t *__restrict__ q,
+                                                               const uint16_t *__restrict__ kc,
+                                                               const uint16_t *__restrict__ vc, PfArgs a,
+                                                               float *__restrict__ out)
+    {
+        constexpr int D = 32 * KB, NT = 2 * KB; // NT output tiles of 16 dims
+        constexpr int SK = D + 8, SV = D + 16;  // LDS row strides (elements)
+        constexpr int NTHR = 64 * HPG;
+        constexpr int LPR = D / 8;                    // 16-byte pieces per key row
+        constexpr int NPC = kPfK * LPR;               // pieces per tile of K (or V)
+        constexpr int PPT = (2 * NPC + NTHR - 1) / NTHR; // staged pieces per thread
+        __shared__ __align__(16) uint16_t lk[2][kPfK * SK];
+        __shared__ __align__(16) uint16_t lv[2][kPfK * SV];
+        const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
+        const int n = lane & 15, c = lane >> 4;
+        // the last query tiles attend the most keys: they start first
+        const int64_t qt = a.nqt - 1 - int64_t(blockIdx.x) / a.nkv;
+        const int64_t g = int64_t(blockIdx.x) - (int64_t(blockIdx.x) / a.nkv) * a.nkv;
+        const int64_t h = g * HPG + wv;
+        const int64_t q0 = qt * kPfQ;                            // first query row
+        const int64_t qlast = (q0 + kPfQ < a.T ? q0 + kPfQ : a.T) - 1; // last live row
+        const int64_t khi = a.pos0 + qlast;                      // last key any row attends
+        const int64_t p0 = a.pos0 + q0;
+        const int64_t klo = a.window > 0 ? (p0 - a.window + 1 > 0 ? p0 - a.window + 1 : 0) : 0;
+        const int64_t rowstride = a.nkv * D;
+
+        // B of S^T: lane (query n, c) of tile u holds q[q0 + 16u + n][h][32 kb + 8c ..]
+        const bf16x8 zero8 = {};
+        bf16x8 qop[2][KB];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t row = q0 + 16 * u + n <= qlast ? q0 + 16 * u + n : qlast;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) qop[u][kb] = ld_bf16x8(q + row * a.ldq + h * D + 32 * kb + 8 * c);
+        }
+        // this lane's query positions and window starts (S^T layout: query n)
+        int64_t qp[2], ql[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            qp[u] = p0 + 16 * u + n;
+            ql[u] = a.window > 0 ? (qp[u] - a.window + 1 > 0 ? qp[u] - a.window + 1 : 0) : 0;
+        }
+
+        // staging: piece i of a step is K piece i (i < NPC) or V piece i - NPC,
+        // key i / LPR (mod NPC), 16 bytes at column i % LPR
+        Vec<uint32_t, 4> stg[PPT];
+        auto stage = [&](int64_t jb, int64_t sb) {
+#pragma unroll
+            for (int u = 0; u < PPT; ++u) {
+                const int i = tid + NTHR * u;
+                const int iv = i < NPC ? i : i - NPC;
+                const int key = iv / LPR, col = iv - key * LPR;
+                int64_t sl = sb + key;
+                sl = sl >= a.slots ? sl - a.slots : sl;
+                const uint16_t *base = i < NPC ? kc : vc;
+                stg[u] = Vec<uint32_t, 4>{{0u, 0u, 0u, 0u}};
+                if (i < 2 * NPC && jb + key <= khi)
+                    stg[u] = ld16_stream<uint32_t, 4>(
+                        reinterpret_cast<const uint32_t *>(base + sl * rowstride + g * D + 8 * col));
+            }
+        };
+        auto commit = [&](int buf) {
+#pragma unroll
+            for (int u = 0; u < PPT; ++u) {
+                const int i = tid + NTHR * u;
+                if (i < 2 * NPC) {
+                    const int iv = i < NPC ? i : i - NPC;
+                    const int key = iv / LPR, col = iv - key * LPR;
+                    uint16_t *dst = i < NPC ? lk[buf] + key * SK : lv[buf] + key * SV;
+                    *reinterpret_cast<Vec<uint32_t, 4> *>(dst + 8 * col) = stg[u];
+                }
+            }
+        };
+
+        f32x4 o[2][NT];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) o[u][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float m[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()}, l[2] = {0.0f, 0.0f};
+
+        int64_t sb = klo % a.slots; // ring slot of key jb
+        stage(klo, sb);
+        commit(0);
+        __syncthreads();
+        int buf = 0;
+        for (int64_t jb = klo; jb <= khi; jb += kPfK) {
+            int64_t sn = sb + kPfK;
+            sn = sn >= a.slots ? sn - a.slots : sn;
+            const bool more = jb + kPfK <= khi;
+            if (more) stage(jb + kPfK, sn); // in flight while this step computes
+            const uint16_t *sk = lk[buf], *sv = lv[buf];
+            // K as A of S^T: lane (key n, c) holds dims 32 kb + 8c.. of key 16 t + n
+            bf16x8 kt[2][KB];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+                    kt[t][kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const Vec<uint32_t, 4> *>(
+                                                               sk + (16 * t + n) * SK + 32 * kb + 8 * c));
+            // the whole step is attended by every row of the wave unless it
+            // reaches past the first row's position or before the last row's window
+            const bool full = jb + kPfK - 1 <= p0 && (a.window <= 0 || jb >= a.pos0 + qlast - a.window + 1);
+            bf16x8 pb[2];
+            bool moved = false;
+            float corr[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                float s[2][4];
+                float mx = -__builtin_huge_valf();
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int kb = 0; kb < KB; ++kb) st = mfma_bf16(kt[t][kb], qop[u][kb], st);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float v = st[r] * a.scale2;
+                        if (!full) {
+                            const int64_t j = jb + 16 * t + 4 * c + r;
+                            v = (j > qp[u] || j < ql[u]) ? -__builtin_huge_valf() : v;
+                        }
+                        s[t][r] = v;
+                        mx = __builtin_fmaxf(mx, v);
+                    }
+                }
+                mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float mn = __builtin_fmaxf(m[u], mx);
+                // a row with nothing attended yet keeps a zero reference: its
+                // weights are 2^-inf = 0 and nothing is rescaled into NaN
+                const float mref = mn == -__builtin_huge_valf() ? 0.0f : mn;
+                float ps = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float e = __builtin_amdgcn_exp2f(s[t][r] - mref);
+                        ps += e;
+                        pb[u][4 * t + r] = __bf16(e);
+                    }
+                corr[u] = __builtin_amdgcn_exp2f(m[u] - mref);
+                moved |= mn != m[u];
+                l[u] = (mn != m[u] ? l[u] * corr[u] : l[u]) + ps;
+                m[u] = mn;
+            }
+            if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+                // O rows are query rows 4c + r: their factors come from lanes 4c + r
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    float cr[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr[u], 4 * c + r, 64);
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[u][t][r] *= cr[r];
+                }
+            }
+            // V as B of P V: lane (dim n, c) gets keys 4c + r and 16 + 4c + r of
+            // dim 16 s + n from the transposing read (lanes 4j + q address key
+            // 4c + j (+16), dims 16 s + 4q..)
+            const uint16_t *vr = sv + (4 * c + (n >> 2)) * SV + 4 * (n & 3);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const bf16x4 v0 = lds_read_tr(vr + 16 * t);
+                const bf16x4 v1 = lds_read_tr(vr + 16 * SV + 16 * t);
+                const bf16x8 vb = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+#pragma unroll
+                for (int u = 0; u < 2; ++u) o[u][t] = mfma_bf16(pb[u], vb, o[u][t]);
+            }
+            if (more) commit(buf ^ 1);
+            __syncthreads(); // the next buffer is written; this one is free again
+            buf ^= 1;
+            sb = sn;
+        }
+
+        // out = acc / sumexp, rows 4c + r of each tile from lanes 4c + r
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            float lt = l[u];
+            lt += __shfl_xor(lt, 16, 64);
+            lt += __shfl_xor(lt, 32, 64);
+            const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float ir = __shfl(inv, 4 * c + r, 64);
+                const int64_t row = q0 + 16 * u + 4 * c + r;
+                if (row <= qlast) {
+                    float *dst = out + row * a.ldo + h * D + n;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) dst[16 * t] = o[u][t][r] * ir;
+                }
+            }
+        }
+    }
+
+    void launch_attn_prefill(mg_ctx *c, const uint16_t *q, int64_t ldq, const uint16_t *kc, const uint16_t *vc,
+                             int64_t T, int64_t nq, int64_t nkv, int64_t D, int64_t slots, int64_t pos0,
+                             int64_t window, double scaling, float *out, int64_t ldo)
+    {
+        need(nq > 0 && nkv > 0 && nq % nkv == 0, "attn_prefill: q_heads must be a multiple of kv_heads");
+        const int64_t hpg = nq / nkv;
+        need(hpg <= 8, "attn_prefill: at most 8 query heads per kv head");
+        need(D == 64 || D == 128, "attn_prefill: head_dim must be 64 or 128");
+        need(T >= 0 && pos0 >= 0 && slots > 0, "attn_prefill: bad shape");
+        need(q && kc && vc && out, "attn_prefill: NULL tensor");
+        if (ldq == 0) ldq = nq * D;
+        if (ldo == 0) ldo = nq * D;
+        need(ldq >= nq * D && ldo >= nq * D && ldq % 8 == 0, "attn_prefill: token stride too small or unaligned");
+        need(aligned16(q) && aligned16(kc) && aligned16(vc), "attn_prefill: q and caches must be 16-byte aligned");
+        if (T == 0) return;
+        const int64_t lo0 = window > 0 ? (pos0 - window + 1 > 0 ? pos0 - window + 1 : 0) : 0;
+        need(pos0 + T - 1 - lo0 + 1 <= slots,
+             "attn_prefill: the attended keys do not fit the cache ring (pos0 + T - lo > cache_slots)");
+        const int64_t nqt = (T + kPfQ - 1) / kPfQ;
+        need(nqt * nkv <= int64_t(0x7fffffff), "attn_prefill: too many query tiles");
+        const PfArgs a{T, nkv, ldq, ldo, slots, pos0, window, nqt,
+                       float(double(float(scaling)) * 1.4426950408889634)};
+        const dim3 grid{unsigned(nqt * nkv), 1u, 1u};
+        auto go = [&](auto kern, int waves) {
+            hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * waves)), 0, c->stream, q, kc, vc, a, out);
+        };
+#define MG_PF_CASE(H)                                                                                               \
+    case H: D == 128 ? go(k_attn_prefill<H, 4>, H) : go(k_attn_prefill<H, 2>, H); break;
+        switch (hpg) {
+            MG_PF_CASE(1)
+            MG_PF_CASE(2)
+            MG_PF_CASE(3)
+            MG_PF_CASE(4)
+            MG_PF_CASE(5)
+            MG_PF_CASE(6)
+            MG_PF_CASE(7)
+            MG_PF_CASE(8)
+        default: fail("attn_prefill: unsupported group size");
+        }
+#undef MG_PF_CASE
+        check_launch("k_attn_prefill");
+    }
+} // namespace mg

@@ -282,6 +282,17 @@ int mg_gemv_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, const uint16_
     });
 }
 
+int mg_attn_prefill(mg_ctx *ctx, const uint16_t *q, int64_t ldq, const uint16_t *k_cache, const uint16_t *v_cache,
+                    int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t cache_slots,
+                    int64_t pos0, int64_t window, double scaling, float *out, int64_t ldo)
+{
+    MG_GUARD(-1, {
+        mg::launch_attn_prefill(ctx_of(ctx), q, ldq, k_cache, v_cache, tokens, q_heads, kv_heads, head_dim,
+                                cache_slots, pos0, window, scaling, out, ldo);
+        return 0;
+    });
+}
+
 int mg_attn_decode(mg_ctx *ctx, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache, int64_t q_heads,
                    int64_t kv_heads, int64_t head_dim, int64_t cache_slots, int64_t q_pos, int64_t window,
                    double scaling, float *out)

@@ -284,6 +284,30 @@ namespace mg
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 
+    // ------------------------------------------------------------ matrix cores
+    // v_mfma_f32_16x16x32_bf16: lane l = 16c + n holds row n of A (column n of
+    // B) and its k-elements 8c..8c+7; C lane l holds rows 4c..4c+3 of column n
+    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+    MG_DEV f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c)
+    {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    MG_DEV bf16x8 ld_bf16x8(const uint16_t *p)
+    {
+        return __builtin_bit_cast(bf16x8, *reinterpret_cast<const Vec<uint32_t, 4> *>(p));
+    }
+    // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+    // i % 4 of the 8-byte pieces addressed by lanes 4j + i / 4, j = 0..3
+    MG_DEV bf16x4 lds_read_tr(const uint16_t *p)
+    {
+        typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+        return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p)));
+    }
+
     MG_DEV int lane_rank(uint64_t mask)
     {
         return int(__builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u)));

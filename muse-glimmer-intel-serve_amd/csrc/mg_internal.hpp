@@ -81,6 +81,9 @@ namespace mg
     void launch_quantize_q8_0(mg_ctx *c, const uint16_t *w, int64_t rows, int64_t in, int8_t *qs, uint16_t *d);
     void launch_gemv_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, const uint16_t *x, int64_t batch,
                           int64_t rows, int64_t in, int64_t ldx, float *y, int64_t ldy, bool blockdot);
+    void launch_attn_prefill(mg_ctx *c, const uint16_t *q, int64_t ldq, const uint16_t *kc, const uint16_t *vc,
+                             int64_t T, int64_t nq, int64_t nkv, int64_t D, int64_t slots, int64_t pos0,
+                             int64_t window, double scaling, float *out, int64_t ldo);
     void launch_attn_decode(mg_ctx *c, const uint16_t *q, const uint16_t *kc, const uint16_t *vc, int64_t nq,
                             int64_t nkv, int64_t D, int64_t slots, int64_t qpos, int64_t window, double scaling,
                             float *out);

@@ -58,6 +58,7 @@ _SIGS = {
     "mg_quantize_q8_0": ([_P, _P, _I, _I, _P, _P], _INT),
     "mg_gemv_q8_0": ([_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _INT], _INT),
     "mg_attn_decode": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _D, _P], _INT),
+    "mg_attn_prefill": ([_P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _D, _P, _I], _INT),
     "mg_sample_dist": ([_P, _P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P], _INT),
     "mg_vocab_reduce_tail": ([_P, _P, _I, _I, _INT, _D, _D, _I, _P, _P, _P, _P, _P], _INT),
 }
@@ -193,6 +194,19 @@ class Prims:
             self.h, _ptr(q), qh, q.stride(0), _ptr(k), kh, k.stride(0) if k is not None else 0, T, D, eps,
             qk_scale, _ptr(cos), _ptr(sin), cos.shape[0] if cos is not None else 0, _ptr(positions), pos0,
             _ptr(v), v.stride(0) if v is not None else 0, _ptr(k_cache), _ptr(v_cache), slots, _dtype_code(q)))
+
+    def attn_prefill(self, q, k_cache, v_cache, pos0, scaling, window=0, out=None):
+        """Attention of a prompt chunk over the KV ring (the flash-prefill tier,
+        src/gpu/gpu_engine.cpp:3292-3372): q [T, Hq, D] bf16, caches [slots, Hk, D]
+        bf16 holding keys up to pos0 + T - 1 -> out [T, Hq, D] f32."""
+        import torch
+        T, hq, D = q.shape
+        slots, hk, _ = k_cache.shape
+        if out is None:
+            out = torch.empty((T, hq, D), dtype=torch.float32, device=q.device)
+        self._check(self.lib.mg_attn_prefill(self.h, _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), T, hq, hk,
+                                             D, slots, pos0, window, scaling, _ptr(out), out.stride(0)))
+        return out
 
     def attn_decode(self, q, k_cache, v_cache, q_pos, scaling, window=0, out=None):
         """One query token's attention over the KV ring (split-K flash decode):
