@@ -34,8 +34,7 @@
 
 namespace mg
 {
-    constexpr int kPfQ = 32; // query rows per work-group (two 16-row tiles per wave)
-    constexpr int kPfK = 32; // keys per step
+    constexpr int kPfQ = 32; // query rows per work-group (two 16-row tiles)
 
     struct PfArgs
     {
@@ -43,49 +42,52 @@ namespace mg
         float scale2; // scaling * log2(e)
     };
 
-    template <int HPG, int KB> // KB = head_dim / 32
-    __global__ __launch_bounds__(64 * HPG) void k_attn_prefill(const uint16_t *__restrict__ q,
-                                                               const uint16_t *__restrict__ kc,
-                                                               const uint16_t *__restrict__ vc, PfArgs a,
-                                                               float *__restrict__ out)
+    // HPG query heads per kv head, KB = head_dim / 32, RT 16-row tiles per
+    // wave (the work-group has HPG * 2 / RT waves), KT 16-key tiles per step
+    template <int HPG, int KB, int RT, int KT>
+    __global__ __launch_bounds__(64 * HPG * 2 / RT) void k_attn_prefill(const uint16_t *__restrict__ q,
+                                                                        const uint16_t *__restrict__ kc,
+                                                                        const uint16_t *__restrict__ vc, PfArgs a,
+                                                                        float *__restrict__ out)
     {
         constexpr int D = 32 * KB, NT = 2 * KB; // NT output tiles of 16 dims
         constexpr int SK = D + 8, SV = D + 16;  // LDS row strides (elements)
-        constexpr int NTHR = 64 * HPG;
-        constexpr int LPR = D / 8;                    // 16-byte pieces per key row
-        constexpr int NPC = kPfK * LPR;               // pieces per tile of K (or V)
+        constexpr int KS = 16 * KT;             // keys per step
+        constexpr int NTHR = 64 * HPG * 2 / RT;
+        constexpr int LPR = D / 8;                       // 16-byte pieces per key row
+        constexpr int NPC = KS * LPR;                    // pieces per tile of K (or V)
         constexpr int PPT = (2 * NPC + NTHR - 1) / NTHR; // staged pieces per thread
-        __shared__ __align__(16) uint16_t lk[2][kPfK * SK];
-        __shared__ __align__(16) uint16_t lv[2][kPfK * SV];
+        __shared__ __align__(16) uint16_t lk[2][KS * SK];
+        __shared__ __align__(16) uint16_t lv[2][KS * SV];
         const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
         const int n = lane & 15, c = lane >> 4;
         // the last query tiles attend the most keys: they start first
         const int64_t qt = a.nqt - 1 - int64_t(blockIdx.x) / a.nkv;
         const int64_t g = int64_t(blockIdx.x) - (int64_t(blockIdx.x) / a.nkv) * a.nkv;
-        const int64_t h = g * HPG + wv;
-        const int64_t q0 = qt * kPfQ;                            // first query row
+        const int64_t h = g * HPG + wv % HPG;
+        const int u0 = (wv / HPG) * RT;                           // this wave's first row tile
+        const int64_t q0 = qt * kPfQ;                             // the work-group's first query row
         const int64_t qlast = (q0 + kPfQ < a.T ? q0 + kPfQ : a.T) - 1; // last live row
-        const int64_t khi = a.pos0 + qlast;                      // last key any row attends
+        const int64_t khi = a.pos0 + qlast;                       // last key any row attends
         const int64_t p0 = a.pos0 + q0;
         const int64_t klo = a.window > 0 ? (p0 - a.window + 1 > 0 ? p0 - a.window + 1 : 0) : 0;
         const int64_t rowstride = a.nkv * D;
 
-        // B of S^T: lane (query n, c) of tile u holds q[q0 + 16u + n][h][32 kb + 8c ..]
+        // B of S^T: lane (query n, c) of tile u holds q[q0 + 16(u0 + u) + n][h][32 kb + 8c ..]
         const bf16x8 zero8 = {};
-        bf16x8 qop[2][KB];
+        bf16x8 qop[RT][KB];
+        int64_t qp[RT], ql[RT]; // this lane's query position and window start
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int64_t row = q0 + 16 * u + n <= qlast ? q0 + 16 * u + n : qlast;
+        for (int u = 0; u < RT; ++u) {
+            const int64_t r0 = q0 + 16 * (u0 + u) + n;
+            const int64_t row = r0 <= qlast ? r0 : qlast;
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) qop[u][kb] = ld_bf16x8(q + row * a.ldq + h * D + 32 * kb + 8 * c);
-        }
-        // this lane's query positions and window starts (S^T layout: query n)
-        int64_t qp[2], ql[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            qp[u] = p0 + 16 * u + n;
+            qp[u] = a.pos0 + r0;
             ql[u] = a.window > 0 ? (qp[u] - a.window + 1 > 0 ? qp[u] - a.window + 1 : 0) : 0;
         }
+        // the wave's rows: first and last position (for the unmasked-step test)
+        const int64_t wp0 = p0 + 16 * u0, wp1 = p0 + 16 * (u0 + RT) - 1;
 
         // staging: piece i of a step is K piece i (i < NPC) or V piece i - NPC,
         // key i / LPR (mod NPC), 16 bytes at column i % LPR
@@ -118,47 +120,46 @@ namespace mg
             }
         };
 
-        f32x4 o[2][NT];
+        f32x4 o[RT][NT];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < RT; ++u)
 #pragma unroll
             for (int t = 0; t < NT; ++t) o[u][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        float m[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()}, l[2] = {0.0f, 0.0f};
+        float m[RT], l[RT];
+#pragma unroll
+        for (int u = 0; u < RT; ++u) {
+            m[u] = -__builtin_huge_valf();
+            l[u] = 0.0f;
+        }
 
         int64_t sb = klo % a.slots; // ring slot of key jb
         stage(klo, sb);
         commit(0);
         __syncthreads();
         int buf = 0;
-        for (int64_t jb = klo; jb <= khi; jb += kPfK) {
-            int64_t sn = sb + kPfK;
+        for (int64_t jb = klo; jb <= khi; jb += KS) {
+            int64_t sn = sb + KS;
             sn = sn >= a.slots ? sn - a.slots : sn;
-            const bool more = jb + kPfK <= khi;
-            if (more) stage(jb + kPfK, sn); // in flight while this step computes
+            const bool more = jb + KS <= khi;
+            if (more) stage(jb + KS, sn); // in flight while this step computes
             const uint16_t *sk = lk[buf], *sv = lv[buf];
-            // K as A of S^T: lane (key n, c) holds dims 32 kb + 8c.. of key 16 t + n
-            bf16x8 kt[2][KB];
+            // every row of the wave attends the whole step unless it reaches
+            // past the wave's first row or before its last row's window
+            const bool full = jb + KS - 1 <= wp0 && (a.window <= 0 || jb >= wp1 - a.window + 1);
+            // S^T tiles: lane (query n, c) holds keys 16 t + 4c + r
+            float s[RT][KT][4];
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < KT; ++t) {
+                bf16x8 kt[KB]; // K as A: lane (key n, c) holds dims 32 kb + 8c.. of key 16 t + n
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb)
-                    kt[t][kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const Vec<uint32_t, 4> *>(
-                                                               sk + (16 * t + n) * SK + 32 * kb + 8 * c));
-            // the whole step is attended by every row of the wave unless it
-            // reaches past the first row's position or before the last row's window
-            const bool full = jb + kPfK - 1 <= p0 && (a.window <= 0 || jb >= a.pos0 + qlast - a.window + 1);
-            bf16x8 pb[2];
-            bool moved = false;
-            float corr[2];
+                    kt[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const Vec<uint32_t, 4> *>(
+                                                            sk + (16 * t + n) * SK + 32 * kb + 8 * c));
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                float s[2][4];
-                float mx = -__builtin_huge_valf();
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
+                for (int u = 0; u < RT; ++u) {
                     f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                    for (int kb = 0; kb < KB; ++kb) st = mfma_bf16(kt[t][kb], qop[u][kb], st);
+                    for (int kb = 0; kb < KB; ++kb) st = mfma_bf16(kt[kb], qop[u][kb], st);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         float v = st[r] * a.scale2;
@@ -166,10 +167,22 @@ namespace mg
                             const int64_t j = jb + 16 * t + 4 * c + r;
                             v = (j > qp[u] || j < ql[u]) ? -__builtin_huge_valf() : v;
                         }
-                        s[t][r] = v;
-                        mx = __builtin_fmaxf(mx, v);
+                        s[u][t][r] = v;
                     }
                 }
+            }
+            // online softmax per row; P for the p.v product, element 4(t%2) + r
+            // of pair t/2 is key 16 t + 4c + r
+            bf16x8 pb[RT][KT / 2];
+            bool moved = false;
+            float corr[RT];
+#pragma unroll
+            for (int u = 0; u < RT; ++u) {
+                float mx = -__builtin_huge_valf();
+#pragma unroll
+                for (int t = 0; t < KT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) mx = __builtin_fmaxf(mx, s[u][t][r]);
                 mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
                 mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
                 const float mn = __builtin_fmaxf(m[u], mx);
@@ -178,12 +191,12 @@ namespace mg
                 const float mref = mn == -__builtin_huge_valf() ? 0.0f : mn;
                 float ps = 0.0f;
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
+                for (int t = 0; t < KT; ++t)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float e = __builtin_amdgcn_exp2f(s[t][r] - mref);
+                        const float e = __builtin_amdgcn_exp2f(s[u][t][r] - mref);
                         ps += e;
-                        pb[u][4 * t + r] = __bf16(e);
+                        pb[u][t / 2][4 * (t % 2) + r] = __bf16(e);
                     }
                 corr[u] = __builtin_amdgcn_exp2f(m[u] - mref);
                 moved |= mn != m[u];
@@ -193,7 +206,7 @@ namespace mg
             if (__builtin_amdgcn_ballot_w64(moved) != 0) {
                 // O rows are query rows 4c + r: their factors come from lanes 4c + r
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
+                for (int u = 0; u < RT; ++u) {
                     float cr[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr[u], 4 * c + r, 64);
@@ -203,18 +216,20 @@ namespace mg
                         for (int r = 0; r < 4; ++r) o[u][t][r] *= cr[r];
                 }
             }
-            // V as B of P V: lane (dim n, c) gets keys 4c + r and 16 + 4c + r of
-            // dim 16 s + n from the transposing read (lanes 4j + q address key
-            // 4c + j (+16), dims 16 s + 4q..)
+            // V as B of P V: lane (dim n, c) gets keys 32 i + 4c + r and
+            // 32 i + 16 + 4c + r of dim 16 s + n from the transposing read (lanes
+            // 4j + q address key 32 i + 4c + j (+16), dims 16 s + 4q..)
             const uint16_t *vr = sv + (4 * c + (n >> 2)) * SV + 4 * (n & 3);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const bf16x4 v0 = lds_read_tr(vr + 16 * t);
-                const bf16x4 v1 = lds_read_tr(vr + 16 * SV + 16 * t);
-                const bf16x8 vb = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            for (int i = 0; i < KT / 2; ++i)
 #pragma unroll
-                for (int u = 0; u < 2; ++u) o[u][t] = mfma_bf16(pb[u], vb, o[u][t]);
-            }
+                for (int t = 0; t < NT; ++t) {
+                    const bf16x4 v0 = lds_read_tr(vr + 32 * i * SV + 16 * t);
+                    const bf16x4 v1 = lds_read_tr(vr + (32 * i + 16) * SV + 16 * t);
+                    const bf16x8 vb = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+#pragma unroll
+                    for (int u = 0; u < RT; ++u) o[u][t] = mfma_bf16(pb[u][i], vb, o[u][t]);
+                }
             if (more) commit(buf ^ 1);
             __syncthreads(); // the next buffer is written; this one is free again
             buf ^= 1;
@@ -223,7 +238,7 @@ namespace mg
 
         // out = acc / sumexp, rows 4c + r of each tile from lanes 4c + r
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < RT; ++u) {
             float lt = l[u];
             lt += __shfl_xor(lt, 16, 64);
             lt += __shfl_xor(lt, 32, 64);
@@ -231,7 +246,7 @@ namespace mg
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float ir = __shfl(inv, 4 * c + r, 64);
-                const int64_t row = q0 + 16 * u + 4 * c + r;
+                const int64_t row = q0 + 16 * (u0 + u) + 4 * c + r;
                 if (row <= qlast) {
                     float *dst = out + row * a.ldo + h * D + n;
 #pragma unroll
@@ -267,8 +282,10 @@ namespace mg
         auto go = [&](auto kern, int waves) {
             hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * waves)), 0, c->stream, q, kc, vc, a, out);
         };
+        // one 16-row tile per wave (2 * HPG waves) for groups of up to 8 heads;
+        // 64-key steps
 #define MG_PF_CASE(H)                                                                                               \
-    case H: D == 128 ? go(k_attn_prefill<H, 4>, H) : go(k_attn_prefill<H, 2>, H); break;
+    case H: D == 128 ? go(k_attn_prefill<H, 4, 1, 4>, 2 * H) : go(k_attn_prefill<H, 2, 1, 4>, 2 * H); break;
         switch (hpg) {
             MG_PF_CASE(1)
             MG_PF_CASE(2)
