@@ -157,8 +157,7 @@ namespace mg
 #pragma unroll
                 for (int r = 0; r < 4; ++r) mx = __builtin_fmaxf(mx, sc[t][r]);
             }
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = rows4_max(mx);
             const float mn = __builtin_fmaxf(m, mx);
             // P as A of the P V product: element 4t + r of lane (head n, c) is key 16 t + 4c + r
             bf16x8 phi, plo;
@@ -203,8 +202,7 @@ namespace mg
             wave_lds_sync(); // this step's reads are done before the next step's writes
             sb = sn;
         }
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
+        l = rows4_sum(l);
         const bool empty = j0 > j1;
         if (c == 0 && n < HPG) {
             const int64_t base = (g * HPG + n) * a.nsplit + sp;

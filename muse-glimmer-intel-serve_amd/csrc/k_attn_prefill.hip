@@ -183,8 +183,7 @@ namespace mg
                 for (int t = 0; t < KT; ++t)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) mx = __builtin_fmaxf(mx, s[u][t][r]);
-                mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
-                mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+                mx = rows4_max(mx);
                 const float mn = __builtin_fmaxf(m[u], mx);
                 // a row with nothing attended yet keeps a zero reference: its
                 // weights are 2^-inf = 0 and nothing is rescaled into NaN
@@ -239,9 +238,7 @@ namespace mg
         // out = acc / sumexp, rows 4c + r of each tile from lanes 4c + r
 #pragma unroll
         for (int u = 0; u < RT; ++u) {
-            float lt = l[u];
-            lt += __shfl_xor(lt, 16, 64);
-            lt += __shfl_xor(lt, 32, 64);
+            const float lt = rows4_sum(l[u]);
             const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {

@@ -308,6 +308,35 @@ namespace mg
         return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p)));
     }
 
+    // x combined with the value of lane ^ 16 (XOR16) or lane ^ 32 (XOR32) by a
+    // commutative op, through v_permlane16_swap / v_permlane32_swap: with the
+    // same register as both operands, the pair returned holds, in every lane,
+    // its own value and its partner's (no LDS traffic)
+    template <int XOR, class OP>
+    MG_DEV float lane_pair(float x, OP op)
+    {
+        const uint32_t u = __builtin_bit_cast(uint32_t, x);
+        if constexpr (XOR == 16) {
+            const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+            return op(__builtin_bit_cast(float, uint32_t(p[0])), __builtin_bit_cast(float, uint32_t(p[1])));
+        } else {
+            static_assert(XOR == 32, "lane_pair: XOR 16 or 32");
+            const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+            return op(__builtin_bit_cast(float, uint32_t(p[0])), __builtin_bit_cast(float, uint32_t(p[1])));
+        }
+    }
+    // the max / sum over the four 16-lane rows (lanes n, n+16, n+32, n+48)
+    MG_DEV float rows4_max(float x)
+    {
+        auto mx = [](float a, float b) { return __builtin_fmaxf(a, b); };
+        return lane_pair<32>(lane_pair<16>(x, mx), mx);
+    }
+    MG_DEV float rows4_sum(float x)
+    {
+        auto add = [](float a, float b) { return a + b; };
+        return lane_pair<32>(lane_pair<16>(x, add), add);
+    }
+
     MG_DEV int lane_rank(uint64_t mask)
     {
         return int(__builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u)));
