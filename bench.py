@@ -64,7 +64,12 @@ BYTES = {
     # q, k read + written, v read, k/v cache rows written, cos/sin read
     "qk_norm_rope_kv": 2 * (2 * T * Q_H * HD + 2 * T * K_H * HD) + 2 * T * K_H * HD + 2 * 2 * T * K_H * HD
                        + 2 * 2 * T * (HD // 2),
+    # q and the K/V ring read, f32 out written (the op is bound by the matrix cores: FLOPS)
+    "attn_prefill_4096": 2 * T * Q_H * HD + 2 * 2 * T * K_H * HD + 4 * T * Q_H * HD,
 }
+# matrix-core ops: q.k and p.v over the causal pairs, 2 * 2 * head_dim flops per (query, key)
+FLOPS = {"attn_prefill_4096": Q_H * (T * (T + 1) // 2) * 4 * HD}
+PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 STEP_OPS = ("residual_rmsnorm", "swiglu", "softmax_causal")
 KERNEL_OF = {
     "residual_rmsnorm": "k_norm_tree",
@@ -79,6 +84,7 @@ KERNEL_OF = {
     "attn_decode_131072": "k_attn_split<5,4> + k_attn_combine",
     "gemv_q8_0_decode": "k_gemv_q8_0<1>",
     "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
+    "attn_prefill_4096": "k_attn_prefill<5,4,1,4>",
 }
 
 
@@ -146,6 +152,9 @@ def make_inputs(torch, P):
     I["hdec"] = randn((64, D))
     I["xdec"] = randn((64, D))
     I["ydec"] = torch.empty((64, D), dtype=bf, device=dev)
+    I["pk"] = randn((T, K_H, HD))
+    I["pv"] = randn((T, K_H, HD))
+    I["pout"] = torch.empty((T, Q_H, HD), dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
     scale = 1.0 / math.sqrt(HD)
@@ -167,6 +176,7 @@ def make_inputs(torch, P):
         "quantize_q8_0": lambda: P.quantize_q8_0(I["wq"], I["qs2"], I["qd2"]),
         "attn_decode_131072": lambda: P.attn_decode(I["qd1"], I["kring"], I["vring"], DEC_K - 1, scale, 0, I["attn_out"]),
         "gemv_q8_0_decode": lambda: P.gemv_q8_0(I["qs"], I["qd"], I["xg"], I["yg"]),
+        "attn_prefill_4096": lambda: P.attn_prefill(I["q"], I["pk"], I["pv"], 0, scale, 0, I["pout"]),
         "qk_norm_rope_kv": lambda: P.qk_norm_rope(I["q"], I["k"], 1e-6, 3.87, I["cos"], I["sin"], None, 0, I["v"],
                                                   I["kcache"], I["vcache"]),
     }
@@ -323,6 +333,13 @@ def main():
         per[name] = {"us": round(med, 2), "us_min": round(best, 2), "bytes": BYTES[name],
                      "GBps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
                      "kernel": KERNEL_OF[name]}
+        if name in FLOPS:
+            tf = FLOPS[name] / (med * 1e-6) / 1e12
+            per[name].update({"flops": FLOPS[name], "TFLOPs": round(tf, 1), "bound": "mfma",
+                              "pct_peak": round(100 * tf / PEAK_TFLOPS, 1)})
+            print(f"# {name:28s} {med:9.2f} us  {tf:8.1f} TFLOP/s {100 * tf / PEAK_TFLOPS:5.1f} % of bf16 MFMA",
+                  file=sys.stderr, flush=True)
+            continue
         print(f"# {name:28s} {med:9.2f} us  {gbps:8.1f} GB/s  {100 * gbps / PEAK_GBPS:5.1f} %",
               file=sys.stderr, flush=True)
 
