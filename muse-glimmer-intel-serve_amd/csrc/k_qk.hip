@@ -118,17 +118,40 @@ namespace mg
                     cv = *reinterpret_cast<const Vec<raw, PV> *>(co + p * half + j);
                     sv = *reinterpret_cast<const Vec<raw, PV> *>(si + p * half + j);
                 }
+                if constexpr (S::dt == BF16) {
+                    // bf16: NaN propagates through every step and the twin's NaN
+                    // is the single pattern 0x7FC0, so the steps round without
+                    // NaN checks and the outputs are made canonical once
+                    auto rn = [](float f) { return SBf16::enc_finite(f); };
 #pragma unroll
-                for (int e = 0; e < PV; ++e) {
-                    raw l = S::enc64(double(S::dec(lo.v[e])) * rs);
-                    raw h = S::enc64(double(S::dec(hi.v[e])) * rs);
-                    if (isq) {
-                        l = S::enc(S::dec(l) * qs);
-                        h = S::enc(S::dec(h) * qs);
+                    for (int e = 0; e < PV; ++e) {
+                        raw l = rn(float(double(S::dec(lo.v[e])) * rs));
+                        raw h = rn(float(double(S::dec(hi.v[e])) * rs));
+                        if (isq) {
+                            l = rn(S::dec(l) * qs);
+                            h = rn(S::dec(h) * qs);
+                        }
+                        if (rot) {
+                            const float fl = S::dec(l), fh = S::dec(h), cc = S::dec(cv.v[e]), ss = S::dec(sv.v[e]);
+                            l = rn(S::dec(rn(fl * cc)) + S::dec(rn(-(fh * ss))));
+                            h = rn(S::dec(rn(fh * cc)) + S::dec(rn(fl * ss)));
+                        }
+                        lo.v[e] = S::dec(l) != S::dec(l) ? raw(0x7fc0) : l;
+                        hi.v[e] = S::dec(h) != S::dec(h) ? raw(0x7fc0) : h;
                     }
-                    if (rot) rope_pair<S>(l, h, cv.v[e], sv.v[e]);
-                    lo.v[e] = l;
-                    hi.v[e] = h;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < PV; ++e) {
+                        raw l = S::enc64(double(S::dec(lo.v[e])) * rs);
+                        raw h = S::enc64(double(S::dec(hi.v[e])) * rs);
+                        if (isq) {
+                            l = S::enc(S::dec(l) * qs);
+                            h = S::enc(S::dec(h) * qs);
+                        }
+                        if (rot) rope_pair<S>(l, h, cv.v[e], sv.v[e]);
+                        lo.v[e] = l;
+                        hi.v[e] = h;
+                    }
                 }
                 raw *dst = rptr[rr];
                 stv<raw, PV>(dst + j, lo);

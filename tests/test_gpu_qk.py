@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from util import BF16, F16, F32, F64, from_dev, same_bits, storage, to_dev
+from util import BF16, F16, F32, F64, from_dev, same_bits, same_bits_or_nan, storage, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -32,11 +32,22 @@ def oracle_seq(q, k, dt, theta, dim, table_T, pos, use_rope):
 
 
 def run_case(prims, dt, T, qh, kh, dim, theta=1e6, pos0=0, positions=None, table_T=None, use_rope=True,
-             slots=0, with_v=True):
+             slots=0, with_v=True, specials=False):
     import torch
     table_T = table_T or (pos0 + T)
     qs, q = storage(31, (T, qh, dim), dt)
     ks, k = storage(32, (T, kh, dim), dt)
+    if specials:
+        big = 1e30 if dt == BF16 else 6e4
+        q[0, 0, 5] = np.nan           # a NaN row: rs and every output NaN
+        q[1, 3, :] = 0.0              # an all-zero row: rs = 1/sqrt(eps), outputs +-0
+        q[1, 3, 9] = -0.0
+        q[2, 2, 7] = np.inf           # inf: mean_sq inf, rs 0, inf * 0 = NaN
+        q[3, 0, :] *= big             # large values: mean_sq near the top of the range
+        k[0, 1, 3] = -np.inf
+        k[2, 0, 64:] = 0.0            # the rotated half zero
+        qs, q = O.from_f64(q, dt), O.to_f64(O.from_f64(q, dt), dt)
+        ks, k = O.from_f64(k, dt), O.to_f64(O.from_f64(k, dt), dt)
     vs, v = storage(33, (T, kh, dim), dt)
     dq, dk, dv = to_dev(qs, dt), to_dev(ks, dt), to_dev(vs, dt)
     dco = dsi = None
@@ -58,6 +69,10 @@ def run_case(prims, dt, T, qh, kh, dim, theta=1e6, pos0=0, positions=None, table
             vc = None
     prims.qk_norm_rope(dq, dk, EPS, QK, dco, dsi, dpos, pos0, dv if with_v else None, kc, vc)
     rq, rk = oracle_seq(q, k, dt, theta, dim, table_T, pos, use_rope)
+    if specials and dt != BF16:  # bf16's NaN is the one pattern 0x7FC0: bitwise there
+        assert same_bits_or_nan(from_dev(dq, dt), O.from_f64(rq, dt), dt)
+        assert same_bits_or_nan(from_dev(dk, dt), O.from_f64(rk, dt), dt)
+        return
     assert same_bits(from_dev(dq, dt), O.from_f64(rq, dt))
     assert same_bits(from_dev(dk, dt), O.from_f64(rk, dt))
     if slots:
@@ -75,6 +90,13 @@ def run_case(prims, dt, T, qh, kh, dim, theta=1e6, pos0=0, positions=None, table
 @pytest.mark.parametrize("dt", (BF16, F16, F32, F64))
 def test_sequence_bitwise(prims, dt):
     run_case(prims, dt, 65, 40, 8, 128, pos0=7, slots=128)
+
+
+@pytest.mark.parametrize("dt", (BF16, F16))
+def test_special_values(prims, dt):
+    """NaN, inf, zero and large rows through the fused sequence (16-bit paths;
+    NaN has to meet NaN, its sign being unspecified by IEEE)"""
+    run_case(prims, dt, 8, 40, 8, 128, pos0=3, specials=True)
 
 
 def test_prefill_shape_bf16(prims):
