@@ -82,7 +82,8 @@ namespace mg
         const int64_t per_tok = int64_t(qh + kh) * vph;
         const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
         if (idx >= tokens * per_tok) return;
-        const int64_t t = idx / per_tok;
+        const int64_t t = tokens * per_tok <= int64_t(0xffffffff) ? int64_t(uint32_t(idx) / uint32_t(per_tok))
+                                                                    : idx / per_tok;
         const int rem = int(idx - t * per_tok);
         const int hh = rem / vph, jv = rem - hh * vph;
         const int64_t p = pos ? pos[t] : pos0 + t;
@@ -93,8 +94,23 @@ namespace mg
         Vec<raw, VEC> hi = ldv<raw, VEC>(x + half);
         const Vec<raw, VEC> c = *reinterpret_cast<const Vec<raw, VEC> *>(co + p * half + jv * VEC);
         const Vec<raw, VEC> s = *reinterpret_cast<const Vec<raw, VEC> *>(si + p * half + jv * VEC);
+        if constexpr (S::dt == BF16) {
+            // bf16: NaN propagates and the twin's NaN is the one pattern
+            // 0x7FC0, so the steps round without NaN checks and the outputs
+            // are made canonical once
+            auto rn = [](float f) { return SBf16::enc_finite(f); };
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) rope_pair<S>(lo.v[e], hi.v[e], c.v[e], s.v[e]);
+            for (int e = 0; e < VEC; ++e) {
+                const float fl = S::dec(lo.v[e]), fh = S::dec(hi.v[e]), cc = S::dec(c.v[e]), ss = S::dec(s.v[e]);
+                const raw l = rn(S::dec(rn(fl * cc)) + S::dec(rn(-(fh * ss))));
+                const raw h = rn(S::dec(rn(fh * cc)) + S::dec(rn(fl * ss)));
+                lo.v[e] = S::dec(l) != S::dec(l) ? raw(0x7fc0) : l;
+                hi.v[e] = S::dec(h) != S::dec(h) ? raw(0x7fc0) : h;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) rope_pair<S>(lo.v[e], hi.v[e], c.v[e], s.v[e]);
+        }
         stv<raw, VEC>(x, lo);
         stv<raw, VEC>(x + half, hi);
     }

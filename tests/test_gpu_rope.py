@@ -23,12 +23,21 @@ def test_table_bitwise(prims, dt, theta, dim, T):
     assert same_bits(from_dev(si, dt), O.from_f64(rs, dt))
 
 
-def rope_case(prims, dt, T, qh, kh, dim, theta=1e6, positions=None, pos0=0, table_T=None):
+def rope_case(prims, dt, T, qh, kh, dim, theta=1e6, positions=None, pos0=0, table_T=None, specials=False):
     table_T = table_T or T
     rc, rs = O.rope_table(theta, dim, table_T, dt)
     dco, dsi = to_dev(O.from_f64(rc, dt), dt), to_dev(O.from_f64(rs, dt), dt)
     qs, q = storage(6, (T, qh, dim), dt)
     ks, k = storage(7, (T, kh, dim), dt)
+    if specials:
+        big = 3e38 if dt == BF16 else 6e4
+        q[0, 0, 3] = np.nan                 # NaN in the low half: both rotated outputs NaN
+        q[0, 1, 70] = np.inf                # inf in the high half
+        q[1, 2, 5], q[1, 2, 69] = big, big  # products and sums near overflow
+        q[2, 3, :] = -0.0                   # signed zeros
+        k[3, 0, 10] = -np.inf
+        qs, q = O.from_f64(q, dt), O.to_f64(O.from_f64(q, dt), dt)
+        ks, k = O.from_f64(k, dt), O.to_f64(O.from_f64(k, dt), dt)
     dq, dk = to_dev(qs, dt), to_dev(ks, dt)
     dpos = None
     if positions is not None:
@@ -48,6 +57,13 @@ def test_apply_bitwise(prims, dt):
     q, k, rq, rk = rope_case(prims, dt, 257, 40, 8, 128)
     assert same_bits(q, O.from_f64(rq, dt))
     assert same_bits(k, O.from_f64(rk, dt))
+
+
+def test_special_values_bf16(prims):
+    """NaN, inf, overflow and signed zeros: bitwise (bf16's NaN is the one pattern 0x7FC0)"""
+    q, k, rq, rk = rope_case(prims, BF16, 9, 8, 2, 128, specials=True)
+    assert same_bits(q, O.from_f64(rq, BF16))
+    assert same_bits(k, O.from_f64(rk, BF16))
 
 
 def test_config3_full(prims):
