@@ -235,6 +235,7 @@ namespace mg
         need(ldx >= in && ldy >= rows, "gemv_q8_0: leading dimension too small");
         need(aligned16(qs) && aligned16(x) && ldx % 8 == 0, "gemv_q8_0: quants and activations must be 16-byte aligned");
         if (rows == 0) return;
+        need(rows < (int64_t(1) << 33), "gemv_q8_0: too many rows");
         const dim3 g{unsigned((rows + 3) / 4), 1u, 1u};
         // up to four activation rows per pass over the weights
         for (int64_t b0 = 0; b0 < batch; b0 += 4) {
