@@ -39,8 +39,10 @@ enum mg_norm_kind { MG_NORM_CENTERED = 0, MG_NORM_PLAIN = 1, MG_NORM_WEIGHTLESS 
 
 /* mask of a [heads, q, k] score block; qpos = q_pos0 + row.
  * causal: key j visible iff j <= qpos; window: qpos - window < j <= qpos
- * (src/muse_glimmer.hpp:838-843, the sliding-window rule). */
-enum mg_mask { MG_MASK_NONE = 0, MG_MASK_CAUSAL = 1, MG_MASK_WINDOW = 2 };
+ * (src/muse_glimmer.hpp:838-843, the sliding-window rule); biwindow: the
+ * drafter's bidirectional window, qpos - window <= j <= qpos + window
+ * (src/dflash.hpp:339-344). */
+enum mg_mask { MG_MASK_NONE = 0, MG_MASK_CAUSAL = 1, MG_MASK_WINDOW = 2, MG_MASK_BIWINDOW = 3 };
 
 /* Thread-local message of the last failing call on this thread
  * (muse_last_error, src/gpu/c_api.cpp:35, 170-188). */

@@ -43,6 +43,13 @@ namespace mg
         const int64_t qpos = a.q_pos0 + row % a.q;
         lo = 0;
         hi = a.kc - 1;
+        if (a.mask == 3) {
+            // the drafter's bidirectional window (src/dflash.hpp:339-344)
+            const int64_t l = qpos - a.window, h = qpos + a.window;
+            lo = l > 0 ? l : 0;
+            hi = h < hi ? h : hi;
+            return;
+        }
         if (a.mask >= 1) hi = qpos < hi ? qpos : hi;
         if (a.mask == 2) {
             const int64_t l = qpos - a.window + 1;
@@ -551,8 +558,8 @@ namespace mg
     {
         need(heads >= 0 && q >= 0 && kc >= 0, "softmax: bad shape");
         need(x && y, "softmax: NULL tensor");
-        need(mask >= 0 && mask <= 2, "softmax: unknown mask kind");
-        need(mask != 2 || window > 0, "softmax: window mask needs window > 0");
+        need(mask >= 0 && mask <= 3, "softmax: unknown mask kind");
+        need(mask < 2 || window > 0, "softmax: window masks need window > 0");
         if (heads == 0 || q == 0 || kc == 0) return;
         SmArgs a;
         a.nrows = heads * q;

@@ -27,7 +27,7 @@ HEADER = os.path.join(ROOT, "include", "mg_prims.h")
 
 F64, BF16, F16, F32 = 0, 1, 2, 3
 CENTERED, PLAIN, WEIGHTLESS = 0, 1, 2
-MASK_NONE, MASK_CAUSAL, MASK_WINDOW = 0, 1, 2
+MASK_NONE, MASK_CAUSAL, MASK_WINDOW, MASK_BIWINDOW = 0, 1, 2, 3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int64

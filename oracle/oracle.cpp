@@ -419,8 +419,14 @@ extern "C"
                     double *yr = y + (h * q + r) * kc;
                     const int64_t qpos = q_pos0 + r;
                     int64_t lo = 0, hi = kc - 1;
-                    if (mask >= 1) hi = std::min<int64_t>(hi, qpos);
-                    if (mask == 2) lo = std::max<int64_t>(0, qpos - window + 1);
+                    if (mask == 3) {
+                        // the drafter's bidirectional window, src/dflash.hpp:339-344
+                        lo = std::max<int64_t>(0, qpos - window);
+                        hi = std::min<int64_t>(hi, qpos + window);
+                    } else {
+                        if (mask >= 1) hi = std::min<int64_t>(hi, qpos);
+                        if (mask == 2) lo = std::max<int64_t>(0, qpos - window + 1);
+                    }
                     for (int64_t j = 0; j < kc; ++j) yr[j] = 0.0;
                     if (hi < lo) continue;
                     double mx = -HUGE_VAL;

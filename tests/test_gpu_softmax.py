@@ -34,6 +34,9 @@ def visible(heads, q, kc, mask, window, q_pos0):
     qpos = q_pos0 + np.arange(q)[:, None]
     j = np.arange(kc)[None, :]
     v = np.ones((q, kc), bool)
+    if mask == 3:
+        v &= (j >= qpos - window) & (j <= qpos + window)
+        return np.broadcast_to(v, (heads, q, kc))
     if mask >= 1:
         v &= j <= qpos
     if mask == 2:
@@ -140,6 +143,16 @@ def test_split_two_kernel_nonfinite(prims):
     assert np.array_equal(y[bad], ref[bad])
     d = ulp_diff16(y[~bad], ref[~bad])
     assert d.max() <= 1
+
+
+@pytest.mark.parametrize("dt_out", (BF16, F32))
+def test_bidirectional_window(prims, dt_out):
+    """the drafter's bidirectional window (src/dflash.hpp:339-344): keys within
+    `window` of the query position on both sides, clipped to the block"""
+    y, ref = run(prims, 4, 16, 300, mask=O.MASK_BIWINDOW, window=40, q_pos0=-5, dt_out=dt_out)
+    check(y, ref, dt_out, visible(4, 16, 300, O.MASK_BIWINDOW, 40, -5))
+    y, ref = run(prims, 2, 8, 5000, mask=O.MASK_BIWINDOW, window=2100, q_pos0=2900, dt_out=dt_out)
+    check(y, ref, dt_out, visible(2, 8, 5000, O.MASK_BIWINDOW, 2100, 2900))
 
 
 def test_all_masked_row_is_zero(prims):

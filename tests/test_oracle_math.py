@@ -255,7 +255,8 @@ def np_softmax(s, vis):
 
 
 @pytest.mark.parametrize("mask,window,q0", ((O.MASK_NONE, 0, 0), (O.MASK_CAUSAL, 0, 0), (O.MASK_CAUSAL, 0, 100),
-                                            (O.MASK_WINDOW, 50, 200)))
+                                            (O.MASK_WINDOW, 50, 200), (O.MASK_BIWINDOW, 30, 10),
+                                            (O.MASK_BIWINDOW, 30, 280)))
 def test_softmax_vs_numpy(mask, window, q0):
     heads, q, k = 3, 64, 300
     x = O.rnd(RNG.normal(0, 30, (heads, q, k)), F32)
@@ -264,14 +265,18 @@ def test_softmax_vs_numpy(mask, window, q0):
     s = (x.astype(np.float32) * np.float32(scale)).astype(np.float64)
     qpos = q0 + np.arange(q)[:, None]
     j = np.arange(k)[None, :]
-    vis = np.ones((q, k), bool) if mask == O.MASK_NONE else (j <= qpos)
+    vis = np.ones((q, k), bool) if mask in (O.MASK_NONE, O.MASK_BIWINDOW) else (j <= qpos)
     if mask == O.MASK_WINDOW:
         vis &= j > qpos - window
+    if mask == O.MASK_BIWINDOW:
+        vis &= (j >= qpos - window) & (j <= qpos + window)
     ref = np_softmax(s, vis[None])
     assert np.all(y[:, ~vis] == 0.0)
     v = np.broadcast_to(vis, y.shape) & (ref > 1e-300)
     assert np.abs(y[v] / ref[v] - 1).max() < 1e-13
-    assert np.abs(y.sum(-1) - 1).max() < 1e-13
+    live = vis.any(-1)  # rows with no visible key are all zero
+    assert np.abs(y.sum(-1)[:, live] - 1).max() < 1e-13
+    assert np.all(y.sum(-1)[:, ~live] == 0.0)
 
 
 def test_softmax_softcap_and_16bit_scores():
