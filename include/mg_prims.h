@@ -34,6 +34,16 @@ typedef struct mg_ctx mg_ctx;
 
 enum mg_dtype { MG_F64 = 0, MG_BF16 = 1, MG_F16 = 2, MG_F32 = 3 };
 
+/* Flag OR-ed into a dtype argument, together with MG_F64 only: the reference's
+ * --hf-f32-compat mode (src/main.cpp:164-165; f64 runs only,
+ * src/muse_glimmer.hpp:951-955), which places stock HF's f32 upcasts inside an
+ * f64 run, bit for bit. Taken by mg_rmsnorm_rows, mg_residual_rmsnorm and
+ * mg_qk_norm_rope (rmsnorm_rows's f32 chain with mean_sq_f32,
+ * src/muse_glimmer.hpp:530-556, 581-594; 799-803 for the QK-norm), by
+ * mg_rope_table (the f32 inverse-frequency chain stored as double(float(v)),
+ * 634-657) and by mg_softmax_rows as dtype_in (the f32 softmax, 856-870). */
+enum { MG_F32_COMPAT = 0x100 };
+
 /* muse::NormKind (src/muse_glimmer.hpp:558-563) */
 enum mg_norm_kind { MG_NORM_CENTERED = 0, MG_NORM_PLAIN = 1, MG_NORM_WEIGHTLESS = 2 };
 
@@ -65,8 +75,9 @@ void *mg_get_stream(mg_ctx *ctx);
  * and bf16exec norm_rows (src/bf16exec.hpp:398-421); GPU k_rmsnorm_auto
  * (src/gpu/gpu_engine.cpp:285-390). Centered: x*rs*(1+w); Plain: x*rs*w;
  * Weightless: x*rs (w may be NULL); rs = 1/sqrt(mean(x^2)+eps), f64 internals,
- * one rounding to `dtype`. ldx/ldy: row strides in elements (0 = dim).
- * In place (y == x) is allowed. */
+ * one rounding to `dtype`. MG_F64 | MG_F32_COMPAT: the reference's f32 chain
+ * (mean_sq_f32, rs = 1.0f/sqrtf(ms + float(eps)), f32 products, y = double(v)).
+ * ldx/ldy: row strides in elements (0 = dim). In place (y == x) is allowed. */
 int mg_rmsnorm_rows(mg_ctx *ctx, int kind, const void *x, int64_t ldx, const void *w,
                     double eps, void *y, int64_t ldy, int64_t rows, int64_t dim, int dtype);
 
@@ -97,7 +108,8 @@ int mg_scale(mg_ctx *ctx, void *x, int64_t n, double s, int dtype);
 
 /* RoPE table [positions, head_dim/2] of cos and sin, stored at `dtype` —
  * muse::build_rope_table (src/muse_glimmer.hpp:625-674): f32 inverse-frequency
- * chain for bf16/f16/f32, f64 chain for f64; FDLIBM pow/cos/sin on the device. */
+ * chain for bf16/f16/f32, f64 chain for f64; FDLIBM pow/cos/sin on the device.
+ * MG_F64 | MG_F32_COMPAT: the f32 chain, entries stored as double(float(v)). */
 int mg_rope_table(mg_ctx *ctx, double theta, int64_t head_dim, int64_t positions, int dtype,
                   void *cos_out, void *sin_out);
 
@@ -123,7 +135,8 @@ int mg_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k, int64_t
  *   the caches are [cache_slots, k_heads, head_dim] (the ring of k_kv_append);
  *   two tokens of one call that map to one slot race, as in the reference.
  * Each step rounds to `dtype` exactly as mg_rmsnorm_rows, mg_scale and mg_rope
- * do, so the result is bit-identical to running them in sequence.
+ * do, so the result is bit-identical to running them in sequence
+ * (MG_F64 | MG_F32_COMPAT: the QK-norm takes the f32 chain, 801-803).
  * ldq/ldk/ldv: token strides in elements (0 = heads*head_dim). */
 int mg_qk_norm_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k, int64_t k_heads,
                     int64_t ldk, int64_t tokens, int64_t head_dim, double eps, double qk_scale,
@@ -137,6 +150,12 @@ int mg_qk_norm_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k,
  * apply_output_tail's op order (src/muse_glimmer.hpp:920-943; cap 0 = off),
  * masked keys get probability exactly 0, p = exp(s - max)/sum.
  * dtype_in: f32, bf16 or f16 scores; dtype_out: bf16, f16 or f32 probs.
+ * f64 scores (dtype_in MG_F64, dtype_out MG_F64): the twin's f64 softmax
+ * (845-848, 871-880), scale and softcap in f64, the sum in a fixed parallel
+ * order (within 1e-12 relative of the ascending loop). dtype_in
+ * MG_F64 | MG_F32_COMPAT: the f32 softmax of 856-870 bit for bit (f32 max,
+ * float(exp(double(float(s) - m))), the f32 sum in ascending key order,
+ * double(float(e) / sum)); no softcap.
  * Rows longer than one work-group's registers are split across work-groups
  * and merged in chunk order (the k_attn_decode_combine rule,
  * src/gpu/gpu_engine.cpp:1816-1857). */

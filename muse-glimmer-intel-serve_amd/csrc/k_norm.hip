@@ -21,6 +21,8 @@
 //               lane/wave order (deterministic, within 1e-16 relative of the
 //               twin's order; the bf16 output equals the twin's except where
 //               x*rs*w lies within that distance of a rounding boundary).
+// f64 storage with the f32-compat flag takes k_norm_f32compat, the
+// reference's --hf-f32-compat branch bit for bit (see the kernel).
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
 
@@ -166,6 +168,80 @@ namespace mg
         }
     }
 
+    // f32 division and square root, correctly rounded: the f64 operation
+    // rounded to f32 (53 >= 2*24 + 2, so the double rounding cannot differ)
+    MG_DEV float div_f32(float a, float b) { return float(double(a) / double(b)); }
+    MG_DEV float sqrt_f32(float a) { return float(__builtin_sqrt(double(a))); }
+
+    // The f32-compat branch of rmsnorm_rows over f64 storage
+    // (src/muse_glimmer.hpp:530-556, 581-594):
+    //   ms = mean_sq_f32(x) + float(eps)   eight f32 accumulators a_l over
+    //                                      i = l mod 8, the tree
+    //                                      ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)),
+    //                                      the n mod 8 tail in order, / float(n)
+    //   rs = 1.0f / sqrtf(ms)
+    //   y  = double(float(x)*rs [* (1.0f + float(w)) | * float(w)])
+    // every sum and product an f32 operation. Eight lanes per row, each
+    // touching only its own elements (i = l mod 8; lane 0 also the tail), so a
+    // residual update it stores is the value it reads back.
+    __global__ __launch_bounds__(256) void k_norm_f32compat(int kind, double *h, const double *__restrict__ x,
+                                                            int64_t ldh, int64_t ldx, const double *__restrict__ w,
+                                                            float eps, double *y, int64_t ldy, int64_t rows,
+                                                            int dim)
+    {
+        const int64_t r = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 3;
+        const int l = threadIdx.x & 7;
+        const bool live = r < rows;
+        double *hr = h + (live ? r : 0) * ldh;
+        const double *xr = x ? x + (live ? r : 0) * ldx : nullptr;
+        const int full = dim & ~7;
+        // the row's value at i, after the residual update h = h + x (f64: the
+        // twin's round_act at f64 is the identity)
+        auto val = [&](int i) {
+            double v = hr[i];
+            if (xr) {
+                v = v + xr[i];
+                hr[i] = v;
+            }
+            return float(v);
+        };
+        float a = 0.0f;
+        if (live) {
+#pragma unroll 8
+            for (int i = l; i < full; i += 8) {
+                const float f = val(i);
+                a = a + f * f;
+            }
+        }
+        const float s1 = a + __shfl_xor(a, 1, 64);   // a0+a1, a2+a3, ...
+        const float s2 = s1 + __shfl_xor(s1, 2, 64);  // (a0+a1)+(a2+a3), (a4+a5)+(a6+a7)
+        const float s3 = s2 + __shfl_xor(s2, 4, 64);  // the fixed tree
+        float rs = 0.0f;
+        if (live && l == 0) {
+            float tail = 0.0f;
+            for (int i = full; i < dim; ++i) {
+                const float f = val(i);
+                tail = tail + f * f;
+            }
+            rs = div_f32(1.0f, sqrt_f32(div_f32(s3 + tail, float(dim)) + eps));
+        }
+        rs = __shfl(rs, int(threadIdx.x & 56), 64);
+        if (!live) return;
+        double *yr = y + r * ldy;
+        auto out = [&](int i) {
+            const float v = float(hr[i]) * rs;
+            float o = v;
+            if (kind == 0)
+                o = v * (1.0f + float(w[i]));
+            else if (kind == 1)
+                o = v * float(w[i]);
+            yr[i] = double(o);
+        };
+        for (int i = l; i < full; i += 8) out(i);
+        if (l == 0)
+            for (int i = full; i < dim; ++i) out(i);
+    }
+
     template <class S, int VEC>
     void launch_tree(mg_ctx *c, int kind, void *h, const void *x, int64_t ldh, int64_t ldx,
                      const void *w, double eps, void *y, int64_t ldy, int64_t rows, int dim)
@@ -228,6 +304,16 @@ namespace mg
         need(h != nullptr && y != nullptr, "rmsnorm: NULL tensor");
         need(ldh >= dim && ldy >= dim && (!x || ldx >= dim), "rmsnorm: leading dimension < dim");
         if (rows == 0) return;
+        if (dt & kF32Compat) {
+            need(dt == (F64 | kF32Compat), "rmsnorm: the f32-compat chain takes f64 storage only");
+            need(rows <= (int64_t(1) << 28), "rmsnorm: too many rows");
+            const unsigned blocks = unsigned((rows + 31) / 32); // 8 lanes per row
+            hipLaunchKernelGGL(k_norm_f32compat, dim3(blocks), dim3(256), 0, c->stream, kind, static_cast<double *>(h),
+                               static_cast<const double *>(x), ldh, ldx, static_cast<const double *>(w),
+                               float(eps), static_cast<double *>(y), ldy, rows, int(dim));
+            check_launch("k_norm_f32compat");
+            return;
+        }
         switch (dt) {
         case BF16: launch_norm_t<SBf16>(c, kind, h, x, ldh, ldx, w, eps, y, ldy, rows, int(dim)); break;
         case F16: launch_norm_t<SF16>(c, kind, h, x, ldh, ldx, w, eps, y, ldy, rows, int(dim)); break;

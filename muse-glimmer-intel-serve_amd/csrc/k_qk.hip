@@ -16,7 +16,12 @@
 // 16-byte loads; eight lanes per row run mean_sq's eight interleaved f64
 // accumulators in the reference order and its fixed tree (bit-identical rs);
 // then every thread takes (lo, hi) pairs of a row: normalize, scale, rotate,
-// store back and append to the caches.
+// store back and append to the caches. With the f32-compat flag (f64 storage)
+// the norm takes the f32 chain of rmsnorm_rows (src/muse_glimmer.hpp:530-556,
+// 581-594): f32 accumulators in the same order and tree, rs = 1.0f/sqrtf(ms),
+// x = double(float(x) * rs); the scale and the rotation stay f64.
+#include <type_traits>
+
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
 
@@ -31,7 +36,7 @@ namespace mg
         double eps;
     };
 
-    template <class S, int VEC>
+    template <class S, int VEC, bool C>
     __global__ __launch_bounds__(256) void k_qk_norm_rope(typename S::raw *q, typename S::raw *k,
                                                           const typename S::raw *__restrict__ v, QkArgs a,
                                                           typename S::comp qs,
@@ -80,24 +85,41 @@ namespace mg
         {
             const int rr = threadIdx.x >> 3, l = threadIdx.x & 7;
             const int full = D & ~7;
-            double acc = 0.0;
+            // the accumulator type: f64 (mean_sq), f32 for the compat chain (mean_sq_f32)
+            using acc_t = std::conditional_t<C, float, double>;
+            acc_t acc = 0;
             if (rr < nr)
                 for (int i = l; i < full; i += 8) {
-                    const double x = double(S::dec(st[rr * SD + i]));
-                    acc += x * x;
+                    const acc_t x = acc_t(S::dec(st[rr * SD + i]));
+                    acc = acc + x * x;
                 }
-            const double s1 = acc + __shfl_xor(acc, 1, 64);
-            const double s2 = s1 + __shfl_xor(s1, 2, 64);
-            const double s3 = s2 + __shfl_xor(s2, 4, 64);
+            const acc_t s1 = acc + __shfl_xor(acc, 1, 64);
+            const acc_t s2 = s1 + __shfl_xor(s1, 2, 64);
+            const acc_t s3 = s2 + __shfl_xor(s2, 4, 64);
             if (rr < nr && l == 0) {
-                double tail = 0.0;
+                acc_t tail = 0;
                 for (int i = full; i < D; ++i) {
-                    const double x = double(S::dec(st[rr * SD + i]));
-                    tail += x * x;
+                    const acc_t x = acc_t(S::dec(st[rr * SD + i]));
+                    tail = tail + x * x;
                 }
-                rsq[rr] = 1.0 / __builtin_sqrt((s3 + tail) / double(D) + a.eps);
+                if constexpr (C) {
+                    // f32 quotient, sum, sqrt and reciprocal, each correctly
+                    // rounded (the f64 operation rounded to f32: 53 >= 2*24 + 2)
+                    const float ms = float(double(s3 + tail) / double(D)) + float(a.eps);
+                    const float sq = float(__builtin_sqrt(double(ms)));
+                    rsq[rr] = double(float(1.0 / double(sq)));
+                } else {
+                    rsq[rr] = 1.0 / __builtin_sqrt((s3 + tail) / double(D) + a.eps);
+                }
             }
         }
+        // x * rs: f64 (or at the storage format), f32 in the compat chain
+        auto nrm = [](typename S::raw x, double rs) -> typename S::raw {
+            if constexpr (C)
+                return S::enc64(double(float(S::dec(x)) * float(rs)));
+            else
+                return S::enc64(double(S::dec(x)) * rs);
+        };
         __syncthreads();
 
         // (lo, hi) pairs, VEC at a time when the halves allow 16-byte
@@ -142,8 +164,8 @@ namespace mg
                 } else {
 #pragma unroll
                     for (int e = 0; e < PV; ++e) {
-                        raw l = S::enc64(double(S::dec(lo.v[e])) * rs);
-                        raw h = S::enc64(double(S::dec(hi.v[e])) * rs);
+                        raw l = nrm(lo.v[e], rs);
+                        raw h = nrm(hi.v[e], rs);
                         if (isq) {
                             l = S::enc(S::dec(l) * qs);
                             h = S::enc(S::dec(h) * qs);
@@ -173,8 +195,8 @@ namespace mg
             const int rr = idx / half, j = idx - rr * half;
             const bool isq = risq[rr] != 0;
             const double rs = rsq[rr];
-            raw lo = S::enc64(double(S::dec(st[rr * SD + j])) * rs);
-            raw hi = S::enc64(double(S::dec(st[rr * SD + j + half])) * rs);
+            raw lo = nrm(st[rr * SD + j], rs);
+            raw hi = nrm(st[rr * SD + j + half], rs);
             if (isq) {
                 lo = S::enc(S::dec(lo) * qs);
                 hi = S::enc(S::dec(hi) * qs);
@@ -197,7 +219,7 @@ namespace mg
         }
     }
 
-    template <class S>
+    template <class S, bool C = false>
     void launch_qk_t(mg_ctx *c, void *q, void *k, const void *v, const QkArgs &a, double qk_scale, const void *co,
                      const void *si, const int64_t *pos, void *kc, void *vc)
     {
@@ -219,9 +241,9 @@ namespace mg
                                static_cast<raw *>(kc), static_cast<raw *>(vc));
         };
         if (vec)
-            go(k_qk_norm_rope<S, V16>);
+            go(k_qk_norm_rope<S, V16, C>);
         else
-            go(k_qk_norm_rope<S, 1>);
+            go(k_qk_norm_rope<S, 1, C>);
         check_launch("k_qk_norm_rope");
     }
 
@@ -250,6 +272,7 @@ namespace mg
         case F16: launch_qk_t<SF16>(c, q, k, v, a, qk_scale, co, si, pos, kc, vc); break;
         case F32: launch_qk_t<SF32>(c, q, k, v, a, qk_scale, co, si, pos, kc, vc); break;
         case F64: launch_qk_t<SF64>(c, q, k, v, a, qk_scale, co, si, pos, kc, vc); break;
+        case F64 | kF32Compat: launch_qk_t<SF64, true>(c, q, k, v, a, qk_scale, co, si, pos, kc, vc); break;
         default: fail("qk_norm_rope: unknown dtype " + std::to_string(dt));
         }
     }

@@ -4,7 +4,8 @@
 // device with the FDLIBM pow/cos/sin that the twin uses, so every entry is
 // bit-identical to the reference's host table. bf16/f16/f32 follow the f32
 // inverse-frequency chain (f32 exponent, f32 reciprocal, f32 angle), f64 the
-// pure f64 chain.
+// pure f64 chain, f64 with the f32-compat flag the f32 chain with entries
+// stored as double(float(v)) (src/muse_glimmer.hpp:654-657).
 //
 // Application: muse::apply_rope (src/muse_glimmer.hpp:681-705) over (token, head)
 // as muse_glimmer.hpp:809-819 drives it:
@@ -20,7 +21,7 @@
 
 namespace mg
 {
-    template <class S>
+    template <class S, bool C>
     __global__ __launch_bounds__(256) void k_rope_table(double theta, int dim, int64_t T,
                                                         typename S::raw *__restrict__ co,
                                                         typename S::raw *__restrict__ si)
@@ -31,7 +32,7 @@ namespace mg
         const int64_t t = idx / half;
         const int j = int(idx - t * half);
         double cv, sv;
-        if (S::dt != F64) {
+        if (S::dt != F64 || C) {
             const float e = float(2 * j) / float(dim);
             const float pw = float(mgm::pow(double(float(theta)), double(e)));
             const float inv = 1.0f / pw;
@@ -43,6 +44,10 @@ namespace mg
             const double ang = double(t) * inv;
             cv = mgm::cos(ang);
             sv = mgm::sin(ang);
+        }
+        if (C) {
+            cv = double(float(cv));
+            sv = double(float(sv));
         }
         co[idx] = S::enc64(cv);
         si[idx] = S::enc64(sv);
@@ -57,10 +62,11 @@ namespace mg
         const int64_t n = T * (dim / 2);
         const unsigned blocks = unsigned((n + 255) / 256);
         switch (dt) {
-        case BF16: hipLaunchKernelGGL(k_rope_table<SBf16>, dim3(blocks), dim3(256), 0, c->stream, theta, int(dim), T, static_cast<uint16_t *>(co), static_cast<uint16_t *>(si)); break;
-        case F16: hipLaunchKernelGGL(k_rope_table<SF16>, dim3(blocks), dim3(256), 0, c->stream, theta, int(dim), T, static_cast<uint16_t *>(co), static_cast<uint16_t *>(si)); break;
-        case F32: hipLaunchKernelGGL(k_rope_table<SF32>, dim3(blocks), dim3(256), 0, c->stream, theta, int(dim), T, static_cast<float *>(co), static_cast<float *>(si)); break;
-        case F64: hipLaunchKernelGGL(k_rope_table<SF64>, dim3(blocks), dim3(256), 0, c->stream, theta, int(dim), T, static_cast<double *>(co), static_cast<double *>(si)); break;
+        case BF16: hipLaunchKernelGGL((k_rope_table<SBf16, false>), dim3(blocks), dim3(256), 0, c->stream, theta, int(dim), T, static_cast<uint16_t *>(co), static_cast<uint16_t *>(si)); break;
+        case F16: hipLaunchKernelGGL((k_rope_table<SF16, false>), dim3(blocks), dim3(256), 0, c->stream, theta, int(dim), T, static_cast<uint16_t *>(co), static_cast<uint16_t *>(si)); break;
+        case F32: hipLaunchKernelGGL((k_rope_table<SF32, false>), dim3(blocks), dim3(256), 0, c->stream, theta, int(dim), T, static_cast<float *>(co), static_cast<float *>(si)); break;
+        case F64: hipLaunchKernelGGL((k_rope_table<SF64, false>), dim3(blocks), dim3(256), 0, c->stream, theta, int(dim), T, static_cast<double *>(co), static_cast<double *>(si)); break;
+        case F64 | kF32Compat: hipLaunchKernelGGL((k_rope_table<SF64, true>), dim3(blocks), dim3(256), 0, c->stream, theta, int(dim), T, static_cast<double *>(co), static_cast<double *>(si)); break;
         default: fail("rope_table: unknown dtype " + std::to_string(dt));
         }
         check_launch("k_rope_table");

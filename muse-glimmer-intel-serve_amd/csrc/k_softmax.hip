@@ -40,21 +40,7 @@ namespace mg
     // visible key range [lo, hi] of the row
     MG_DEV void row_range(const SmArgs &a, int64_t row, int64_t &lo, int64_t &hi)
     {
-        const int64_t qpos = a.q_pos0 + row % a.q;
-        lo = 0;
-        hi = a.kc - 1;
-        if (a.mask == 3) {
-            // the drafter's bidirectional window (src/dflash.hpp:339-344)
-            const int64_t l = qpos - a.window, h = qpos + a.window;
-            lo = l > 0 ? l : 0;
-            hi = h < hi ? h : hi;
-            return;
-        }
-        if (a.mask >= 1) hi = qpos < hi ? qpos : hi;
-        if (a.mask == 2) {
-            const int64_t l = qpos - a.window + 1;
-            lo = l > 0 ? l : 0;
-        }
+        mask_range(a.mask, a.q_pos0 + row % a.q, a.kc, a.window, lo, hi);
     }
 
     // score transform: scale (and softcap) with the input dtype's materializations
@@ -570,11 +556,16 @@ namespace mg
         a.mask = mask;
         a.window = window;
         a.q_pos0 = q_pos0;
+        if (dt_in == F64 || dt_in == (F64 | kF32Compat)) {
+            need(dt_out == F64, "softmax: f64 scores give f64 probabilities");
+            launch_softmax_f64(c, x, y, heads * q, q, kc, scale, mask, window, q_pos0, softcap, dt_in != F64);
+            return;
+        }
         switch (dt_in) {
         case F32: launch_softmax_out<SF32>(c, x, y, a, dt_out); break;
         case BF16: launch_softmax_out<SBf16>(c, x, y, a, dt_out); break;
         case F16: launch_softmax_out<SF16>(c, x, y, a, dt_out); break;
-        default: fail("softmax: input dtype must be f32, bf16 or f16");
+        default: fail("softmax: input dtype must be f32, bf16, f16 or f64");
         }
     }
 } // namespace mg

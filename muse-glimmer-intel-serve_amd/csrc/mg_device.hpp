@@ -12,6 +12,31 @@
 namespace mg
 {
     enum Dt : int { F64 = 0, BF16 = 1, F16 = 2, F32 = 3 };
+    // OR-ed into an f64 dtype: the reference's --hf-f32-compat chains
+    constexpr int kF32Compat = 0x100;
+
+    // Visible keys [lo, hi] of a score row at position qpos over kc keys
+    // (hi < lo: none). mask 1 causal: j <= qpos; 2 sliding window:
+    // qpos - window < j <= qpos (src/muse_glimmer.hpp:838-843); 3 the drafter's
+    // bidirectional window: qpos - window <= j <= qpos + window
+    // (src/dflash.hpp:339-344).
+    __host__ __device__ __forceinline__ void mask_range(int mask, int64_t qpos, int64_t kc, int64_t window,
+                                                        int64_t &lo, int64_t &hi)
+    {
+        lo = 0;
+        hi = kc - 1;
+        if (mask == 3) {
+            const int64_t l = qpos - window, h = qpos + window;
+            lo = l > 0 ? l : 0;
+            hi = h < hi ? h : hi;
+            return;
+        }
+        if (mask >= 1) hi = qpos < hi ? qpos : hi;
+        if (mask == 2) {
+            const int64_t l = qpos - window + 1;
+            lo = l > 0 ? l : 0;
+        }
+    }
 
     // ------------------------------------------------------------ rounding
     // f32 -> bf16 bits, RNE (the gfx950 v_cvt_pk_bf16_f32 conversion), NaN

@@ -71,6 +71,9 @@ namespace mg
     void launch_softmax(mg_ctx *c, const void *x, void *y, int64_t heads, int64_t q,
                         int64_t kc, double scale, int mask, int64_t window, int64_t q_pos0,
                         double softcap, int dt_in, int dt_out);
+    // k_softmax64.hip (f64 scores: the pure f64 and the f32-compat chains)
+    void launch_softmax_f64(mg_ctx *c, const void *x, void *y, int64_t rows, int64_t q, int64_t kc, double scale,
+                            int mask, int64_t window, int64_t q_pos0, double softcap, bool compat);
     // k_q8.hip
     void launch_dequant_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, void *out,
                              int64_t rows, int64_t in, int dt_out);

@@ -26,6 +26,7 @@ LIB_PATH = os.path.join(HERE, "libmgprims.so")
 HEADER = os.path.join(ROOT, "include", "mg_prims.h")
 
 F64, BF16, F16, F32 = 0, 1, 2, 3
+F32_COMPAT = 0x100  # with F64: the reference's --hf-f32-compat chains
 CENTERED, PLAIN, WEIGHTLESS = 0, 1, 2
 MASK_NONE, MASK_CAUSAL, MASK_WINDOW, MASK_BIWINDOW = 0, 1, 2, 3
 
@@ -97,6 +98,12 @@ def _dtype_code(t):
     return {torch.float64: F64, torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}[t.dtype]
 
 
+def _code(t, f32_compat=False):
+    """dtype code of t, with the f32-compat flag when asked (the library
+    accepts it with f64 storage only and raises otherwise)"""
+    return _dtype_code(t) | (F32_COMPAT if f32_compat else 0)
+
+
 def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
@@ -139,18 +146,19 @@ class Prims:
         return self.lib.mg_get_stream(self.h)
 
     # ------------------------------------------------------------- norms
-    def rmsnorm_rows(self, kind, X, w, eps, Y):
-        """muse::rmsnorm_rows (src/muse_glimmer.hpp:572-608); X, Y: [rows, dim]."""
+    def rmsnorm_rows(self, kind, X, w, eps, Y, f32_compat=False):
+        """muse::rmsnorm_rows (src/muse_glimmer.hpp:572-608); X, Y: [rows, dim].
+        f32_compat (f64 tensors): the --hf-f32-compat f32 chain."""
         rows, dim = X.shape
         self._check(self.lib.mg_rmsnorm_rows(self.h, kind, _ptr(X), X.stride(0), _ptr(w), eps, _ptr(Y),
-                                             Y.stride(0), rows, dim, _dtype_code(X)))
+                                             Y.stride(0), rows, dim, _code(X, f32_compat)))
 
-    def residual_rmsnorm(self, kind, h, x, w, eps, y):
+    def residual_rmsnorm(self, kind, h, x, w, eps, y, f32_compat=False):
         """h = rnd(h + x) in place, then y = norm(h)."""
         rows, dim = h.shape
         assert h.is_contiguous() and x.is_contiguous() and y.is_contiguous()
         self._check(self.lib.mg_residual_rmsnorm(self.h, kind, _ptr(h), _ptr(x), _ptr(w), eps, _ptr(y),
-                                                 rows, dim, _dtype_code(h)))
+                                                 rows, dim, _code(h, f32_compat)))
 
     def residual_add(self, h, x):
         self._check(self.lib.mg_residual_add(self.h, _ptr(h), _ptr(x), h.numel(), _dtype_code(h)))
@@ -166,12 +174,14 @@ class Prims:
         self._check(self.lib.mg_scale(self.h, _ptr(x), x.numel(), s, _dtype_code(x)))
 
     # --------------------------------------------------------------- rope
-    def build_rope_table(self, theta, head_dim, positions, dtype):
-        """muse::build_rope_table (src/muse_glimmer.hpp:625-674) -> (cos, sin) [positions, head_dim/2]."""
+    def build_rope_table(self, theta, head_dim, positions, dtype, f32_compat=False):
+        """muse::build_rope_table (src/muse_glimmer.hpp:625-674) -> (cos, sin) [positions, head_dim/2].
+        f32_compat (torch.float64): the f32 chain stored as double(float(v))."""
         import torch
         co = torch.empty((positions, head_dim // 2), dtype=dtype, device=f"cuda:{self.device}")
         si = torch.empty_like(co)
-        self._check(self.lib.mg_rope_table(self.h, theta, head_dim, positions, _dtype_code(co), _ptr(co), _ptr(si)))
+        self._check(self.lib.mg_rope_table(self.h, theta, head_dim, positions, _code(co, f32_compat), _ptr(co),
+                                           _ptr(si)))
         return co, si
 
     def apply_rope(self, q, k, cos, sin, positions=None, pos0=0):
@@ -183,7 +193,7 @@ class Prims:
                                      cos.shape[0], _ptr(positions), pos0, _dtype_code(q)))
 
     def qk_norm_rope(self, q, k, eps, qk_scale, cos=None, sin=None, positions=None, pos0=0, v=None,
-                     k_cache=None, v_cache=None):
+                     k_cache=None, v_cache=None, f32_compat=False):
         """The sequence around RoPE in one pass (src/muse_glimmer.hpp:799-819): weight-less
         QK-norm over head_dim, q *= qk_scale, RoPE (when a table is given), and the KV-cache
         append k_cache/v_cache [slots, Hk, D] at row position % slots (k_kv_append)."""
@@ -193,7 +203,8 @@ class Prims:
         self._check(self.lib.mg_qk_norm_rope(
             self.h, _ptr(q), qh, q.stride(0), _ptr(k), kh, k.stride(0) if k is not None else 0, T, D, eps,
             qk_scale, _ptr(cos), _ptr(sin), cos.shape[0] if cos is not None else 0, _ptr(positions), pos0,
-            _ptr(v), v.stride(0) if v is not None else 0, _ptr(k_cache), _ptr(v_cache), slots, _dtype_code(q)))
+            _ptr(v), v.stride(0) if v is not None else 0, _ptr(k_cache), _ptr(v_cache), slots,
+            _code(q, f32_compat)))
 
     def attn_prefill(self, q, k_cache, v_cache, pos0, scaling, window=0, out=None):
         """Attention of a prompt chunk over the KV ring (the flash-prefill tier,
@@ -221,12 +232,13 @@ class Prims:
         return out
 
     # ------------------------------------------------------------ softmax
-    def softmax_rows(self, x, y, scale, mask=MASK_NONE, window=0, q_pos0=0, softcap=0.0):
-        """x [heads, q, k] scores -> y probabilities (attention_forward's softmax, src/muse_glimmer.hpp:828-885)."""
+    def softmax_rows(self, x, y, scale, mask=MASK_NONE, window=0, q_pos0=0, softcap=0.0, f32_compat=False):
+        """x [heads, q, k] scores -> y probabilities (attention_forward's softmax, src/muse_glimmer.hpp:828-885).
+        f64 x and y: the twin's f64 softmax, or with f32_compat its --hf-f32-compat f32 chain (856-870)."""
         heads, q, kc = x.shape
         assert x.is_contiguous() and y.is_contiguous()
         self._check(self.lib.mg_softmax_rows(self.h, _ptr(x), _ptr(y), heads, q, kc, scale, mask, window, q_pos0,
-                                             softcap, _dtype_code(x), _dtype_code(y)))
+                                             softcap, _code(x, f32_compat), _dtype_code(y)))
 
     def apply_output_tail(self, z, mult, cap):
         """muse::apply_output_tail (src/muse_glimmer.hpp:920-943), in place."""

@@ -13,19 +13,25 @@
 //
 // Dtype codes: 0 = f64, 1 = bf16, 2 = f16 (prec::Dtype order, rounding.hpp:31-36),
 // 3 = f32 (this build's extra storage type; rounding = one f64->f32 RNE).
+// Flag 0x100 OR-ed into an f64 code: the --hf-f32-compat chains (norm, RoPE
+// table, softmax), src/main.cpp:164-165, muse_glimmer.hpp:951-955.
 //
 // Pinning (what checks each part independently of this restatement):
 //   rounding      exhaustive over all 2^16 bf16/f16 patterns + crafted f32 ties,
 //                 bitwise vs oracle/_ref (reference rounding.hpp compiled)
 //   fmath         bitwise vs oracle/_ref (reference fmath.hpp compiled), ulp vs libm
-//   mean_sq/norm  bitwise vs oracle/_ref (reference rmsnorm_rows compiled)
-//   rope          bitwise vs oracle/_ref (reference build_rope_table/apply_rope)
+//   mean_sq/norm  bitwise vs oracle/_ref (reference rmsnorm_rows compiled),
+//                 the f32-compat branch included
+//   rope          bitwise vs oracle/_ref (reference build_rope_table/apply_rope),
+//                 the f32-compat table included
 //   silu/sigmoid  bitwise vs oracle/_ref (reference ok_siluv/ok_sigmoidv)
 //   output tail   bitwise vs oracle/_ref (reference apply_output_tail)
 //   residual/swiglu/gate loops: composition of the pinned pieces, plus
 //                 brute-force f64 identities in tests
 //   softmax       invariants (sum 1, masked exactly 0, shift invariance) and an
-//                 independent numpy f64 brute force in tests
+//                 independent numpy f64 brute force in tests; the f32-compat
+//                 chain by known answers that only the ascending f32 sum gives
+//                 and by a numpy float32 restatement
 //   q8_0 dequant  exactness argument + brute force in tests (no CPU dequant
 //                 exists in the reference; formula from gpu_engine.cpp:1117-1171)
 //   q8_0 quantize parity unpinned against llama.cpp (not vendored); checked
@@ -47,6 +53,7 @@
 namespace orc
 {
     enum Dt : int { F64 = 0, BF16 = 1, F16 = 2, F32 = 3 };
+    constexpr int COMPAT = 0x100; // f64 with the f32-compat chains
 
     // ---------------------------------------------------------------- rounding
     // rounding.hpp:64-75 — f64 -> f32 (hardware RNE) -> bf16 (c10 RNE), NaN -> 0x7FC0
@@ -148,9 +155,44 @@ namespace orc
     enum Norm : int { CENTERED = 0, PLAIN = 1, WEIGHTLESS = 2 };
 
     // muse_glimmer.hpp:572-608 (pure / twin branch: f64 internals, one rounding)
+    // muse_glimmer.hpp:530-556 — mean_sq_f32: the same order in f32
+    inline float mean_sq_f32(const double *x, int64_t n)
+    {
+        float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int64_t i = 0;
+        for (; i + 8 <= n; i += 8)
+            for (int l = 0; l < 8; ++l) {
+                const float v = float(x[i + l]);
+                a[l] += v * v;
+            }
+        float tail = 0;
+        for (; i < n; ++i) {
+            const float v = float(x[i]);
+            tail += v * v;
+        }
+        return ((((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail) / float(n);
+    }
+
+    // muse_glimmer.hpp:581-594 — the f32_compat branch (f64 storage)
+    inline void norm_row_f32(int kind, const double *x, const double *w, double eps, double *y, int64_t dim)
+    {
+        const float ms = mean_sq_f32(x, dim) + float(eps);
+        const float rs = 1.0f / std::sqrt(ms);
+        for (int64_t i = 0; i < dim; ++i) {
+            float v = float(x[i]) * rs;
+            if (kind == CENTERED) v = v * (1.0f + float(w[i]));
+            else if (kind == PLAIN) v = v * float(w[i]);
+            y[i] = double(v);
+        }
+    }
+
     inline void norm_row(int kind, const double *x, const double *w, double eps, double *y,
                          int64_t dim, int dt)
     {
+        if (dt == (F64 | COMPAT)) {
+            norm_row_f32(kind, x, w, eps, y, dim);
+            return;
+        }
         const double rs = 1.0 / std::sqrt(mean_sq(x, dim) + eps);
         for (int64_t i = 0; i < dim; ++i) {
             double v = x[i] * rs;
@@ -274,7 +316,7 @@ extern "C"
         for (int64_t r = 0; r < rows; ++r) {
             double *hr = h + r * dim;
             const double *xr = x + r * dim;
-            for (int64_t i = 0; i < dim; ++i) hr[i] = rnd(dt, hr[i] + xr[i]);
+            for (int64_t i = 0; i < dim; ++i) hr[i] = rnd(dt & 0xff, hr[i] + xr[i]);
             norm_row(kind, hr, w, eps, Y + r * dim, dim, dt);
         }
     }
@@ -315,10 +357,12 @@ extern "C"
     // muse_glimmer.hpp:625-674 — build_rope_table(c, T, f32_compat, dt). The f32
     // chain runs when dt != f64 (or f32_compat); with dt == f32 the table is
     // stored at f32 (the f32_compat branch, 654-656).
+    // With dt = f64 | COMPAT: the f32 chain, entries double(float(v)) (654-657).
     void or_rope_table(double theta, int64_t dim, int64_t T, int dt, double *cos_out, double *sin_out)
     {
         const int64_t half = dim / 2;
         if (dt != F64) {
+            const int st = dt == (F64 | COMPAT) ? F32 : dt; // double(float(v)) is rnd at f32
             std::vector<float> inv(static_cast<size_t>(half));
             for (int64_t j = 0; j < half; ++j) {
                 const float e = float(2 * j) / float(dim);
@@ -330,8 +374,8 @@ extern "C"
                 for (int64_t j = 0; j < half; ++j) {
                     const float ang = float(t) * inv[size_t(j)];
                     const double cv = orc::cos(double(ang)), sv = orc::sin(double(ang));
-                    cos_out[t * half + j] = rnd(dt, cv);
-                    sin_out[t * half + j] = rnd(dt, sv);
+                    cos_out[t * half + j] = rnd(st, cv);
+                    sin_out[t * half + j] = rnd(st, sv);
                 }
             return;
         }
@@ -401,6 +445,9 @@ extern "C"
     //   m = max, e = exp(s - m) (FDLIBM, f64), ascending f64 sum, p = e / sum,
     //   output rounded once to dt_out (the `.to(query.dtype)` of 866-868).
     // A row with no unmasked key writes zeros.
+    // dt_in = f64 | COMPAT: the f32 chain of 856-870 on the f64 scores s
+    // (dt_out f64): m32 = std::max over float(s), e = float(exp(double(float(s)
+    // - m32))), sum32 += e in ascending key order, p = double(float(e) / sum32).
     void or_softmax_rows(const double *x, double *y, int64_t heads, int64_t q, int64_t kc,
                          double scale, int mask, int64_t window, int64_t q_pos0, double softcap,
                          int dt_in, int dt_out)
@@ -429,6 +476,19 @@ extern "C"
                     }
                     for (int64_t j = 0; j < kc; ++j) yr[j] = 0.0;
                     if (hi < lo) continue;
+                    if (dt_in == (F64 | COMPAT)) {
+                        for (int64_t j = lo; j <= hi; ++j) s[size_t(j)] = xr[j] * scale;
+                        float m32 = -HUGE_VALF;
+                        for (int64_t j = lo; j <= hi; ++j) m32 = std::max(m32, float(s[size_t(j)]));
+                        float sum32 = 0;
+                        for (int64_t j = lo; j <= hi; ++j) {
+                            const float e = float(orc::exp(double(float(s[size_t(j)]) - m32)));
+                            s[size_t(j)] = e;
+                            sum32 += e;
+                        }
+                        for (int64_t j = lo; j <= hi; ++j) yr[j] = double(float(s[size_t(j)]) / sum32);
+                        continue;
+                    }
                     double mx = -HUGE_VAL;
                     for (int64_t j = lo; j <= hi; ++j) {
                         double v = rnd(dt_in, xr[j] * sc);

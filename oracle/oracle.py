@@ -22,6 +22,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 F64, BF16, F16, F32 = 0, 1, 2, 3
+F32_COMPAT = 0x100  # OR-ed into F64: the --hf-f32-compat chains (norm, RoPE table, softmax)
 CENTERED, PLAIN, WEIGHTLESS = 0, 1, 2
 MASK_NONE, MASK_CAUSAL, MASK_WINDOW, MASK_BIWINDOW = 0, 1, 2, 3
 

@@ -8,7 +8,8 @@ tools/oracle_kernels.cpp (the reference's referee library: fmath exp/tanh/
 sin/cos/pow, silu, sigmoid, the blocked-8 mean of squares) and
 oracle/ref_shim.cpp over src/rounding.hpp, src/safetensors.hpp and
 src/muse_glimmer.hpp (round_act, f16_to_f64, rmsnorm_rows, build_rope_table,
-apply_rope, apply_output_tail). Inputs come from the oracle's portable seeded
+apply_rope, apply_output_tail; rmsnorm_rows and build_rope_table also in
+their --hf-f32-compat branches). Inputs come from the oracle's portable seeded
 generator (splitmix64 + Box-Muller), stored in the fixtures as well, so the
 tests never regenerate them. Loops the reference writes inline (the residual
 add, SwiGLU) are composed here from its round_act and ok_siluv exactly as
@@ -95,6 +96,9 @@ def norms():
             xr, wr = R.round(x, dt), R.round(w, dt)
             for kind in (0, 1, 2):
                 out[f"y{dim}_k{kind}_d{dt}"] = R.rmsnorm_rows(kind, xr, None if kind == 2 else wr, 1e-6, dt)
+        for kind in (0, 1, 2):  # the --hf-f32-compat branch (f64 storage)
+            out[f"y{dim}_k{kind}_compat"] = R.rmsnorm_rows(kind, x, None if kind == 2 else w, 1e-6, F64,
+                                                           f32_compat=True)
     save("norms.npz", **out)
 
 
@@ -108,6 +112,8 @@ def rope():
             x = R.round(O.to_f64(O.normal(30 + dt, (T, dim), 0, 1, F64), F64), dt)
             out[f"x_{tag}_d{dt}"] = x
             out[f"rot_{tag}_d{dt}"] = np.stack([R.apply_rope_vec(x[t], c, s, t, dt) for t in range(T)])
+        c, s = R.rope_table(theta, dim, T, F64, f32_compat=True)  # the --hf-f32-compat table
+        out[f"cos_{tag}_compat"], out[f"sin_{tag}_compat"] = c, s
     save("rope.npz", **out)
 
 

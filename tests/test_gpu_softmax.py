@@ -179,5 +179,9 @@ def test_errors(prims):
     import torch
     x = torch.zeros((1, 1, 64), dtype=torch.float64, device="cuda:0")
     y = torch.zeros((1, 1, 64), dtype=torch.bfloat16, device="cuda:0")
-    with pytest.raises(mgprims.MgError, match="input dtype"):
+    with pytest.raises(mgprims.MgError, match="f64 probabilities"):
         prims.softmax_rows(x, y, 1.0)
+    # the compat flag goes with f64 scores only
+    xb = torch.zeros((1, 1, 64), dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(mgprims.MgError, match="input dtype"):
+        prims.softmax_rows(xb, y, 1.0, f32_compat=True)

@@ -63,6 +63,9 @@ def test_norms(dim):
         x, w = O.rnd(g[f"x{dim}"], dt), O.rnd(g[f"w{dim}"], dt)
         for kind in (0, 1, 2):
             assert eq(O.rmsnorm_rows(kind, x, w, 1e-6, dt), g[f"y{dim}_k{kind}_d{dt}"])
+    for kind in (0, 1, 2):
+        assert eq(O.rmsnorm_rows(kind, g[f"x{dim}"], g[f"w{dim}"], 1e-6, F64 | O.F32_COMPAT),
+                  g[f"y{dim}_k{kind}_compat"])
 
 
 @pytest.mark.parametrize("theta,dim,T", ((1e6, 128, 64), (5e5, 128, 48), (1e4, 64, 40)))
@@ -75,6 +78,8 @@ def test_rope(theta, dim, T):
         x = g[f"x_{tag}_d{dt}"]
         rot = O.apply_rope(x[:, None, :], c, s, np.arange(T), dt)[:, 0, :]
         assert eq(rot, g[f"rot_{tag}_d{dt}"])
+    c, s = O.rope_table(theta, dim, T, F64 | O.F32_COMPAT)
+    assert eq(c, g[f"cos_{tag}_compat"]) and eq(s, g[f"sin_{tag}_compat"])
 
 
 def test_output_tail():

@@ -296,6 +296,58 @@ def test_softmax_shift_invariance():
     assert np.abs(a / b - 1).max() < 1e-13
 
 
+def test_softmax_f64_scores_vs_numpy():
+    x = RNG.normal(0, 4, (2, 16, 200))
+    y = O.softmax_rows(x, 0.3, O.MASK_CAUSAL, 0, 150, 0.0, F64, F64)
+    qpos = 150 + np.arange(16)[:, None]
+    vis = np.arange(200)[None, :] <= qpos
+    ref = np_softmax(x * 0.3, vis[None])
+    v = np.broadcast_to(vis, y.shape)
+    assert np.all(y[~v] == 0.0)
+    assert np.abs(y[v] / ref[v] - 1).max() < 1e-13
+
+
+def _compat(x, scale=1.0, mask=O.MASK_NONE, window=0, q0=0):
+    return O.softmax_rows(np.asarray(x, np.float64), scale, mask, window, q0, 0.0, F64 | O.F32_COMPAT, F64)
+
+
+def test_softmax_f32_compat_known_answers():
+    """The --hf-f32-compat softmax (muse_glimmer.hpp:856-870) on rows whose
+    answer only its exact chain gives."""
+    # 1. the sum is one f32 chain in ascending key order: with e = float(exp(s))
+    #    just below 2^-24, 1 + e rounds back to 1 at every step, so the row
+    #    [0, s, ..., s] keeps sum32 = 1 and p[0] = 1 exactly; an f64 sum, a
+    #    pairwise sum or the descending order gives sum32 > 1
+    s32 = np.float32(-24 * math.log(2))
+    while O.exp(np.array([float(s32)]))[0].astype(np.float32) >= np.float32(2.0 ** -24):
+        s32 = np.nextafter(s32, np.float32(-np.inf))
+    e = float(np.float32(O.exp(np.array([float(s32)]))[0]))
+    assert 2.0 ** -25 < e < 2.0 ** -24
+    n = 1000
+    row = np.full(n + 1, float(s32))
+    row[0] = 0.0
+    y = _compat(row[None, None, :])[0, 0]
+    assert y[0] == 1.0 and np.all(y[1:] == e)
+    #    the reversed row adds the small terms first: sum32 > 1 + (n - 1) e
+    y = _compat(row[::-1].copy()[None, None, :])[0, 0]
+    assert y[-1] < 1.0 and abs(y[-1] * (1 + n * e) - 1) < 1e-6
+    # 2. the max and the differences are f32: scores that differ below f32
+    #    resolution become equal and split the mass exactly
+    y = _compat([[[1.0 + 1e-12, 1.0, 1.0 - 1e-12]]])[0, 0]
+    assert np.all(y == float(np.float32(1.0 / 3.0)))
+    p64 = O.softmax_rows(np.array([[[1.0 + 1e-12, 1.0]]]), 1.0, O.MASK_NONE, 0, 0, 0.0, F64, F64)[0, 0]
+    assert p64[0] != p64[1]
+    # 3. masked keys exactly 0, f32-valued outputs, within f32 error of f64
+    x = RNG.normal(0, 3, (2, 40, 120))
+    y = _compat(x, 0.7, O.MASK_WINDOW, 17, 60)
+    ref = O.softmax_rows(x, 0.7, O.MASK_WINDOW, 17, 60, 0.0, F64, F64)
+    assert np.array_equal(y, y.astype(np.float32).astype(np.float64))
+    assert np.all((y == 0.0) == (ref == 0.0))
+    nz = ref > 1e-30
+    assert np.abs(y[nz] / ref[nz] - 1).max() < 1e-5
+    assert not np.array_equal(y, ref)
+
+
 # --------------------------------------------------------------------- Q8_0
 def test_dequant_vs_numpy():
     qs = O.int8_uniform(1, (64, 256), -128, 127)

@@ -45,6 +45,12 @@ def test_rmsnorm(R, dim):
         for kind in (0, 1, 2):
             assert eq(O.rmsnorm_rows(kind, x, w, 1e-6, dt), R.rmsnorm_rows(kind, x, w, 1e-6, dt))
     assert eq(O.mean_sq(x), R.mean_sq(x))
+    # the f32-compat branch (f64 storage; mean_sq_f32 and the f32 chain)
+    x = RNG.normal(0, 3, (7, dim))
+    w = RNG.normal(1, 0.05, dim)
+    for kind in (0, 1, 2):
+        assert eq(O.rmsnorm_rows(kind, x, w, 1e-6, F64 | O.F32_COMPAT),
+                  R.rmsnorm_rows(kind, x, w, 1e-6, F64, f32_compat=True))
 
 
 @pytest.mark.parametrize("theta,dim,T", ((1e6, 128, 4096), (5e5, 128, 1024), (1e4, 256, 300)))
@@ -58,6 +64,9 @@ def test_rope(R, theta, dim, T):
         y = O.apply_rope(x, c, s, pos, dt)
         for t in range(16):
             assert eq(y[t, 0], R.apply_rope_vec(x[t, 0], c, s, int(pos[t]), dt))
+    c, s = O.rope_table(theta, dim, T, F64 | O.F32_COMPAT)
+    rc, rs = R.rope_table(theta, dim, T, F64, f32_compat=True)
+    assert eq(c, rc) and eq(s, rs)
 
 
 def test_output_tail(R):
