@@ -79,7 +79,7 @@ KERNEL_OF = {
     "softmax_decode": "k_softmax_partial_fast + k_softmax_finish_fast",
     "dequant_q8_0": "k_dequant_q8_0",
     "vocab_lse_argmax_top64": "k_vocab_chunk + k_vocab_merge",
-    "qk_norm_rope_kv": "k_qk_norm_rope",
+    "qk_norm_rope_kv": "k_qk_pairs",
     "quantize_q8_0": "k_quantize_q8_0",
     "attn_decode_131072": "k_attn_split<5,4> + k_attn_combine",
     "gemv_q8_0_decode": "k_gemv_q8_0<1>",

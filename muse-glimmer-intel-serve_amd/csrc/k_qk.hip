@@ -12,10 +12,11 @@
 // the result is bit-identical to running mg_rmsnorm_rows, mg_scale, mg_rope and
 // the two cache copies one after the other.
 //
-// A work-group takes 32 head rows (of q and k alike) staged in LDS with
+// Each wave takes 8 head rows (of q and k alike) on its own, with no
+// work-group barrier: the rows are staged in the wave's part of LDS with
 // 16-byte loads; eight lanes per row run mean_sq's eight interleaved f64
 // accumulators in the reference order and its fixed tree (bit-identical rs);
-// then every thread takes (lo, hi) pairs of a row: normalize, scale, rotate,
+// then every lane takes (lo, hi) pairs of a row: normalize, scale, rotate,
 // store back and append to the caches. With the f32-compat flag (f64 storage)
 // the norm takes the f32 chain of rmsnorm_rows (src/muse_glimmer.hpp:530-556,
 // 581-594): f32 accumulators in the same order and tree, rs = 1.0f/sqrtf(ms),
@@ -27,7 +28,8 @@
 
 namespace mg
 {
-    constexpr int kQkRows = 32;
+    constexpr int kQkRows = 32;    // head rows per work-group
+    constexpr int kQkWaveRows = 8; // head rows per wave (eight lanes per row for mean_sq)
 
     struct QkArgs
     {
@@ -52,43 +54,48 @@ namespace mg
         const int D = a.D, half = D / 2;
         const int SD = D + 16 / int(sizeof(raw)); // row stride: 16 bytes of padding against bank conflicts
         const int64_t heads = a.nq + a.nkv, rows = a.T * heads;
-        const int64_t r0 = int64_t(blockIdx.x) * kQkRows;
-        const int nr = int(rows - r0 < kQkRows ? rows - r0 : kQkRows);
+        // each wave owns kQkWaveRows rows of the group's kQkRows and works on
+        // them alone: no work-group barrier anywhere
+        const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        const int64_t r0 = int64_t(blockIdx.x) * kQkRows + wv * kQkWaveRows;
+        if (r0 >= rows) return; // the whole wave
+        const int nr = int(rows - r0 < kQkWaveRows ? rows - r0 : kQkWaveRows);
+        const int w0 = wv * kQkWaveRows; // the wave's slots in the per-row arrays
         // per row, once: its address, table position, and the cache row it
         // appends to (k rows with a cache and a position >= 0), or -1
         __shared__ raw *rptr[kQkRows];
         __shared__ const raw *vptr[kQkRows];
         __shared__ int64_t rpos[kQkRows], rcache[kQkRows];
         __shared__ int risq[kQkRows];
-        if (threadIdx.x < nr) {
-            const int64_t r = r0 + threadIdx.x, t = r / heads, hh = r - t * heads;
+        if (lane < nr) {
+            const int64_t r = r0 + lane, t = r / heads, hh = r - t * heads;
             const int64_t p = pos ? pos[t] : a.pos0 + t;
             const bool isq = hh < a.nq;
-            rptr[threadIdx.x] = isq ? q + t * a.ldq + hh * D : k + t * a.ldk + (hh - a.nq) * D;
-            vptr[threadIdx.x] = isq || !v ? nullptr : v + t * a.ldv + (hh - a.nq) * D;
-            rpos[threadIdx.x] = p;
-            risq[threadIdx.x] = isq;
-            rcache[threadIdx.x] = !isq && kc && p >= 0 ? (p % a.slots) * (a.nkv * D) + (hh - a.nq) * D : -1;
+            rptr[w0 + lane] = isq ? q + t * a.ldq + hh * D : k + t * a.ldk + (hh - a.nq) * D;
+            vptr[w0 + lane] = isq || !v ? nullptr : v + t * a.ldv + (hh - a.nq) * D;
+            rpos[w0 + lane] = p;
+            risq[w0 + lane] = isq;
+            rcache[w0 + lane] = !isq && kc && p >= 0 ? (p % a.slots) * (a.nkv * D) + (hh - a.nq) * D : -1;
         }
-        __syncthreads();
+        wave_lds_sync();
 
         // stage the head rows
         const int vpr = D / VEC;
-        for (int idx = threadIdx.x; idx < nr * vpr; idx += blockDim.x) {
-            const int rr = idx / vpr, i = (idx - rr * vpr) * VEC;
+        for (int idx = lane; idx < nr * vpr; idx += 64) {
+            const int rr = w0 + idx / vpr, i = (idx - (rr - w0) * vpr) * VEC;
             *reinterpret_cast<Vec<raw, VEC> *>(st + rr * SD + i) = *reinterpret_cast<const Vec<raw, VEC> *>(rptr[rr] + i);
         }
-        __syncthreads();
+        wave_lds_sync();
 
         // mean_sq (src/muse_glimmer.hpp:509-527): lane l of a row's 8-lane
         // group owns accumulator a_l
         {
-            const int rr = threadIdx.x >> 3, l = threadIdx.x & 7;
+            const int rr = w0 + (lane >> 3), l = lane & 7;
             const int full = D & ~7;
             // the accumulator type: f64 (mean_sq), f32 for the compat chain (mean_sq_f32)
             using acc_t = std::conditional_t<C, float, double>;
             acc_t acc = 0;
-            if (rr < nr)
+            if (rr < w0 + nr)
                 for (int i = l; i < full; i += 8) {
                     const acc_t x = acc_t(S::dec(st[rr * SD + i]));
                     acc = acc + x * x;
@@ -96,7 +103,7 @@ namespace mg
             const acc_t s1 = acc + __shfl_xor(acc, 1, 64);
             const acc_t s2 = s1 + __shfl_xor(s1, 2, 64);
             const acc_t s3 = s2 + __shfl_xor(s2, 4, 64);
-            if (rr < nr && l == 0) {
+            if (rr < w0 + nr && l == 0) {
                 acc_t tail = 0;
                 for (int i = full; i < D; ++i) {
                     const acc_t x = acc_t(S::dec(st[rr * SD + i]));
@@ -120,15 +127,15 @@ namespace mg
             else
                 return S::enc64(double(S::dec(x)) * rs);
         };
-        __syncthreads();
+        wave_lds_sync();
 
         // (lo, hi) pairs, VEC at a time when the halves allow 16-byte
         // accesses: normalize, scale q, rotate, store, append
         constexpr int PV = VEC;
         const int npv = half % PV == 0 ? half / PV : 0;
         if (npv) {
-            for (int idx = threadIdx.x; idx < nr * npv; idx += blockDim.x) {
-                const int rr = idx / npv, j = (idx - rr * npv) * PV;
+            for (int idx = lane; idx < nr * npv; idx += 64) {
+                const int rr = w0 + idx / npv, j = (idx - (rr - w0) * npv) * PV;
                 const bool isq = risq[rr] != 0;
                 const double rs = rsq[rr];
                 Vec<raw, PV> lo = *reinterpret_cast<const Vec<raw, PV> *>(st + rr * SD + j);
@@ -191,8 +198,8 @@ namespace mg
             }
             return;
         }
-        for (int idx = threadIdx.x; idx < nr * half; idx += blockDim.x) {
-            const int rr = idx / half, j = idx - rr * half;
+        for (int idx = lane; idx < nr * half; idx += 64) {
+            const int rr = w0 + idx / half, j = idx - (rr - w0) * half;
             const bool isq = risq[rr] != 0;
             const double rs = rsq[rr];
             raw lo = nrm(st[rr * SD + j], rs);
@@ -219,6 +226,150 @@ namespace mg
         }
     }
 
+    // 16-bit storage with head_dim 64, 128 or 256: RoPE's layout, one lane per
+    // 8-element piece of the first half and the matching piece of the second
+    // (TPR = head_dim / 16 lanes per head row), no LDS on the common path.
+    // Sum of squares: the square of a p-bit value is exact in f64, and when
+    // the row's nonzero magnitudes span few enough binades, 2 (emax - emin) +
+    // ceil(log2 D) + 2p <= 53, every partial sum in any order is exact (all
+    // are multiples of the smallest square's last bit and below 2^53 of it), so
+    // a butterfly over the row's lanes gives mean_sq's bits. A wave with a row
+    // outside that range (or holding inf or NaN) stages its rows in LDS and
+    // runs mean_sq's own order (eight interleaved accumulators, fixed tree).
+    template <class S, int TPR>
+    __global__ __launch_bounds__(256) void k_qk_pairs(typename S::raw *q, typename S::raw *k,
+                                                      const typename S::raw *__restrict__ v, QkArgs a,
+                                                      typename S::comp qs,
+                                                      const typename S::raw *__restrict__ co,
+                                                      const typename S::raw *__restrict__ si,
+                                                      const int64_t *__restrict__ pos, typename S::raw *kc,
+                                                      typename S::raw *vc)
+    {
+        using raw = typename S::raw;
+        constexpr int VEC = 8, D = 16 * TPR, half = D / 2, RPW = 64 / TPR;
+        constexpr int LOG2D = TPR == 4 ? 6 : TPR == 8 ? 7 : 8;
+        constexpr int MB = S::dt == BF16 ? 7 : 10;              // stored mantissa bits
+        constexpr int EALL = S::dt == BF16 ? 0xff : 0x1f;       // inf / NaN exponent field
+        constexpr int SPAN = (53 - LOG2D - 2 * (MB + 1)) / 2;   // binades the exact sum allows
+        __shared__ __align__(16) raw st[4][RPW][D + 8];
+        __shared__ double rsf[4][RPW];
+        const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+        const int64_t heads = a.nq + a.nkv, rows = a.T * heads;
+        const int64_t wrow0 = (int64_t(blockIdx.x) * 256 + wv * 64) / TPR; // the wave's first row
+        if (wrow0 >= rows) return; // the whole wave
+        const int64_t r = wrow0 + lane / TPR;
+        const int j = lane & (TPR - 1);
+        const bool live = r < rows;
+        const int64_t rc = live ? r : rows - 1; // addresses of a dead lane stay in bounds
+        const int64_t t = rows <= int64_t(0xffffffff) ? int64_t(uint32_t(rc) / uint32_t(heads)) : rc / heads;
+        const int hh = int(rc - t * heads);
+        const bool isq = hh < a.nq;
+        raw *x = isq ? q + t * a.ldq + int64_t(hh) * D : k + t * a.ldk + int64_t(hh - a.nq) * D;
+        Vec<raw, VEC> lo = ldv<raw, VEC>(x + VEC * j);
+        Vec<raw, VEC> hi = ldv<raw, VEC>(x + half + VEC * j);
+        const int64_t p = pos ? pos[t] : a.pos0 + t;
+
+        double ss = 0.0;
+        int emin = 0x7fff, emax = 0;
+#pragma unroll
+        for (int e = 0; e < 2 * VEC; ++e) {
+            const raw b = e < VEC ? lo.v[e] : hi.v[e - VEC];
+            const double d = double(S::dec(b));
+            ss += d * d;
+            const int u = b & 0x7fff, ef = u >> MB;
+            if (u) {
+                emin = min(emin, ef > 1 ? ef : 1);
+                emax = max(emax, ef);
+            }
+        }
+#pragma unroll
+        for (int m = 1; m < TPR; m <<= 1) {
+            ss += __shfl_xor(ss, m, 64);
+            emin = min(emin, __shfl_xor(emin, m, 64));
+            emax = max(emax, __shfl_xor(emax, m, 64));
+        }
+        const bool exact = emax == 0 || (emax < EALL && emax - emin <= SPAN);
+        double rs;
+        if (__builtin_amdgcn_ballot_w64(!exact) == 0) {
+            rs = 1.0 / __builtin_sqrt(ss / double(D) + a.eps);
+        } else {
+            // mean_sq's order (src/muse_glimmer.hpp:509-527) over the wave's rows
+            raw *sr = st[wv][lane / TPR];
+            *reinterpret_cast<Vec<raw, VEC> *>(sr + VEC * j) = lo;
+            *reinterpret_cast<Vec<raw, VEC> *>(sr + half + VEC * j) = hi;
+            wave_lds_sync();
+            for (int rw = lane >> 3; rw < RPW; rw += 8) {
+                const int l = lane & 7;
+                double acc = 0.0;
+                for (int i = l; i < D; i += 8) {
+                    const double d = double(S::dec(st[wv][rw][i]));
+                    acc += d * d;
+                }
+                const double s1 = acc + __shfl_xor(acc, 1, 64);
+                const double s2 = s1 + __shfl_xor(s1, 2, 64);
+                const double s3 = s2 + __shfl_xor(s2, 4, 64);
+                if (l == 0) rsf[wv][rw] = 1.0 / __builtin_sqrt(s3 / double(D) + a.eps);
+            }
+            wave_lds_sync();
+            rs = rsf[wv][lane / TPR];
+        }
+
+        const bool rot = co && p >= 0 && p < a.table_rows;
+        Vec<raw, VEC> cv, sv;
+        if (rot) {
+            cv = *reinterpret_cast<const Vec<raw, VEC> *>(co + p * half + VEC * j);
+            sv = *reinterpret_cast<const Vec<raw, VEC> *>(si + p * half + VEC * j);
+        }
+        if constexpr (S::dt == BF16) {
+            // NaN propagates through every step and the twin's NaN is the one
+            // pattern 0x7FC0: the steps round without NaN checks and the
+            // outputs are made canonical once
+            auto rn = [](float f) { return SBf16::enc_finite(f); };
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                raw l = rn(float(double(S::dec(lo.v[e])) * rs));
+                raw h = rn(float(double(S::dec(hi.v[e])) * rs));
+                if (isq) {
+                    l = rn(S::dec(l) * qs);
+                    h = rn(S::dec(h) * qs);
+                }
+                if (rot) {
+                    const float fl = S::dec(l), fh = S::dec(h), cc = S::dec(cv.v[e]), sn = S::dec(sv.v[e]);
+                    l = rn(S::dec(rn(fl * cc)) + S::dec(rn(-(fh * sn))));
+                    h = rn(S::dec(rn(fh * cc)) + S::dec(rn(fl * sn)));
+                }
+                lo.v[e] = S::dec(l) != S::dec(l) ? raw(0x7fc0) : l;
+                hi.v[e] = S::dec(h) != S::dec(h) ? raw(0x7fc0) : h;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                raw l = S::enc64(double(S::dec(lo.v[e])) * rs);
+                raw h = S::enc64(double(S::dec(hi.v[e])) * rs);
+                if (isq) {
+                    l = S::enc(S::dec(l) * qs);
+                    h = S::enc(S::dec(h) * qs);
+                }
+                if (rot) rope_pair<S>(l, h, cv.v[e], sv.v[e]);
+                lo.v[e] = l;
+                hi.v[e] = h;
+            }
+        }
+        if (!live) return;
+        stv<raw, VEC>(x + VEC * j, lo);
+        stv<raw, VEC>(x + half + VEC * j, hi);
+        if (!isq && kc && p >= 0) {
+            const int64_t o = (p % a.slots) * (a.nkv * D) + int64_t(hh - a.nq) * D + VEC * j;
+            stv<raw, VEC>(kc + o, lo);
+            stv<raw, VEC>(kc + o + half, hi);
+            if (vc) {
+                const raw *vr = v + t * a.ldv + int64_t(hh - a.nq) * D + VEC * j;
+                stv<raw, VEC>(vc + o, ldv<raw, VEC>(vr));
+                stv<raw, VEC>(vc + o + half, ldv<raw, VEC>(vr + half));
+            }
+        }
+    }
+
     template <class S, bool C = false>
     void launch_qk_t(mg_ctx *c, void *q, void *k, const void *v, const QkArgs &a, double qk_scale, const void *co,
                      const void *si, const int64_t *pos, void *kc, void *vc)
@@ -240,6 +391,27 @@ namespace mg
                                static_cast<const raw *>(co), static_cast<const raw *>(si), pos,
                                static_cast<raw *>(kc), static_cast<raw *>(vc));
         };
+        if constexpr (sizeof(raw) == 2) {
+            if (vec && (a.D == 64 || a.D == 128 || a.D == 256)) {
+                const int tpr = a.D / 16;
+                need(rows * tpr / 256 < (int64_t(1) << 31), "qk_norm_rope: too many rows");
+                const unsigned pblocks = unsigned((rows * tpr + 255) / 256);
+                auto gp = [&](auto kern) {
+                    hipLaunchKernelGGL(kern, dim3(pblocks), dim3(256), 0, c->stream, static_cast<raw *>(q),
+                                       static_cast<raw *>(k), static_cast<const raw *>(v), a, qs,
+                                       static_cast<const raw *>(co), static_cast<const raw *>(si), pos,
+                                       static_cast<raw *>(kc), static_cast<raw *>(vc));
+                };
+                if (tpr == 4)
+                    gp(k_qk_pairs<S, 4>);
+                else if (tpr == 8)
+                    gp(k_qk_pairs<S, 8>);
+                else
+                    gp(k_qk_pairs<S, 16>);
+                check_launch("k_qk_pairs");
+                return;
+            }
+        }
         if (vec)
             go(k_qk_norm_rope<S, V16, C>);
         else

@@ -122,6 +122,35 @@ def test_odd_shapes(prims):
     run_case(prims, F32, 5, 2, 2, 18, theta=1e4, pos0=3, slots=7)  # half = 9, scalar staging
 
 
+def wide_rows(seed, shape, dt, span):
+    """values +-m * 2^e with e drawn over `span` binades per row (some rows
+    also get exact zeros): the row sums of squares round in f64 once the
+    span passes the exact-sum bound, so only mean_sq's own order matches"""
+    rng = np.random.default_rng(seed)
+    m = rng.uniform(1.0, 2.0, shape) * rng.choice([-1.0, 1.0], shape)
+    e = rng.integers(-span // 2, span - span // 2 + 1, shape)
+    x = m * np.exp2(e)
+    x[..., ::17] = 0.0
+    return O.to_f64(O.from_f64(x, dt), dt)
+
+
+@pytest.mark.parametrize("dt", (BF16, F16))
+@pytest.mark.parametrize("dim", (64, 128, 256))
+def test_wide_magnitude_rows(prims, dt, dim):
+    """rows around and beyond the span where any summation order is exact
+    (the 16-bit kernel's fast sum), and far beyond it (its ordered fallback)"""
+    for span in (6, 11, 12, 13, 14, 15, 16, 17, 24):
+        T, qh, kh = 9, 4, 2
+        q = wide_rows(700 + span, (T, qh, dim), dt, span)
+        k = wide_rows(800 + span, (T, kh, dim), dt, span)
+        dq, dk = to_dev(O.from_f64(q, dt), dt), to_dev(O.from_f64(k, dt), dt)
+        rc, rs = O.rope_table(1e6, dim, T, dt)
+        prims.qk_norm_rope(dq, dk, EPS, QK, to_dev(O.from_f64(rc, dt), dt), to_dev(O.from_f64(rs, dt), dt))
+        eq, ek = oracle_seq(q, k, dt, 1e6, dim, T, np.arange(T), True)
+        assert same_bits(from_dev(dq, dt), O.from_f64(eq, dt)), span
+        assert same_bits(from_dev(dk, dt), O.from_f64(ek, dt)), span
+
+
 def test_errors(prims):
     import torch
     q = torch.zeros((2, 4, 128), dtype=torch.bfloat16, device="cuda:0")
