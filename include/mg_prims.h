@@ -186,8 +186,8 @@ int mg_dequant_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, void *out,
  * h / (q_heads / kv_heads). out f32 [tokens, q_heads, head_dim] (token stride
  * ldo, 0 = q_heads*head_dim). Tile-wise online softmax with bf16
  * probabilities in the p.v product, the reference tier's contract: a
- * numerical envelope, not bits. head_dim 64 or 128, at most 8 query heads per
- * kv head. */
+ * numerical envelope, not bits. head_dim 64 or 128; any number of query heads
+ * per kv head (groups of more than 8 are served by several work-groups). */
 int mg_attn_prefill(mg_ctx *ctx, const uint16_t *q, int64_t ldq, const uint16_t *k_cache, const uint16_t *v_cache,
                     int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t cache_slots,
                     int64_t pos0, int64_t window, double scaling, float *out, int64_t ldo);
@@ -199,8 +199,9 @@ int mg_attn_prefill(mg_ctx *ctx, const uint16_t *q, int64_t ldq, const uint16_t 
  * [cache_slots, kv_heads, head_dim] with key position j in slot j % cache_slots;
  * keys lo..q_pos, lo = window > 0 ? max(0, q_pos - window + 1) : 0 (at most
  * cache_slots of them); query head h reads kv head h / (q_heads / kv_heads).
- * out f32 [q_heads, head_dim] = softmax(q.k * scaling) v. head_dim 64 or 128,
- * at most 8 query heads per kv head. Like the reference's split-K path, a
+ * out f32 [q_heads, head_dim] = softmax(q.k * scaling) v. head_dim 64 or 128;
+ * any number of query heads per kv head (one wave serves up to 16). Like the
+ * reference's split-K path, a
  * numerical envelope rather than bits (f32 online softmax, split merge). */
 int mg_attn_decode(mg_ctx *ctx, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache, int64_t q_heads,
                    int64_t kv_heads, int64_t head_dim, int64_t cache_slots, int64_t q_pos, int64_t window,

@@ -12,8 +12,9 @@
 // not bits.
 //
 // MI355X layout of the work: one wave per (KV head, split) runs ALL the
-// query heads of its GQA group (5 for the 30B), so every K and V row is read
-// from HBM once, and both products run on the matrix cores
+// query heads of its GQA group (5 for the 30B-class config, 16 for 32 q / 2 kv
+// heads; larger groups take several waves of up to 16 heads), so every K and
+// V row is read from HBM once, and both products run on the matrix cores
 // (v_mfma_f32_16x16x32_bf16; lane l = 16c + n holds row/column n and
 // k-elements 8c..8c+7 of an operand, and C rows 4c..4c+3 of column n).
 // Per step of 32 keys:
@@ -47,10 +48,11 @@ namespace mg
     {
         int64_t nq, nkv, slots, qpos, lo, per;
         int nsplit;
-        float scale2; // scaling * log2(e)
+        int hpg, nsub; // query heads per kv head; waves per (kv head, split), HPG heads each
+        float scale2;  // scaling * log2(e)
     };
 
-    template <int HPG, int KB> // KB = head_dim / 32
+    template <int HPG, int KB> // HPG query heads per wave (<= 16), KB = head_dim / 32
     __global__ __launch_bounds__(256) void k_attn_split(const uint16_t *__restrict__ q,
                                                         const uint16_t *__restrict__ kc,
                                                         const uint16_t *__restrict__ vc, AttnArgs a,
@@ -65,10 +67,12 @@ namespace mg
         __shared__ __align__(16) uint16_t lv[4][32 * SV];
         const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
         const int64_t w = int64_t(blockIdx.x) * 4 + wv;
-        if (w >= a.nkv * a.nsplit) return; // whole wave; nothing below syncs the block
+        if (w >= a.nkv * a.nsub * a.nsplit) return; // whole wave; nothing below syncs the block
         // the kv heads of one split are neighbours: they read the same ring rows
-        const int sp = int(w / a.nkv);
-        const int64_t g = w - int64_t(sp) * a.nkv;
+        const int sp = int(w / (a.nkv * a.nsub));
+        const int64_t gs = w - int64_t(sp) * (a.nkv * a.nsub);
+        const int64_t g = gs / a.nsub;
+        const int64_t h0 = g * a.hpg + (gs - g * a.nsub) * HPG; // the wave's first query head
         const int64_t j0 = a.lo + int64_t(sp) * a.per;
         const int64_t j1 = j0 + a.per - 1 < a.qpos ? j0 + a.per - 1 : a.qpos;
         const int n = lane & 15, c = lane >> 4;
@@ -79,7 +83,7 @@ namespace mg
         bf16x8 qop[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
-            qop[kb] = n < HPG ? ld_bf16x8(q + (g * HPG + n) * D + 32 * kb + 8 * c) : zero8;
+            qop[kb] = n < HPG ? ld_bf16x8(q + (h0 + n) * D + 32 * kb + 8 * c) : zero8;
 
         f32x4 o[NT];
 #pragma unroll
@@ -205,7 +209,7 @@ namespace mg
         l = rows4_sum(l);
         const bool empty = j0 > j1;
         if (c == 0 && n < HPG) {
-            const int64_t base = (g * HPG + n) * a.nsplit + sp;
+            const int64_t base = (h0 + n) * a.nsplit + sp;
             pm[base] = empty ? -__builtin_huge_valf() : m;
             pl[base] = empty ? 0.0f : l;
         }
@@ -213,7 +217,7 @@ namespace mg
         for (int r = 0; r < 4; ++r) {
             const int hh = 4 * c + r;
             if (hh < HPG) {
-                float *dst = pa + ((g * HPG + hh) * a.nsplit + sp) * D + n;
+                float *dst = pa + ((h0 + hh) * a.nsplit + sp) * D + n;
 #pragma unroll
                 for (int t = 0; t < NT; ++t) dst[16 * t] = o[t][r];
             }
@@ -271,7 +275,11 @@ namespace mg
     {
         need(nq > 0 && nkv > 0 && nq % nkv == 0, "attn_decode: q_heads must be a multiple of kv_heads");
         const int64_t hpg = nq / nkv;
-        need(hpg <= 8, "attn_decode: at most 8 query heads per kv head");
+        // a wave serves up to 16 query heads (the MFMA's 16 columns); larger
+        // groups split over waves of the largest divisor <= 16
+        int64_t hw = hpg;
+        while (hw > 16 || hpg % hw != 0) --hw;
+        const int64_t nsub = hpg / hw;
         need(D == 64 || D == 128, "attn_decode: head_dim must be 64 or 128");
         need(q && kc && vc && out, "attn_decode: NULL tensor");
         need(aligned16(kc) && aligned16(vc) && aligned16(q), "attn_decode: tensors must be 16-byte aligned");
@@ -283,7 +291,7 @@ namespace mg
         // about one wave per SIMD, each streaming its keys with the next step's
         // loads in flight; a multiple of 32 keys (one step)
         int64_t ns = (total + kAttnSplit - 1) / kAttnSplit;
-        const int64_t ns_cap = kAttnWaves / nkv > 1 ? kAttnWaves / nkv : 1;
+        const int64_t ns_cap = kAttnWaves / (nkv * nsub) > 1 ? kAttnWaves / (nkv * nsub) : 1;
         ns = ns < ns_cap ? ns : ns_cap;
         int64_t per = (total + ns - 1) / ns;
         per = (per + 31) / 32 * 32;
@@ -293,14 +301,16 @@ namespace mg
         float *pm = static_cast<float *>(c->work);
         float *pl = pm + nq * nsplit;
         float *pa = pl + nq * nsplit;
-        const AttnArgs a{nq, nkv, slots, qpos, lo, per, nsplit, float(double(float(scaling)) * 1.4426950408889634)};
-        const dim3 g1{unsigned((nkv * nsplit + 3) / 4), 1u, 1u};
+        const AttnArgs a{nq, nkv, slots, qpos, lo, per, nsplit, int(hpg), int(nsub),
+                         float(double(float(scaling)) * 1.4426950408889634)};
+        need((nkv * nsub * nsplit + 3) / 4 < (int64_t(1) << 31), "attn_decode: too many heads");
+        const dim3 g1{unsigned((nkv * nsub * nsplit + 3) / 4), 1u, 1u};
         auto go = [&](auto kern) {
             hipLaunchKernelGGL(kern, g1, dim3(256), 0, c->stream, q, kc, vc, a, pm, pl, pa);
         };
 #define MG_ATTN_CASE(H)                                                                                             \
     case H: D == 128 ? go(k_attn_split<H, 4>) : go(k_attn_split<H, 2>); break;
-        switch (hpg) {
+        switch (hw) {
             MG_ATTN_CASE(1)
             MG_ATTN_CASE(2)
             MG_ATTN_CASE(3)
@@ -309,6 +319,14 @@ namespace mg
             MG_ATTN_CASE(6)
             MG_ATTN_CASE(7)
             MG_ATTN_CASE(8)
+            MG_ATTN_CASE(9)
+            MG_ATTN_CASE(10)
+            MG_ATTN_CASE(11)
+            MG_ATTN_CASE(12)
+            MG_ATTN_CASE(13)
+            MG_ATTN_CASE(14)
+            MG_ATTN_CASE(15)
+            MG_ATTN_CASE(16)
         default: fail("attn_decode: unsupported group size");
         }
 #undef MG_ATTN_CASE

@@ -14,18 +14,19 @@
 // schedule with bf16 probabilities in the second product, gated on an
 // envelope rather than bits.
 //
-// Layout of the work: a work-group of HPG waves serves one KV head and 32
-// query rows; wave w runs query head g * HPG + w, so every K/V tile staged in
-// LDS is used by the whole GQA group. Per 32-key step:
+// Layout of the work: a work-group serves one KV head, 32 query rows and up to
+// 8 query heads of its GQA group (two waves per head, one per 16-row tile), so
+// every K/V tile staged in LDS is used by all of them; larger groups (16 for
+// 32 q / 2 kv heads) take several work-groups. Per 64-key step:
 //   staging   coalesced 16-byte loads of the next step's K and V (whole 256-
 //             byte key rows per instruction), held in registers while this
 //             step computes, then written to the other LDS buffer (padded
 //             rows, conflict-free reads); one barrier per step;
-//   S^T       A = 16 keys x 32 dims of K from LDS, B = 16 query rows
-//             (registers): C lane (query n, c) holds keys 4c..4c+3 of the tile,
-//             two key tiles x two query tiles per step;
+//   S^T       A = 16 keys x 32 dims of K from LDS, B = the wave's 16 query
+//             rows (registers): C lane (query n, c) holds keys 4c..4c+3 of the
+//             tile, four key tiles per step;
 //   softmax   per query row in f32 (hardware exp2 on log2-scaled scores), the
-//             row max across the four lane groups by two shuffles;
+//             row max and sum across the four lane groups by permlane swaps;
 //   P V       A = P of two key tiles, straight from the S^T layout, B = V from
 //             LDS through the transposing ds_read_b64_tr_b16.
 // Work-groups of the last query tiles (the most keys) start first.
@@ -39,10 +40,11 @@ namespace mg
     struct PfArgs
     {
         int64_t T, nkv, ldq, ldo, slots, pos0, window, nqt;
-        float scale2; // scaling * log2(e)
+        int64_t hpg, nsub; // query heads per kv head; work-groups per (kv head, tile), HPG heads each
+        float scale2;      // scaling * log2(e)
     };
 
-    // HPG query heads per kv head, KB = head_dim / 32, RT 16-row tiles per
+    // HPG query heads per work-group, KB = head_dim / 32, RT 16-row tiles per
     // wave (the work-group has HPG * 2 / RT waves), KT 16-key tiles per step
     template <int HPG, int KB, int RT, int KT>
     __global__ __launch_bounds__(64 * HPG * 2 / RT) void k_attn_prefill(const uint16_t *__restrict__ q,
@@ -62,9 +64,11 @@ namespace mg
         const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
         const int n = lane & 15, c = lane >> 4;
         // the last query tiles attend the most keys: they start first
-        const int64_t qt = a.nqt - 1 - int64_t(blockIdx.x) / a.nkv;
-        const int64_t g = int64_t(blockIdx.x) - (int64_t(blockIdx.x) / a.nkv) * a.nkv;
-        const int64_t h = g * HPG + wv % HPG;
+        const int64_t per_tile = a.nkv * a.nsub;
+        const int64_t qt = a.nqt - 1 - int64_t(blockIdx.x) / per_tile;
+        const int64_t gs = int64_t(blockIdx.x) - (int64_t(blockIdx.x) / per_tile) * per_tile;
+        const int64_t g = gs / a.nsub;
+        const int64_t h = g * a.hpg + (gs - g * a.nsub) * HPG + wv % HPG;
         const int u0 = (wv / HPG) * RT;                           // this wave's first row tile
         const int64_t q0 = qt * kPfQ;                             // the work-group's first query row
         const int64_t qlast = (q0 + kPfQ < a.T ? q0 + kPfQ : a.T) - 1; // last live row
@@ -259,7 +263,11 @@ namespace mg
     {
         need(nq > 0 && nkv > 0 && nq % nkv == 0, "attn_prefill: q_heads must be a multiple of kv_heads");
         const int64_t hpg = nq / nkv;
-        need(hpg <= 8, "attn_prefill: at most 8 query heads per kv head");
+        // a work-group serves up to 8 query heads of one kv head (2 waves
+        // each); larger groups split over work-groups of the largest divisor <= 8
+        int64_t hw = hpg;
+        while (hw > 8 || hpg % hw != 0) --hw;
+        const int64_t nsub = hpg / hw;
         need(D == 64 || D == 128, "attn_prefill: head_dim must be 64 or 128");
         need(T >= 0 && pos0 >= 0 && slots > 0, "attn_prefill: bad shape");
         need(q && kc && vc && out, "attn_prefill: NULL tensor");
@@ -272,10 +280,10 @@ namespace mg
         need(pos0 + T - 1 - lo0 + 1 <= slots,
              "attn_prefill: the attended keys do not fit the cache ring (pos0 + T - lo > cache_slots)");
         const int64_t nqt = (T + kPfQ - 1) / kPfQ;
-        need(nqt * nkv <= int64_t(0x7fffffff), "attn_prefill: too many query tiles");
-        const PfArgs a{T, nkv, ldq, ldo, slots, pos0, window, nqt,
+        need(nqt * nkv * nsub <= int64_t(0x7fffffff), "attn_prefill: too many query tiles");
+        const PfArgs a{T, nkv, ldq, ldo, slots, pos0, window, nqt, hpg, nsub,
                        float(double(float(scaling)) * 1.4426950408889634)};
-        const dim3 grid{unsigned(nqt * nkv), 1u, 1u};
+        const dim3 grid{unsigned(nqt * nkv * nsub), 1u, 1u};
         auto go = [&](auto kern, int waves) {
             hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * waves)), 0, c->stream, q, kc, vc, a, out);
         };
@@ -283,7 +291,7 @@ namespace mg
         // 64-key steps
 #define MG_PF_CASE(H)                                                                                               \
     case H: D == 128 ? go(k_attn_prefill<H, 4, 1, 4>, 2 * H) : go(k_attn_prefill<H, 2, 1, 4>, 2 * H); break;
-        switch (hpg) {
+        switch (hw) {
             MG_PF_CASE(1)
             MG_PF_CASE(2)
             MG_PF_CASE(3)

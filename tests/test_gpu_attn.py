@@ -56,6 +56,19 @@ def test_group_sizes(prims, hpg, D):
     attn_case(prims, 2 * hpg, 2, D, 3000, 2999, seed=80 + hpg)
 
 
+@pytest.mark.parametrize("hpg", (9, 12, 16, 20, 32))
+def test_large_groups(prims, hpg):
+    """groups past 8 heads: up to 16 per wave (the MFMA's columns), larger
+    groups over several waves of a divisor (20 -> 2 x 10, 32 -> 2 x 16)"""
+    attn_case(prims, 2 * hpg, 2, 128, 3000, 2999, seed=90 + hpg)
+
+
+def test_real_model_heads(prims):
+    """32 query / 2 kv heads, head_dim 128 (the checkpoint's attention shape)"""
+    attn_case(prims, 32, 2, 128, 8192, 8000, seed=95)
+    attn_case(prims, 32, 2, 128, 1024, 5000, window=1024, seed=96)
+
+
 def test_peaked_scores(prims):
     """scaling 1: scores spread over tens of units, so the running maxima move
     late in the splits and the lazy rescale runs"""

@@ -68,6 +68,17 @@ def test_group_sizes(prims, hpg, D):
     prefill_case(prims, 70, 2 * hpg, 2, D, 80, 0, seed=110 + hpg)
 
 
+@pytest.mark.parametrize("hpg", (9, 10, 16))
+def test_large_groups(prims, hpg):
+    """groups past 8 heads over several work-groups (9 -> 3 x 3, 10 -> 2 x 5, 16 -> 2 x 8)"""
+    prefill_case(prims, 70, 2 * hpg, 2, 128, 80, 0, seed=160 + hpg)
+
+
+def test_real_model_heads(prims):
+    """32 query / 2 kv heads, head_dim 128, a chunk after a 200-token prefix"""
+    prefill_case(prims, 130, 32, 2, 128, 400, 200, seed=170)
+
+
 def test_chunked_prefill(prims):
     """a second chunk: rows at positions 50..126 see the first chunk's keys too"""
     prefill_case(prims, 77, 40, 8, 128, 160, 50, seed=120)
