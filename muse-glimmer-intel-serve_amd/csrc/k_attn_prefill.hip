@@ -96,7 +96,26 @@ namespace mg
         // staging: piece i of a step is K piece i (i < NPC) or V piece i - NPC,
         // key i / LPR (mod NPC), 16 bytes at column i % LPR
         Vec<uint32_t, 4> stg[PPT];
+        // per piece, fixed for the whole kernel: its source row offset within a
+        // step (from the step's first ring slot) and its K or V array
+        const uint16_t *gsrc[PPT];
+#pragma unroll
+        for (int u = 0; u < PPT; ++u) {
+            const int i = tid + NTHR * u;
+            const int iv = i < NPC ? i : i - NPC;
+            const int key = iv / LPR, col = iv - key * LPR;
+            gsrc[u] = (i < NPC ? kc : vc) + key * rowstride + g * D + 8 * col;
+        }
         auto stage = [&](int64_t jb, int64_t sb) {
+            if (jb + KS - 1 <= khi && sb + KS <= a.slots) {
+                // a whole step inside the ring: fixed offsets from one base
+                const int64_t off = sb * rowstride;
+#pragma unroll
+                for (int u = 0; u < PPT; ++u)
+                    if (tid + NTHR * u < 2 * NPC)
+                        stg[u] = *reinterpret_cast<const Vec<uint32_t, 4> *>(gsrc[u] + off);
+                return;
+            }
 #pragma unroll
             for (int u = 0; u < PPT; ++u) {
                 const int i = tid + NTHR * u;
@@ -107,8 +126,7 @@ namespace mg
                 const uint16_t *base = i < NPC ? kc : vc;
                 stg[u] = Vec<uint32_t, 4>{{0u, 0u, 0u, 0u}};
                 if (i < 2 * NPC && jb + key <= khi)
-                    stg[u] = ld16_stream<uint32_t, 4>(
-                        reinterpret_cast<const uint32_t *>(base + sl * rowstride + g * D + 8 * col));
+                    stg[u] = *reinterpret_cast<const Vec<uint32_t, 4> *>(base + sl * rowstride + g * D + 8 * col);
             }
         };
         auto commit = [&](int buf) {

@@ -67,7 +67,7 @@ def test_exhaustive_16bit_gate_inputs(prims, dt, gate):
 
 @pytest.mark.parametrize("dt", (BF16, F16, F32, F64))
 @pytest.mark.parametrize("gate", (False, True))
-@pytest.mark.parametrize("n", (64 * 25600 + 5, 1000, 7))
+@pytest.mark.parametrize("n", (64 * 25600 + 5, 33 * 19968, 1000, 7))
 def test_gate_random(prims, dt, gate, n):
     gs, g = storage(4, (n,), dt)
     us, u = storage(5, (n,), dt)
