@@ -651,7 +651,12 @@ namespace mg
                 const bool ok = a[q] != 0 && int64_t(j) < V;
                 if (top_idx) top_idx[row * K + i] = ok ? int64_t(j) : -1;
                 float tv = -__builtin_huge_valf();
-                if (ok) {
+                const uint32_t hk = uint32_t(a[q] >> 32);
+                if (ok && hk != 1u && hk != f32_key(0.0f)) {
+                    // the key's high word is the (transformed) value itself
+                    tv = key_f32(hk);
+                } else if (ok) {
+                    // NaN and +-0 share a key per class: read the value back
                     tv = float(SI::dec(L[row * V + j]));
                     if constexpr (TAIL) tv = vtail<SI>(tv, tail);
                 }
