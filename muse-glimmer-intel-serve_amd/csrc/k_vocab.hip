@@ -546,7 +546,24 @@ namespace mg
         const int D = K < kBlk ? K : kBlk;
         const bool regs = want_top && nch * D <= 64 * kMergeRegs;
 
-        // the blocks' keys, loaded first so their latency overlaps the fold
+        // the lane's chunk partials (up to two: rows of up to 128 chunks) and
+        // the blocks' keys, all requested before any is used, so one round
+        // trip serves the fold, the blocks and the block check
+        constexpr int PPL = 2;
+        const bool pregs = nch <= 64 * PPL;
+        VPart pv[PPL];
+#pragma unroll
+        for (int k = 0; k < PPL; ++k) {
+            const int c = lane + 64 * k;
+            if (pregs && c < nch) {
+                pv[k] = pr[c];
+            } else {
+                pv[k].l = 0.0;
+                pv[k].kd = pv[k].top = 0;
+                pv[k].m = -__builtin_huge_valf();
+                pv[k].fin = pv[k].nlist = pv[k].pad = 0;
+            }
+        }
         uint64_t r[kMergeRegs];
 #pragma unroll
         for (int q = 0; q < kMergeRegs; ++q) {
@@ -560,13 +577,18 @@ namespace mg
         float M = -__builtin_huge_valf();
         uint64_t ak = 0;
         bool any = false;
-        for (int c = lane; c < nch; c += 64) {
-            const VPart p = pr[c];
+        auto fold_max = [&](const VPart &p) {
             if (p.fin) {
                 M = p.m > M ? p.m : M;
                 any = true;
             }
             ak = p.top > ak ? p.top : ak;
+        };
+        if (pregs) {
+#pragma unroll
+            for (int k = 0; k < PPL; ++k) fold_max(pv[k]); // absent ones: fin 0, top 0
+        } else {
+            for (int c = lane; c < nch; c += 64) fold_max(pr[c]);
         }
         M = dpp_max(M);
         ak = dpp_reduce(ak, uint64_t(0), [](uint64_t u, uint64_t v) { return u > v ? u : v; });
@@ -574,11 +596,17 @@ namespace mg
         // sum of l_c * e^(m_c - M): the f32 difference and hardware exp2 keep
         // each term within a few ulp of f32, far inside the lse tolerance
         double S = 0.0;
-        if (any)
-            for (int c = lane; c < nch; c += 64) {
-                const VPart p = pr[c];
-                if (p.fin) S += p.l * double(__builtin_amdgcn_exp2f((p.m - M) * 1.44269504088896341f));
+        auto fold_sum = [&](const VPart &p) {
+            if (p.fin) S += p.l * double(__builtin_amdgcn_exp2f((p.m - M) * 1.44269504088896341f));
+        };
+        if (any) {
+            if (pregs) {
+#pragma unroll
+                for (int k = 0; k < PPL; ++k) fold_sum(pv[k]);
+            } else {
+                for (int c = lane; c < nch; c += 64) fold_sum(pr[c]);
             }
+        }
         S = dpp_sum(S);
         if (lane == 0) {
             if (lse) lse[row] = any ? double(M) + mgm::log(S) : -__builtin_huge_val();
@@ -596,9 +624,14 @@ namespace mg
             if (have >= K) {
                 const uint64_t kap = wave_kth<kMergeRegs>(r, K, hist);
                 bool bad = false;
-                for (int c = lane; c < nch; c += 64) {
-                    const uint64_t kd = pr[c].kd;
-                    bad |= kd != 0 && kd > kap;
+                if (pregs) {
+#pragma unroll
+                    for (int k = 0; k < PPL; ++k) bad |= pv[k].kd != 0 && pv[k].kd > kap;
+                } else {
+                    for (int c = lane; c < nch; c += 64) {
+                        const uint64_t kd = pr[c].kd;
+                        bad |= kd != 0 && kd > kap;
+                    }
                 }
                 done = __builtin_amdgcn_ballot_w64(bad) == 0;
                 if (done) {
