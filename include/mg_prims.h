@@ -64,6 +64,9 @@ const char *mg_last_error(void);
  * whose partials would not fit fail with an error instead of allocating.
  * (muse_open, src/gpu/c_api.cpp:88-168) */
 int mg_open(int device, void *stream, int64_t workspace_bytes, mg_ctx **out);
+/* Wait for the context's stream, then free the context (always, also when the
+ * wait fails); -1 reports the first failure, e.g. an error of earlier work.
+ * (muse_close, src/gpu/c_api.cpp:163-166) */
 int mg_close(mg_ctx *ctx);
 /* Wait for all work queued on the context's stream. */
 int mg_sync(mg_ctx *ctx);

@@ -44,14 +44,21 @@ namespace
         return c;
     }
 
-    void release(mg_ctx *c)
+    // Frees everything the context owns, whatever fails on the way; returns
+    // the first failure (a failed wait reports an error of earlier work).
+    hipError_t release(mg_ctx *c)
     {
-        if (!c) return;
-        hipSetDevice(c->device);
-        hipStreamSynchronize(c->stream);
-        if (c->lut) hipFree(c->lut);
-        if (c->work) hipFree(c->work);
+        if (!c) return hipSuccess;
+        hipError_t first = hipSuccess;
+        auto note = [&](hipError_t e) {
+            if (first == hipSuccess) first = e;
+        };
+        note(hipSetDevice(c->device));
+        note(hipStreamSynchronize(c->stream));
+        if (c->lut) note(hipFree(c->lut));
+        if (c->work) note(hipFree(c->work));
         delete c;
+        return first;
     }
 }
 
@@ -81,7 +88,7 @@ int mg_open(int device, void *stream, int64_t workspace_bytes, mg_ctx **out)
             mg::build_luts(c);
             mg::check(hipStreamSynchronize(c->stream), "building lookup tables");
         } catch (...) {
-            release(c);
+            (void)release(c); // the original error is the one reported
             throw;
         }
         *out = c;
@@ -92,7 +99,7 @@ int mg_open(int device, void *stream, int64_t workspace_bytes, mg_ctx **out)
 int mg_close(mg_ctx *ctx)
 {
     MG_GUARD(-1, {
-        release(ctx);
+        mg::check(release(ctx), "mg_close");
         return 0;
     });
 }
