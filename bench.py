@@ -10,8 +10,10 @@ configs, inputs resident in HBM:
   causal row softmax       f32 scores [40, 2048, 2048] -> bf16, 1/sqrt(128) configs[3]
 `value` is the whole step's algorithmic HBM bytes (each tensor read or written
 once) divided by the measured step time, in GB/s. Every other primitive
-(RoPE, decode softmax, Q8_0 dequant, vocab lse/argmax/top-64, decode-shape
-RMSNorm) is timed on its own under "ops". Inputs are seeded synthetic data
+(RoPE, decode softmax, Q8_0 dequant, quantizer and GEMV, vocab lse/argmax/
+top-64 with and without the output tail and the sampler distribution, the
+fused QK op, decode and prefill attention, decode-shape RMSNorm) is timed on
+its own under "ops". Inputs are seeded synthetic data
 drawn with torch's generator on the device (N(0,1) activations, N(1,0.05)
 weights, N(0,3) scores, U{-127..127} quants, U[1e-3,2e-2] f16 scales, N(0,4)
 logits). Per-op times are the median of R launches bracketed by HIP events on
