@@ -98,11 +98,12 @@ namespace mg
         }
     }
 
-    // Sum over the work-group in a fixed order: butterfly inside each wave,
-    // then the wave partials in wave order. Every thread returns the same value.
+    // Sum over the work-group in a fixed order: the DPP reduction inside each
+    // wave, then the wave partials in wave order. Every thread returns the
+    // same value.
     MG_DEV double block_sum(double v, double *part)
     {
-        v = wave_sum(v);
+        v = dpp_sum(v);
         const int wid = threadIdx.x >> 6;
         if ((threadIdx.x & 63) == 0) part[wid] = v;
         __syncthreads();
