@@ -282,12 +282,17 @@ namespace mg
                 emax = max(emax, ef);
             }
         }
-#pragma unroll
-        for (int m = 1; m < TPR; m <<= 1) {
-            ss += __shfl_xor(ss, m, 64);
-            emin = min(emin, __shfl_xor(emin, m, 64));
-            emax = max(emax, __shfl_xor(emax, m, 64));
-        }
+        // over the row's TPR lanes (a quad, half-row or row of the DPP
+        // network); the sum is exact in any order when it is used
+        auto step = [&](auto mov) {
+            ss += mov(ss);
+            emin = min(emin, mov(emin));
+            emax = max(emax, mov(emax));
+        };
+        step([](auto v) { return dpp_mov<0xB1, 0xf>(v, v); }); // quad_perm [1,0,3,2]
+        step([](auto v) { return dpp_mov<0x4E, 0xf>(v, v); }); // quad_perm [2,3,0,1]
+        if constexpr (TPR >= 8) step([](auto v) { return dpp_mov<0x141, 0xf>(v, v); }); // row_half_mirror
+        if constexpr (TPR >= 16) step([](auto v) { return dpp_mov<0x140, 0xf>(v, v); }); // row_mirror
         const bool exact = emax == 0 || (emax < EALL && emax - emin <= SPAN);
         double rs;
         if (__builtin_amdgcn_ballot_w64(!exact) == 0) {
