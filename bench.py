@@ -276,7 +276,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(every primitive is row-independent; multi-GPU sharding is described in DESIGN.md)",
+              "(every primitive is row-independent: rows or vocab shards split across GPUs without exchange)",
               file=sys.stderr)
         sys.exit(2)
     import torch
