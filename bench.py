@@ -276,7 +276,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(every primitive is row-independent: rows or vocab shards split across GPUs without exchange)",
+              "(the primitives split across GPUs by rows, the vocab pass by shards with one small exchange)",
               file=sys.stderr)
         sys.exit(2)
     import torch
