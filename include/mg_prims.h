@@ -84,6 +84,16 @@ void *mg_get_stream(mg_ctx *ctx);
 int mg_rmsnorm_rows(mg_ctx *ctx, int kind, const void *x, int64_t ldx, const void *w,
                     double eps, void *y, int64_t ldy, int64_t rows, int64_t dim, int dtype);
 
+/* The same norm with each operand at its own storage format — the bf16exec
+ * candidate's norm_rows (src/bf16exec.hpp:398-421: x f32 rows, w bf16, y bf16;
+ * its norm_rows_f32, 423-442, is the same y widened back to f32): f64
+ * internals, one rounding to y_dtype. The sum of squares runs in a fixed
+ * parallel order, not bf16exec's sequential one (within 1e-16 relative).
+ * ldx/ldy: row strides in elements (0 = dim); in place only with one format
+ * and one stride. */
+int mg_norm_rows_mixed(mg_ctx *ctx, int kind, const void *x, int64_t ldx, int x_dtype, const void *w, int w_dtype,
+                       double eps, void *y, int64_t ldy, int y_dtype, int64_t rows, int64_t dim);
+
 /* Fused residual add + norm: h[r,:] = rnd(h[r,:] + x[r,:]) (updated in place),
  * then y[r,:] = norm(h[r,:]). Replaces the residual loop
  * (src/muse_glimmer.hpp:1023-1024, 1048-1049; src/bf16exec.hpp:608-610, 641-643;

@@ -293,6 +293,67 @@ namespace mg
             launch_tree<S, 1>(c, kind, h, x, ldh, ldx, w, eps, y, ldy, rows, dim);
     }
 
+    // Mixed storage formats — the bf16exec candidate's norm_rows
+    // (src/bf16exec.hpp:398-421): rows x at one format (f32 there), weights at
+    // another (bf16), the output at a third (bf16), f64 internals
+    // (rs = 1/sqrt(sum x^2 / dim + eps), y = x*rs*(1+w) | x*rs*w | x*rs) and one
+    // rounding of the f64 value to y's format (f64 -> f32 -> bf16 there). The
+    // sum runs in a fixed order over the work-group instead of bf16exec's
+    // sequential one (within 1e-16 relative). One 256-thread work-group per
+    // row; the formats are uniform branches.
+    MG_DEV double ld_any(const void *p, int64_t i, int dt)
+    {
+        switch (dt) {
+        case BF16: return double(bf16_f32(static_cast<const uint16_t *>(p)[i]));
+        case F16: return double(f16_f32(static_cast<const uint16_t *>(p)[i]));
+        case F32: return double(static_cast<const float *>(p)[i]);
+        default: return static_cast<const double *>(p)[i];
+        }
+    }
+    MG_DEV void st_any(void *p, int64_t i, double v, int dt)
+    {
+        switch (dt) {
+        case BF16: static_cast<uint16_t *>(p)[i] = SBf16::enc64(v); break;
+        case F16: static_cast<uint16_t *>(p)[i] = SF16::enc64(v); break;
+        case F32: static_cast<float *>(p)[i] = float(v); break;
+        default: static_cast<double *>(p)[i] = v; break;
+        }
+    }
+    __global__ __launch_bounds__(256) void k_norm_mixed(int kind, const void *x, int64_t ldx, int dtx, const void *w,
+                                                        int dtw, double eps, void *y, int64_t ldy, int dty, int dim)
+    {
+        __shared__ double part[16];
+        const int64_t row = blockIdx.x;
+        double ss = 0.0;
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+            const double v = ld_any(x, row * ldx + i, dtx);
+            ss += v * v;
+        }
+        const double rs = 1.0 / __builtin_sqrt(block_sum(ss, part) / double(dim) + eps);
+        for (int i = threadIdx.x; i < dim; i += blockDim.x)
+            st_any(y, row * ldy + i,
+                   norm_out(kind, ld_any(x, row * ldx + i, dtx), rs, kind == 2 ? 0.0 : ld_any(w, i, dtw)), dty);
+    }
+
+    void launch_norm_mixed(mg_ctx *c, int kind, const void *x, int64_t ldx, int dtx, const void *w, int dtw,
+                           double eps, void *y, int64_t ldy, int dty, int64_t rows, int64_t dim)
+    {
+        need(kind >= 0 && kind <= 2, "norm_rows_mixed: unknown norm kind " + std::to_string(kind));
+        for (const int dt : {dtx, dtw, dty})
+            need(dt >= F64 && dt <= F32, "norm_rows_mixed: unknown dtype " + std::to_string(dt));
+        need(rows >= 0 && dim > 0 && dim <= (int64_t(1) << 24), "norm_rows_mixed: bad shape");
+        need(rows < (int64_t(1) << 31), "norm_rows_mixed: too many rows");
+        need(x != nullptr && y != nullptr && (kind == 2 || w != nullptr), "norm_rows_mixed: NULL tensor");
+        if (ldx == 0) ldx = dim;
+        if (ldy == 0) ldy = dim;
+        need(ldx >= dim && ldy >= dim, "norm_rows_mixed: leading dimension < dim");
+        need(x != y || (dtx == dty && ldx == ldy), "norm_rows_mixed: in place needs one format and stride");
+        if (rows == 0) return;
+        hipLaunchKernelGGL(k_norm_mixed, dim3(unsigned(rows)), dim3(256), 0, c->stream, kind, x, ldx, dtx, w, dtw, eps,
+                           y, ldy, dty, int(dim));
+        check_launch("k_norm_mixed");
+    }
+
     void launch_norm(mg_ctx *c, int kind, void *h, const void *x, int64_t ldh, int64_t ldx,
                      const void *w, double eps, void *y, int64_t ldy, int64_t rows, int64_t dim,
                      int dt)

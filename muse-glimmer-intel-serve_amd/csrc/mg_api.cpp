@@ -132,6 +132,15 @@ int mg_rmsnorm_rows(mg_ctx *ctx, int kind, const void *x, int64_t ldx, const voi
     });
 }
 
+int mg_norm_rows_mixed(mg_ctx *ctx, int kind, const void *x, int64_t ldx, int x_dtype, const void *w, int w_dtype,
+                       double eps, void *y, int64_t ldy, int y_dtype, int64_t rows, int64_t dim)
+{
+    MG_GUARD(-1, {
+        mg::launch_norm_mixed(ctx_of(ctx), kind, x, ldx, x_dtype, w, w_dtype, eps, y, ldy, y_dtype, rows, dim);
+        return 0;
+    });
+}
+
 int mg_residual_rmsnorm(mg_ctx *ctx, int kind, void *h, const void *x, const void *w, double eps,
                         void *y, int64_t rows, int64_t dim, int dtype)
 {

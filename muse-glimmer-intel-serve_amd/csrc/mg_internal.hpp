@@ -51,6 +51,8 @@ namespace mg
     void launch_norm(mg_ctx *c, int kind, void *h, const void *x, int64_t ldh, int64_t ldx,
                      const void *w, double eps, void *y, int64_t ldy, int64_t rows, int64_t dim,
                      int dt);
+    void launch_norm_mixed(mg_ctx *c, int kind, const void *x, int64_t ldx, int dtx, const void *w, int dtw,
+                           double eps, void *y, int64_t ldy, int dty, int64_t rows, int64_t dim);
     // k_elementwise.hip
     void launch_residual_add(mg_ctx *c, void *h, const void *x, int64_t n, int dt);
     void launch_swiglu(mg_ctx *c, const void *g, const void *u, void *out, int64_t n, int dt,

@@ -43,6 +43,7 @@ _SIGS = {
     "mg_set_stream": ([_P, _P], _INT),
     "mg_get_stream": ([_P], _P),
     "mg_rmsnorm_rows": ([_P, _INT, _P, _I, _P, _D, _P, _I, _I, _I, _INT], _INT),
+    "mg_norm_rows_mixed": ([_P, _INT, _P, _I, _INT, _P, _INT, _D, _P, _I, _INT, _I, _I], _INT),
     "mg_residual_rmsnorm": ([_P, _INT, _P, _P, _P, _D, _P, _I, _I, _INT], _INT),
     "mg_residual_add": ([_P, _P, _P, _I, _INT], _INT),
     "mg_swiglu": ([_P, _P, _P, _P, _I, _INT], _INT),
@@ -152,6 +153,14 @@ class Prims:
         rows, dim = X.shape
         self._check(self.lib.mg_rmsnorm_rows(self.h, kind, _ptr(X), X.stride(0), _ptr(w), eps, _ptr(Y),
                                              Y.stride(0), rows, dim, _code(X, f32_compat)))
+
+    def norm_rows_mixed(self, kind, X, w, eps, Y):
+        """bf16exec's norm_rows (src/bf16exec.hpp:398-421) generalised: X, w and Y each
+        at its own dtype (f32 rows, bf16 weights, bf16 output there); X, Y: [rows, dim]."""
+        rows, dim = X.shape
+        self._check(self.lib.mg_norm_rows_mixed(self.h, kind, _ptr(X), X.stride(0), _dtype_code(X), _ptr(w),
+                                                _dtype_code(w) if w is not None else 0, eps, _ptr(Y), Y.stride(0),
+                                                _dtype_code(Y), rows, dim))
 
     def residual_rmsnorm(self, kind, h, x, w, eps, y, f32_compat=False):
         """h = rnd(h + x) in place, then y = norm(h)."""

@@ -21,7 +21,8 @@
 //                 bitwise vs oracle/_ref (reference rounding.hpp compiled)
 //   fmath         bitwise vs oracle/_ref (reference fmath.hpp compiled), ulp vs libm
 //   mean_sq/norm  bitwise vs oracle/_ref (reference rmsnorm_rows compiled),
-//                 the f32-compat branch included
+//                 the f32-compat branch included; bf16exec's norm_rows equal
+//                 to the pinned f64 norm rounded once wherever its sum is exact
 //   rope          bitwise vs oracle/_ref (reference build_rope_table/apply_rope),
 //                 the f32-compat table included
 //   silu/sigmoid  bitwise vs oracle/_ref (reference ok_siluv/ok_sigmoidv)
@@ -304,6 +305,28 @@ extern "C"
     {
 #pragma omp parallel for schedule(static)
         for (int64_t r = 0; r < rows; ++r) norm_row(kind, X + r * dim, w, eps, Y + r * dim, dim, dt);
+    }
+
+    // bf16exec.hpp:398-421 — norm_rows of the bf16exec candidate: the sum of
+    // squares in f64 in index order, rs = 1/sqrt(ss/dim + eps), v = x*rs
+    // (*(1+w) | *w) in f64, one rounding to dt (f64 -> f32 -> bf16 for bf16).
+    // X and w hold storage-valued f64 (f32 rows and bf16 weights there).
+    void or_norm_rows_mixed(int kind, const double *X, const double *w, double eps, double *Y, int64_t rows,
+                            int64_t dim, int dt)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            const double *x = X + r * dim;
+            double ss = 0;
+            for (int64_t i = 0; i < dim; ++i) ss += x[i] * x[i];
+            const double rs = 1.0 / std::sqrt(ss / double(dim) + eps);
+            for (int64_t i = 0; i < dim; ++i) {
+                double v = x[i] * rs;
+                if (kind == CENTERED) v = v * (1.0 + w[i]);
+                else if (kind == PLAIN) v = v * w[i];
+                Y[r * dim + i] = rnd(dt, v);
+            }
+        }
     }
 
     // Residual add (muse_glimmer.hpp:1023-1024, 1048-1049: h = rnd(h + m)) followed

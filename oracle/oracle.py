@@ -45,6 +45,7 @@ _SIGS = {
     "or_meansq": [_P, _P, _I, _I],
     "or_rmsnorm_rows": [_INT, _P, _P, _D, _P, _I, _I, _INT],
     "or_residual_rmsnorm": [_INT, _P, _P, _P, _D, _P, _I, _I, _INT],
+    "or_norm_rows_mixed": [_INT, _P, _P, _D, _P, _I, _I, _INT],
     "or_residual_add": [_P, _P, _I, _INT],
     "or_swiglu": [_P, _P, _P, _I, _INT],
     "or_sigmoid_gate": [_P, _P, _P, _I, _INT],
@@ -166,6 +167,16 @@ def rmsnorm_rows(kind, X, w, eps, dt):
     Y = np.empty_like(X)
     w = _c(w) if w is not None else None
     lib().or_rmsnorm_rows(kind, _p(X), _p(w), eps, _p(Y), rows, dim, dt)
+    return Y
+
+
+def norm_rows_mixed(kind, X, w, eps, dt):
+    """bf16exec's norm_rows (src/bf16exec.hpp:398-421): X, w storage-valued f64; output rounded to dt."""
+    X = _c(X)
+    rows, dim = X.shape
+    Y = np.empty_like(X)
+    w = _c(w) if w is not None else None
+    lib().or_norm_rows_mixed(kind, _p(X), _p(w), eps, _p(Y), rows, dim, dt)
     return Y
 
 

@@ -147,3 +147,50 @@ def test_errors(prims):
         prims.rmsnorm_rows(O.PLAIN, x, None, 1e-6, x)
     with pytest.raises(mgprims.MgError, match="norm kind"):
         prims.rmsnorm_rows(7, x, None, 1e-6, x)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dim", (13, 128, 5120, 6656))
+def test_bf16exec_norm_rows(prims, kind, dim):
+    """bf16exec's norm_rows (src/bf16exec.hpp:398-421): f32 rows, bf16 weights, bf16
+    output; within 1 bf16 ulp of its f64 sequential-sum formula (the sum order differs)"""
+    xs, x = storage(91 + dim, (33, dim), F32)
+    ws, w = storage(92 + dim, (dim,), BF16, 1.0, 0.05)
+    dy = to_dev(np.zeros((33, dim), np.uint16), BF16)
+    prims.norm_rows_mixed(kind, to_dev(xs, F32), None if kind == O.WEIGHTLESS else to_dev(ws, BF16), 1e-6, dy)
+    ref = O.norm_rows_mixed(kind, x, w, 1e-6, BF16)
+    check_lp(from_dev(dy, BF16), ref, BF16, max_frac=1e-4)
+
+
+@pytest.mark.parametrize("dtx,dtw,dty", ((BF16, F32, F32), (F16, F16, F64), (F64, BF16, F16), (F32, F32, F32)))
+def test_norm_rows_mixed_formats(prims, dtx, dtw, dty):
+    """other format mixes against the same formula: 16-bit outputs within 1 ulp, f32
+    within 1e-6 and f64 within 1e-12 relative"""
+    rows, dim = 21, 777
+    xs, x = storage(95, (rows, dim), dtx)
+    ws, w = storage(96, (dim,), dtw, 1.0, 0.05)
+    for kind in KINDS:
+        yz = np.zeros((rows, dim), np.uint16 if dty in (BF16, F16) else (np.float32 if dty == F32 else np.float64))
+        dy = to_dev(yz, dty)
+        prims.norm_rows_mixed(kind, to_dev(xs, dtx), to_dev(ws, dtw), 1e-6, dy)
+        ref = O.norm_rows_mixed(kind, x, w, 1e-6, dty)
+        got = from_dev(dy, dty)
+        if dty in (BF16, F16):
+            check_lp(got, ref, dty, max_frac=1e-3)
+        else:
+            rel = np.abs(got.astype(np.float64) - ref) / np.maximum(np.abs(ref), 1e-30)
+            assert rel.max() <= (1e-6 if dty == F32 else 1e-12)
+
+
+def test_norm_rows_mixed_strided_inplace(prims):
+    rows, dim, ld = 9, 640, 700
+    xs, x = storage(97, (rows, ld), F32)
+    ws, w = storage(98, (dim,), F32, 1.0, 0.05)
+    dx = to_dev(xs, F32)
+    view = dx[:, :dim]
+    prims.norm_rows_mixed(O.PLAIN, view, to_dev(ws, F32), 1e-6, view)
+    out = from_dev(dx, F32)
+    ref = O.norm_rows_mixed(O.PLAIN, np.ascontiguousarray(x[:, :dim]), w, 1e-6, F32)
+    rel = np.abs(out[:, :dim].astype(np.float64) - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert rel.max() <= 1e-6
+    assert same_bits(out[:, dim:], xs[:, dim:])

@@ -199,6 +199,20 @@ def test_rmsnorm_f64_vs_extended(kind):
     assert rel.max() < 1.5e-15  # a few ulp: the row sum, sqrt, division and two products
 
 
+@pytest.mark.parametrize("kind", (O.CENTERED, O.PLAIN, O.WEIGHTLESS))
+@pytest.mark.parametrize("dt", (BF16, F16, F32))
+def test_bf16exec_norm_rows_is_the_f64_norm_rounded_once(kind, dt):
+    """bf16exec's norm_rows (src/bf16exec.hpp:398-421) sums in index order, the twin in
+    mean_sq's; on integer rows both sums are exact, so its output must be the pinned f64
+    norm rounded once to dt (a wrong weight form, rounding or eps shows up here)"""
+    X = RNG.integers(-40, 41, (13, 200)).astype(np.float64)
+    X[3] = 0.0
+    w = O.rnd(RNG.normal(1, 0.05, 200), BF16)
+    got = O.norm_rows_mixed(kind, X, w, 1e-6, dt)
+    ref = O.rnd(O.rmsnorm_rows(kind, X, w, 1e-6, F64), dt)
+    assert np.array_equal(got, ref)
+
+
 def test_rmsnorm_invariants():
     x = RNG.normal(0, 1, (16, 640))
     w = RNG.normal(1, 0.1, 640)
