@@ -22,6 +22,38 @@ def test_binding_covers_header():
     assert set(mgprims.header_symbols()) == set(mgprims._SIGS)
 
 
+def _header_params():
+    """name -> parameter type strings, parsed from include/mg_prims.h"""
+    import re
+    with open(mgprims.HEADER) as f:
+        text = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(mg_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        params = [p.strip() for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = params
+    return out
+
+
+def test_binding_matches_header_signatures():
+    """each ctypes signature has the header's parameter count, and pointers, 64-bit
+    integers, doubles and ints where the header has them (the ABI cannot drift)"""
+    P, I64, D, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_double, ctypes.c_int
+    params = _header_params()
+    assert set(params) == set(mgprims._SIGS)
+    for name, (args, _) in mgprims._SIGS.items():
+        hp = params[name]
+        assert len(args) == len(hp), (name, len(args), len(hp))
+        for a, h in zip(args, hp):
+            if "*" in h:
+                assert a in (P, ctypes.c_char_p) or issubclass(a, ctypes._Pointer), (name, h, a)
+            elif h.startswith("int64_t"):
+                assert a is I64, (name, h, a)
+            elif h.startswith("double"):
+                assert a is D, (name, h, a)
+            elif h.startswith("int "):
+                assert a is I, (name, h, a)
+
+
 def test_open_reports_error_without_device():
     import torch
     if torch.cuda.is_available():
