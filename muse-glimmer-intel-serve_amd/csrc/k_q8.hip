@@ -12,7 +12,7 @@
 // f32): one Q-byte load and one 16-byte store, so every load and store
 // instruction of a wave covers one contiguous span (512 B in, 1 KiB out for
 // bf16) and no cache line is written in parts. A work-group of 256 lanes
-// takes U = 4 such spans per lane in flight; the grid covers the tensor
+// takes U = 2 such spans per lane in flight; the grid covers the tensor
 // exactly. The scale read is 2 bytes per lane, shared by the 32/Q lanes of
 // its block and coalesced across the wave.
 #include "mg_device.hpp"
@@ -32,6 +32,8 @@ namespace mg
         }
     }
 
+    constexpr int kDequantSpans = 2; // spans per lane (measured: 1 and 2 beat 4 and 8)
+
     template <class SO>
     __global__ __launch_bounds__(256) void k_dequant_q8_0(const int8_t *__restrict__ qs,
                                                           const uint16_t *__restrict__ d,
@@ -39,7 +41,7 @@ namespace mg
                                                           int64_t nspans)
     {
         using raw = typename SO::raw;
-        constexpr int Q = 16 / sizeof(raw), U = 4;
+        constexpr int Q = 16 / sizeof(raw), U = kDequantSpans;
         const int64_t base = int64_t(blockIdx.x) * (256 * U) + threadIdx.x;
         Vec<int8_t, Q> q[U];
         float sc[U];
@@ -269,7 +271,7 @@ namespace mg
         if (rows == 0 || in == 0) return;
         const int64_t n = rows * in;
         const int Q = dt_out == F32 ? 4 : 8;
-        const int64_t nspans = n / Q, blocks = (nspans + 1023) / 1024;
+        const int64_t nspans = n / Q, blocks = (nspans + 256 * kDequantSpans - 1) / (256 * kDequantSpans);
         need(blocks < (int64_t(1) << 31), "dequant_q8_0: tensor too large");
         const dim3 g{unsigned(blocks), 1u, 1u};
         switch (dt_out) {
