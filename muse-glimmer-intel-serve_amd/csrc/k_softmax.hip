@@ -14,8 +14,9 @@
 // a few f32 ulp of the f64 value: the bf16 output is within 1 ulp of the
 // twin's and the f32 output within 1e-6 relative.
 //
-// Rows of up to 2048 keys: one wave per row, the row in registers (8 keys per
-// lane per chunk), one read and one write of HBM. Longer rows (decode,
+// Rows of up to 2048 keys: one wave per row (the fast path runs one-wave
+// work-groups), the row in registers (8 keys per lane per chunk), one read
+// and one write of HBM. Longer rows (decode,
 // q = 1, k = 131072): split over work-groups of 4096 keys; pass A writes each
 // chunk's (max, sum) partial, pass B merges the partials of its row in chunk
 // order (the k_attn_decode_combine rule, src/gpu/gpu_engine.cpp:1816-1857, with
@@ -203,12 +204,12 @@ namespace mg
     // arithmetic and store zeros. A row whose sum is not finite (NaN or
     // infinite scores) is redone on the accurate path.
     template <class SO, int CH>
-    __global__ __launch_bounds__(256) void k_softmax_fast(const float *__restrict__ x,
+    __global__ __launch_bounds__(64) void k_softmax_fast(const float *__restrict__ x,
                                                           typename SO::raw *__restrict__ y, SmArgs a,
                                                           float c2, bool vec)
     {
         using ro = typename SO::raw;
-        const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+        const int64_t row = blockIdx.x; // one wave per work-group (measured: 3-4 % over four)
         const int lane = threadIdx.x & 63;
         if (row >= a.nrows) return;
         int64_t lo64, hi64;
@@ -486,15 +487,16 @@ namespace mg
         ro *yo = static_cast<ro *>(y);
         if (a.kc <= 2048) {
             const unsigned blocks = unsigned((a.nrows + 3) / 4);
-            need((a.nrows + 3) / 4 < (int64_t(1) << 31), "softmax: too many rows");
+            need(a.nrows < (int64_t(1) << 31), "softmax: too many rows");
             if constexpr (SI::dt == F32 && sizeof(ro) == 2 && !CAP) if (a.scale > 0.0) {
                 const float c2 = float(double(a.scale) * 1.4426950408889634);
+                const unsigned rows1 = unsigned(a.nrows); // < 2^31: checked above
                 if (a.kc <= 512)
-                    hipLaunchKernelGGL((k_softmax_fast<SO, 1>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, c2, vec);
+                    hipLaunchKernelGGL((k_softmax_fast<SO, 1>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
                 else if (a.kc <= 1024)
-                    hipLaunchKernelGGL((k_softmax_fast<SO, 2>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, c2, vec);
+                    hipLaunchKernelGGL((k_softmax_fast<SO, 2>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
                 else
-                    hipLaunchKernelGGL((k_softmax_fast<SO, 4>), dim3(blocks), dim3(256), 0, c->stream, xi, yo, a, c2, vec);
+                    hipLaunchKernelGGL((k_softmax_fast<SO, 4>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
                 check_launch("k_softmax_fast");
                 return;
             }
