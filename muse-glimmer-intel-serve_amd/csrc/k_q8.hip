@@ -11,9 +11,9 @@
 // A lane owns Q = 16 / sizeof(out) consecutive quants (8 for bf16/f16, 4 for
 // f32): one Q-byte load and one 16-byte store, so every load and store
 // instruction of a wave covers one contiguous span (512 B in, 1 KiB out for
-// bf16) and no cache line is written in parts. A work-group of 256 lanes
-// takes U = 2 such spans per lane in flight; the grid covers the tensor
-// exactly. The scale read is 2 bytes per lane, shared by the 32/Q lanes of
+// bf16) and no cache line is written in parts. A work-group is one wave
+// (measured faster than four) with U = 2 such spans per lane in flight; the
+// grid covers the tensor exactly. The scale read is 2 bytes per lane, shared by the 32/Q lanes of
 // its block and coalesced across the wave.
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
@@ -35,19 +35,19 @@ namespace mg
     constexpr int kDequantSpans = 2; // spans per lane (measured: 1 and 2 beat 4 and 8)
 
     template <class SO>
-    __global__ __launch_bounds__(256) void k_dequant_q8_0(const int8_t *__restrict__ qs,
+    __global__ __launch_bounds__(64) void k_dequant_q8_0(const int8_t *__restrict__ qs,
                                                           const uint16_t *__restrict__ d,
                                                           typename SO::raw *__restrict__ out,
                                                           int64_t nspans)
     {
         using raw = typename SO::raw;
         constexpr int Q = 16 / sizeof(raw), U = kDequantSpans;
-        const int64_t base = int64_t(blockIdx.x) * (256 * U) + threadIdx.x;
+        const int64_t base = int64_t(blockIdx.x) * (64 * U) + threadIdx.x;
         Vec<int8_t, Q> q[U];
         float sc[U];
 #pragma unroll
         for (int k = 0; k < U; ++k) {
-            const int64_t g = base + 256 * k;
+            const int64_t g = base + 64 * k;
             if (g < nspans) {
                 q[k] = ld_quants<Q>(qs + Q * g);
                 // `in` is a multiple of 32, so span g lies in the row-major
@@ -57,7 +57,7 @@ namespace mg
         }
 #pragma unroll
         for (int k = 0; k < U; ++k) {
-            const int64_t g = base + 256 * k;
+            const int64_t g = base + 64 * k;
             if (g < nspans) {
                 Vec<raw, Q> o;
                 if (__builtin_isfinite(sc[k])) {
@@ -90,11 +90,11 @@ namespace mg
         return v;
     }
 
-    __global__ __launch_bounds__(256) void k_quantize_q8_0(const uint16_t *__restrict__ w, int8_t *__restrict__ qs,
+    __global__ __launch_bounds__(64) void k_quantize_q8_0(const uint16_t *__restrict__ w, int8_t *__restrict__ qs,
                                                            uint16_t *__restrict__ d, int64_t nblk)
     {
         const int lane = threadIdx.x & 63;
-        const int64_t b0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 64; // the wave's first block
+        const int64_t b0 = int64_t(blockIdx.x) * 64; // the wave's (= work-group's) first block
         if (b0 >= nblk) return;
         Vec<uint16_t, 8> v[4];
 #pragma unroll
@@ -139,8 +139,8 @@ namespace mg
         const int64_t nblk = rows * (in / 32);
         if (nblk == 0) return;
         const int64_t waves = (nblk + 63) / 64;
-        need((waves + 3) / 4 <= int64_t(0x7fffffff), "quantize_q8_0: tensor too large");
-        hipLaunchKernelGGL(k_quantize_q8_0, dim3(unsigned((waves + 3) / 4)), dim3(256), 0, c->stream, w, qs, d, nblk);
+        need(waves <= int64_t(0x7fffffff), "quantize_q8_0: tensor too large");
+        hipLaunchKernelGGL(k_quantize_q8_0, dim3(unsigned(waves)), dim3(64), 0, c->stream, w, qs, d, nblk);
         check_launch("k_quantize_q8_0");
     }
 
@@ -271,13 +271,13 @@ namespace mg
         if (rows == 0 || in == 0) return;
         const int64_t n = rows * in;
         const int Q = dt_out == F32 ? 4 : 8;
-        const int64_t nspans = n / Q, blocks = (nspans + 256 * kDequantSpans - 1) / (256 * kDequantSpans);
+        const int64_t nspans = n / Q, blocks = (nspans + 64 * kDequantSpans - 1) / (64 * kDequantSpans);
         need(blocks < (int64_t(1) << 31), "dequant_q8_0: tensor too large");
         const dim3 g{unsigned(blocks), 1u, 1u};
         switch (dt_out) {
-        case BF16: hipLaunchKernelGGL(k_dequant_q8_0<SBf16>, g, dim3(256), 0, c->stream, qs, d, static_cast<uint16_t *>(out), nspans); break;
-        case F16: hipLaunchKernelGGL(k_dequant_q8_0<SF16>, g, dim3(256), 0, c->stream, qs, d, static_cast<uint16_t *>(out), nspans); break;
-        case F32: hipLaunchKernelGGL(k_dequant_q8_0<SF32>, g, dim3(256), 0, c->stream, qs, d, static_cast<float *>(out), nspans); break;
+        case BF16: hipLaunchKernelGGL(k_dequant_q8_0<SBf16>, g, dim3(64), 0, c->stream, qs, d, static_cast<uint16_t *>(out), nspans); break;
+        case F16: hipLaunchKernelGGL(k_dequant_q8_0<SF16>, g, dim3(64), 0, c->stream, qs, d, static_cast<uint16_t *>(out), nspans); break;
+        case F32: hipLaunchKernelGGL(k_dequant_q8_0<SF32>, g, dim3(64), 0, c->stream, qs, d, static_cast<float *>(out), nspans); break;
         default: fail("dequant_q8_0: output dtype must be bf16, f16 or f32");
         }
         check_launch("k_dequant_q8_0");
