@@ -469,19 +469,38 @@ namespace mg
         for (int q = 0; q < SL; ++q)
             if (SL * lane + q < n) lr[SL * lane + q] = a[q];
 
-        // the block: the list's (= the chunk's) top D keys, D = min(8, K)
+        // the block: the list's (= the chunk's) top D keys, D = min(8, K),
+        // taken largest first. Keys are unique, so the wave maximum of the high
+        // words, then of the low words among the slots holding that high word,
+        // is the largest remaining key; it is cleared and lane i keeps the i-th.
+        // Slots past the list's end hold 0 and make the block's tail 0.
         const int D = K < kBlk ? K : kBlk;
-        const uint64_t kd = n > D ? wave_kth<SL>(a, D, shist[wv]) : 0;
         uint64_t *br = blk + cid * kBlk;
-        int nb = 0;
+        uint64_t kd = 0; // the D-th key when the list is longer than the block
+        {
+            uint64_t r[SL];
 #pragma unroll
-        for (int q = 0; q < SL; ++q) {
-            const bool take = a[q] != 0 && a[q] >= kd;
-            const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
-            if (take && nb + lane_rank(mk) < kBlk) br[nb + lane_rank(mk)] = a[q];
-            nb += __builtin_popcountll(mk);
+            for (int q = 0; q < SL; ++q) r[q] = a[q];
+            uint64_t mine = 0;
+            for (int i = 0; i < D; ++i) {
+                uint32_t hm = 0;
+#pragma unroll
+                for (int q = 0; q < SL; ++q) hm = uint32_t(r[q] >> 32) > hm ? uint32_t(r[q] >> 32) : hm;
+                hm = dpp_max_u32(hm);
+                uint32_t lm = 0;
+#pragma unroll
+                for (int q = 0; q < SL; ++q)
+                    lm = (uint32_t(r[q] >> 32) == hm && uint32_t(r[q]) > lm) ? uint32_t(r[q]) : lm;
+                lm = dpp_max_u32(lm);
+                const uint64_t mk = (uint64_t(hm) << 32) | lm;
+#pragma unroll
+                for (int q = 0; q < SL; ++q) r[q] = r[q] == mk ? 0 : r[q];
+                mine = lane == i ? mk : mine;
+                kd = mk;
+            }
+            if (lane < kBlk) br[lane] = mine;
         }
-        if (lane >= nb && lane < kBlk) br[lane] = 0;
+        if (n <= D) kd = 0;
         if (lane == 0) {
             VPart p;
             p.l = l;
