@@ -458,11 +458,6 @@ namespace mg
                 a[q] = vkey(exact ? bits : vhi(__builtin_bit_cast(float, bits)), uint32_t(cb + so[i]));
             }
         }
-        // the largest key is the chunk's argmax under the scan's rule
-        uint64_t top = a[0];
-#pragma unroll
-        for (int q = 1; q < SL; ++q) top = a[q] > top ? a[q] : top;
-        top = dpp_reduce(top, uint64_t(0), [](uint64_t u, uint64_t v) { return u > v ? u : v; });
         const int64_t cid = row * nch + ch;
         uint64_t *lr = lst + cid * CAP;
 #pragma unroll
@@ -477,6 +472,7 @@ namespace mg
         const int D = K < kBlk ? K : kBlk;
         uint64_t *br = blk + cid * kBlk;
         uint64_t kd = 0; // the D-th key when the list is longer than the block
+        uint64_t top = 0; // the first key taken, the list's (= the chunk's) largest: its argmax
         {
             uint64_t r[SL];
 #pragma unroll
@@ -496,6 +492,7 @@ namespace mg
 #pragma unroll
                 for (int q = 0; q < SL; ++q) r[q] = r[q] == mk ? 0 : r[q];
                 mine = lane == i ? mk : mine;
+                top = i == 0 ? mk : top;
                 kd = mk;
             }
             if (lane < kBlk) br[lane] = mine;
