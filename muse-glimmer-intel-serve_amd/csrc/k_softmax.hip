@@ -5,7 +5,7 @@
 //                                    the input dtype as the eager path does (844-845)
 //   softcap (cap != 0):              s = rnd_in(cap * rnd_in(tanh(rnd_in(s / cap)))),
 //                                    apply_output_tail's op order (920-943), with
-//                                    FDLIBM tanh in f64: the capped score is exact
+//                                    FDLIBM's tanh bits: the capped score is exact
 //   masked keys (causal / window):   excluded, probability exactly 0
 //   p = exp(s - max) / sum           written once at the output dtype
 // The reference evaluates the exponentials and the sum in f64 (twin) or f32
@@ -50,9 +50,10 @@ namespace mg
     {
         float s = SI::dec(SI::enc32(x * a.scale));
         if (CAP) {
-            // the twin's FDLIBM tanh in f64, so the capped score is bit-identical
+            // rnd(tanh) with FDLIBM's bits (tanh_stored), so the capped score
+            // is bit-identical to the twin's
             s = SI::dec(SI::enc32(s / a.cap));
-            s = SI::dec(SI::enc64(mgm::tanh(double(s))));
+            s = tanh_stored<SI>(s);
             s = SI::dec(SI::enc32(s * a.cap));
         }
         return s;
@@ -192,18 +193,21 @@ namespace mg
         softmax_row_accurate<SI, SO, CH, CAP>(a, x + row * a.kc, y + row * a.kc, lo, hi, vec, threadIdx.x & 63);
     }
 
-    // Lean row for f32 scores and 16-bit probabilities without softcap (the
-    // attention-score configuration). Scores are taken in the log2 domain,
+    // Lean row for f32 scores and 16-bit probabilities (the attention-score
+    // configuration). Scores are taken in the log2 domain,
     // p = 2^(x*c2 - max*c2) / sum on the hardware exp2, c2 = scale*log2 e > 0:
     // the max is taken over the raw scores (multiplying by c2 > 0 keeps the
     // order) and each key costs one fma, one exp2 and one add before the
     // normalisation; relative error a few 1e-7, well inside the 16-bit
     // output's half-ulp of 2e-3, so outputs stay within 1 ulp of the twin.
+    // With a softcap (CAP) each visible key first becomes the twin's capped
+    // score, bit for bit (score<SF32, true>: the scaled score, the f32
+    // quotient by cap, tanh_stored, the product by cap), and c2 = log2 e.
     // Key indices are 32-bit (rows of at most 2048 keys); chunks entirely
     // visible skip the per-key mask, chunks entirely masked skip the
     // arithmetic and store zeros. A row whose sum is not finite (NaN or
     // infinite scores) is redone on the accurate path.
-    template <class SO, int CH>
+    template <class SO, int CH, bool CAP>
     __global__ __launch_bounds__(64) void k_softmax_fast(const float *__restrict__ x,
                                                           typename SO::raw *__restrict__ y, SmArgs a,
                                                           float c2, bool vec)
@@ -226,15 +230,23 @@ namespace mg
             if (cb > hi || cb + 511 < lo) continue; // nothing of this chunk visible
             if (vec && cb >= lo && cb + 511 <= hi) {
                 load8_stream(xr + j0, v[c]);
+                if constexpr (CAP)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[c][e] = score<SF32, true>(a, v[c][e]);
             } else {
                 if (vec && j0 + 8 <= kc && j0 <= hi && j0 + 7 >= lo)
                     load8_stream(xr + j0, v[c]);
                 else
 #pragma unroll
                     for (int e = 0; e < 8; ++e) v[c][e] = (j0 + e >= lo && j0 + e <= hi) ? xr[j0 + e] : 0.0f;
+                // a row without visible keys (lo = 0, hi = -1, mask_range)
+                // skipped every chunk above, so here 0 <= hi - lo < kc
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    v[c][e] = unsigned(j0 + e - lo) <= unsigned(hi - lo) ? v[c][e] : kNegInf;
+                for (int e = 0; e < 8; ++e) {
+                    const bool vis = unsigned(j0 + e - lo) <= unsigned(hi - lo);
+                    if constexpr (CAP) v[c][e] = vis ? score<SF32, true>(a, v[c][e]) : kNegInf;
+                    else v[c][e] = vis ? v[c][e] : kNegInf;
+                }
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) m = __builtin_fmaxf(m, v[c][e]);
@@ -256,7 +268,7 @@ namespace mg
         }
         sum = dpp_sum_f32(sum);
         if (m != kNegInf && !(sum < __builtin_huge_valf())) { // NaN / infinite scores
-            softmax_row_accurate<SF32, SO, CH, false>(a, xr, yr, lo64, hi64, vec, lane);
+            softmax_row_accurate<SF32, SO, CH, CAP>(a, xr, yr, lo64, hi64, vec, lane);
             return;
         }
         const float inv = m == kNegInf ? 0.0f : __builtin_amdgcn_rcpf(sum);
@@ -488,15 +500,16 @@ namespace mg
         if (a.kc <= 2048) {
             const unsigned blocks = unsigned((a.nrows + 3) / 4);
             need(a.nrows < (int64_t(1) << 31), "softmax: too many rows");
-            if constexpr (SI::dt == F32 && sizeof(ro) == 2 && !CAP) if (a.scale > 0.0) {
-                const float c2 = float(double(a.scale) * 1.4426950408889634);
+            if constexpr (SI::dt == F32 && sizeof(ro) == 2) if (CAP || a.scale > 0.0) {
+                // log2-domain factor: the scale folds in unless the cap comes after it
+                const float c2 = float((CAP ? 1.0 : double(a.scale)) * 1.4426950408889634);
                 const unsigned rows1 = unsigned(a.nrows); // < 2^31: checked above
                 if (a.kc <= 512)
-                    hipLaunchKernelGGL((k_softmax_fast<SO, 1>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
+                    hipLaunchKernelGGL((k_softmax_fast<SO, 1, CAP>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
                 else if (a.kc <= 1024)
-                    hipLaunchKernelGGL((k_softmax_fast<SO, 2>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
+                    hipLaunchKernelGGL((k_softmax_fast<SO, 2, CAP>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
                 else
-                    hipLaunchKernelGGL((k_softmax_fast<SO, 4>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
+                    hipLaunchKernelGGL((k_softmax_fast<SO, 4, CAP>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
                 check_launch("k_softmax_fast");
                 return;
             }

@@ -36,7 +36,6 @@
 // smaller still). Otherwise the selection runs over the full lists.
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
-#include "mg_tanh_fast.hpp"
 
 namespace mg
 {
@@ -67,29 +66,13 @@ namespace mg
     // the product and quotient of two floats rounded once in f32 equal the
     // twin's f64 result rounded f64 -> f32 (products are exact in f64; for
     // the quotient, 53 >= 2*24 + 2 makes the double rounding innocuous).
-    // tanh is the fast f64 evaluation of mg_tanh_fast.hpp, accepted when its
-    // error interval rounds to one stored value, else FDLIBM (an out-of-line
-    // call, so the unrolled per-key code stays small).
+    // tanh is tanh_stored (mg_device.hpp): a short f64 evaluation, accepted
+    // when its error interval rounds to one stored value, else FDLIBM.
     struct VTail
     {
         float mult, cap;
         void *out;
     };
-    __attribute__((noinline)) __device__ double tanh_fdlibm(double x)
-    {
-        return mgm::tanh(x);
-    }
-    template <class SI>
-    MG_DEV float tail_tanh(float v)
-    {
-        const double a = __builtin_fabs(double(v));
-        if (a == a) {
-            const double t = mgm::tanh_fast_abs(a);
-            const auto lo = SI::enc64(t - t * mgm::kTanhFastMargin), hi = SI::enc64(t + t * mgm::kTanhFastMargin);
-            if (lo == hi) return __builtin_copysignf(SI::dec(lo), v);
-        }
-        return SI::dec(SI::enc64(tanh_fdlibm(double(v))));
-    }
     template <class SI>
     MG_DEV float vtail(float x, const VTail &t)
     {
@@ -97,7 +80,7 @@ namespace mg
         if (t.mult != 1.0f) v = SI::dec(SI::enc32(v * t.mult));
         if (t.cap != 0.0f) {
             v = SI::dec(SI::enc32(v / t.cap));
-            v = tail_tanh<SI>(v);
+            v = tanh_stored<SI>(v);
             v = SI::dec(SI::enc32(v * t.cap));
         }
         return v;

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "mg_fdlibm.hpp"
+#include "mg_tanh_fast.hpp"
 
 #define MG_DEV __device__ __forceinline__
 
@@ -15,11 +16,13 @@ namespace mg
     // OR-ed into an f64 dtype: the reference's --hf-f32-compat chains
     constexpr int kF32Compat = 0x100;
 
-    // Visible keys [lo, hi] of a score row at position qpos over kc keys
-    // (hi < lo: none). mask 1 causal: j <= qpos; 2 sliding window:
-    // qpos - window < j <= qpos (src/muse_glimmer.hpp:838-843); 3 the drafter's
-    // bidirectional window: qpos - window <= j <= qpos + window
-    // (src/dflash.hpp:339-344).
+    // Visible keys [lo, hi] of a score row at position qpos over kc keys.
+    // mask 1 causal: j <= qpos; 2 sliding window: qpos - window < j <= qpos
+    // (src/muse_glimmer.hpp:838-843); 3 the drafter's bidirectional window:
+    // qpos - window <= j <= qpos + window (src/dflash.hpp:339-344). A row that
+    // sees no key gets the one canonical empty range lo = 0, hi = -1, so
+    // 0 <= lo <= kc and hi - lo >= -1 always hold (kernels may take hi - lo as
+    // an unsigned span and cast both to 32 bits for rows of < 2^31 keys).
     __host__ __device__ __forceinline__ void mask_range(int mask, int64_t qpos, int64_t kc, int64_t window,
                                                         int64_t &lo, int64_t &hi)
     {
@@ -29,12 +32,16 @@ namespace mg
             const int64_t l = qpos - window, h = qpos + window;
             lo = l > 0 ? l : 0;
             hi = h < hi ? h : hi;
-            return;
+        } else {
+            if (mask >= 1) hi = qpos < hi ? qpos : hi;
+            if (mask == 2) {
+                const int64_t l = qpos - window + 1;
+                lo = l > 0 ? l : 0;
+            }
         }
-        if (mask >= 1) hi = qpos < hi ? qpos : hi;
-        if (mask == 2) {
-            const int64_t l = qpos - window + 1;
-            lo = l > 0 ? l : 0;
+        if (lo > hi) {
+            lo = 0;
+            hi = -1;
         }
     }
 
@@ -111,6 +118,28 @@ namespace mg
         static MG_DEV raw enc64(double d) { return d; }
         static MG_DEV raw enc(comp c) { return c; }
     };
+
+    // rnd(tanh(v)) for a stored value v, the step of apply_output_tail
+    // (src/muse_glimmer.hpp:920-943) and of the score softcap: the short f64
+    // evaluation of mg_tanh_fast.hpp, accepted when t(1 - m) and t(1 + m)
+    // round to one stored value (FDLIBM's tanh, within that interval, rounds
+    // to it too), else FDLIBM itself through an out-of-line call so the
+    // unrolled per-key code that calls this stays small. NaN goes to FDLIBM.
+    __attribute__((noinline)) static __device__ double tanh_fdlibm(double x)
+    {
+        return mgm::tanh(x);
+    }
+    template <class S>
+    MG_DEV float tanh_stored(float v)
+    {
+        const double a = __builtin_fabs(double(v));
+        if (a == a) {
+            const double t = mgm::tanh_fast_abs(a);
+            const auto lo = S::enc64(t - t * mgm::kTanhFastMargin), hi = S::enc64(t + t * mgm::kTanhFastMargin);
+            if (lo == hi) return __builtin_copysignf(S::dec(lo), v);
+        }
+        return S::dec(S::enc64(tanh_fdlibm(double(v))));
+    }
 
     // --------------------------------------------------------- 16-byte vectors
     template <typename T, int N>

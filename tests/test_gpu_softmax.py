@@ -161,6 +161,66 @@ def test_all_masked_row_is_zero(prims):
     assert np.all(O.to_f64(y, BF16) == 0.0)
 
 
+@pytest.mark.parametrize("dt_out", (BF16, F16))
+@pytest.mark.parametrize("mask", (O.MASK_WINDOW, O.MASK_BIWINDOW))
+@pytest.mark.parametrize("kc,q_pos0", ((300, 330), (1000, 1030), (1800, 1830)))
+def test_window_rows_past_the_block(prims, dt_out, mask, kc, q_pos0):
+    """windowed rows whose window starts past the last key (q_pos >= kc + window - 1
+    for WINDOW, q_pos - window > kc - 1 for BIWINDOW) see no key: their clamped
+    range has lo > hi. The fast path (f32 scores, 16-bit probabilities) must
+    write zeros there, not 1/kc, while the rows before them stay exact; kc is
+    not a multiple of 512 (nor of 8 for kc = 300)."""
+    y, ref = run(prims, 3, 16, kc, dt_out=dt_out, mask=mask, window=40, q_pos0=q_pos0)
+    vis = visible(3, 16, kc, mask, 40, q_pos0)
+    empty = ~vis.any(-1)
+    assert empty.any() and (~empty).any()
+    assert np.all(O.to_f64(y, dt_out)[empty] == 0.0)
+    check(y, ref, dt_out, vis)
+
+
+@pytest.mark.parametrize("kc", (2048, 1500, 512))
+def test_softcap_fast_rows(prims, kc):
+    """softcap 30 on the fast path (f32 scores, bf16 out) at every row-length
+    class, scores spread so that the cap bends them (std 60 -> |s| up to ~25)"""
+    y, ref = run(prims, 4, 64, kc, softcap=30.0, std=60.0, q_pos0=kc - 64)
+    check(y, ref, BF16, visible(4, 64, kc, O.MASK_CAUSAL, 0, kc - 64))
+
+
+def test_softcap_split_rows(prims):
+    """softcap 30 on the split path (rows longer than 2048 keys), bf16 and f32 out"""
+    y, ref = run(prims, 3, 2, 9001, softcap=30.0, std=60.0, q_pos0=8990)
+    check(y, ref, BF16, visible(3, 2, 9001, O.MASK_CAUSAL, 0, 8990))
+    y, ref = run(prims, 2, 1, 20000, softcap=30.0, std=60.0, q_pos0=19999, dt_out=F32)
+    check(y, ref, F32, visible(2, 1, 20000, O.MASK_CAUSAL, 0, 19999))
+
+
+def test_softcap_nonfinite(prims):
+    """+-inf scores cap to +-30 (finite); a NaN score makes its row NaN"""
+    heads, q, kc = 2, 4, 2048
+    xs, x = storage(11, (heads, q, kc), F32, 0.0, 3.0)
+    x = x.copy()
+    x[0, 0, 100] = np.inf
+    x[0, 1, 5] = -np.inf
+    x[1, 2, 2000] = np.nan
+    xs = O.from_f64(x, F32)
+    dy = to_dev(np.zeros((heads, q, kc), np.uint16), BF16)
+    prims.softmax_rows(to_dev(xs, F32), dy, SCALE, O.MASK_NONE, 0, 0, 30.0)
+    y = from_dev(dy, BF16)
+    ref = O.from_f64(O.softmax_rows(x, SCALE, O.MASK_NONE, 0, 0, 30.0, F32, O.F64), BF16)
+    nan = np.zeros((heads, q), bool)
+    nan[1, 2] = True
+    assert np.array_equal(y[nan], ref[nan])
+    assert ulp_diff16(y[~nan], ref[~nan]).max() <= 1
+
+
+def test_config4_softcap_full(prims):
+    """Config 4's softcap variant at full size: f32 [40, 2048, 2048] ~ N(0, 3),
+    1/sqrt(128), causal, tanh softcap 30.0, bf16 out"""
+    y, ref = run(prims, 40, 2048, 2048, softcap=30.0)
+    n = check(y, ref, BF16, visible(40, 2048, 2048, O.MASK_CAUSAL, 0, 0))
+    print(f"config4 softcap 30: {n} of {y.size} probabilities differ from the twin by 1 ulp")
+
+
 def test_config4_full(prims):
     """Config 4 prefill at full size: f32 [40, 2048, 2048] ~ N(0, 3), causal, bf16 out."""
     y, ref = run(prims, 40, 2048, 2048)
