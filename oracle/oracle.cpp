@@ -38,11 +38,20 @@
 //   q8_0 quantize parity unpinned against llama.cpp (not vendored); checked
 //                 against its own stated invariants only
 //   vocab         full numpy sort / np.argmax / f64 lse brute force in tests
+//   sampler dist  closed forms: softmax(v/T) (scipy) when top_p = 1, min_p = 0;
+//                 the top_p cut and min_p keep brute-forced with exact
+//                 fractions on rows built away from the cut; point masses
+//                 for T <= 0 and all -inf rows; sum 1; ratios exp((v_i-v_j)/T)
+//   .npy I/O      files written by the reference's own save_npy (oracle/_ref)
+//                 read back exactly and re-written byte for byte; numpy reads
+//                 what it writes
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <numeric>
+#include <string>
 #include <vector>
 
 #include "fmath_port.hpp"
@@ -618,6 +627,245 @@ extern "C"
                 }
             }
         }
+    }
+
+    // ---------------------------------------------------------------- sampler
+    // The final candidate distribution of Sampler._transformed
+    // (serve/sampler.py:85-112), after the logit edits, restated from its
+    // definition on a row's top-K candidates (values descending, ties by lower
+    // index: what or_vocab_reduce / mg_vocab_reduce return), in f64:
+    //   no candidate above -inf, or temperature <= 0: the point mass on the
+    //     row's argmax (the "masked" and "greedy" results, sampler.py:76-78, 95-97)
+    //   C = the candidates above -inf, in order (sampler.py:99-101)
+    //   p = softmax over C (sampler.py:103 with _softmax, 163-165)
+    //   top_p < 1: the shortest prefix of C whose cumulative p reaches top_p
+    //     (sampler.py:104-106: searchsorted(cumsum(p), top_p) + 1); all of C
+    //     when no prefix reaches it
+    //   min_p > 0: of those, the c with p_c >= min_p * max p (sampler.py:107-109)
+    //   q = softmax over the kept of v_c / T, the quotient an f32 value (the
+    //     np.float32 division of sampler.py:111), renormalized
+    // top_p and min_p compare as f32 values, as numpy's float32 arrays take
+    // the python floats. Writes n[r] candidates (ids, probabilities) in order;
+    // the remaining K - n[r] slots are left as they are.
+    void or_sample_dist(const int64_t *top_idx, const double *top_val, const int64_t *amax, int64_t rows,
+                        int64_t K, double temperature, double top_p, double min_p, int64_t *out_ids,
+                        double *out_p, int64_t *out_n)
+    {
+        const double tp = double(float(top_p)), mp = double(float(min_p)), T = double(float(temperature));
+        for (int64_t r = 0; r < rows; ++r) {
+            const int64_t *ir = top_idx + r * K;
+            const double *vr = top_val + r * K;
+            int64_t nc = 0;
+            while (nc < K && vr[nc] > -HUGE_VAL) ++nc; // sorted: the finite ones come first
+            if (nc == 0 || !(temperature > 0.0)) {
+                out_ids[r * K] = amax[r];
+                out_p[r * K] = 1.0;
+                out_n[r] = 1;
+                continue;
+            }
+            std::vector<double> p(static_cast<size_t>(nc));
+            double S = 0.0;
+            for (int64_t i = 0; i < nc; ++i) S += (p[size_t(i)] = orc::exp(vr[i] - vr[0]));
+            for (auto &v : p) v /= S;
+            int64_t n = nc;
+            if (tp < 1.0) {
+                double run = 0.0;
+                for (int64_t i = 0; i < nc; ++i) {
+                    run += p[size_t(i)];
+                    if (run >= tp) {
+                        n = i + 1;
+                        break;
+                    }
+                }
+            }
+            std::vector<int64_t> kept;
+            for (int64_t i = 0; i < n; ++i)
+                if (!(mp > 0.0) || p[size_t(i)] >= mp * p[0]) kept.push_back(i);
+            std::vector<double> q(kept.size());
+            const double y0 = double(float(vr[kept[0]] / T));
+            double F = 0.0;
+            for (size_t i = 0; i < kept.size(); ++i)
+                F += (q[i] = orc::exp(double(float(vr[kept[i]] / T)) - y0));
+            for (size_t i = 0; i < kept.size(); ++i) {
+                out_ids[r * K + int64_t(i)] = ir[kept[i]];
+                out_p[r * K + int64_t(i)] = q[i] / F;
+            }
+            out_n[r] = int64_t(kept.size());
+        }
+    }
+
+    // ------------------------------------------------------------------- .npy
+    // The reference's fixture format (src/tensor.h:11-48, src/tensor.cpp:13-224):
+    // .npy v1.0, little-endian, C order. Writing: '<f8' tensors and '<i8'
+    // vectors, the header dict padded with spaces so magic + version + length
+    // field + dict + '\n' is a multiple of 64 bytes. Reading: v1 or v2 headers,
+    // '<f8', '<f4', '<i8', '<i4' and '|u1' data, widened to f64 (u1 as 0..255).
+    // The calls return 0, or -1 with the reason in or_last_error().
+    static thread_local std::string g_npy_err;
+    const char *or_last_error(void) { return g_npy_err.c_str(); }
+
+    static bool npy_write(const char *path, const char *descr, const int64_t *shape, int ndim, const void *data,
+                          size_t bytes)
+    {
+        std::string d = std::string("{'descr': '") + descr + "', 'fortran_order': False, 'shape': (";
+        for (int i = 0; i < ndim; ++i) {
+            d += std::to_string(shape[i]);
+            if (ndim == 1) d += ",";
+            else if (i + 1 < ndim) d += ", ";
+        }
+        d += "), }";
+        const size_t used = 10 + d.size() + 1; // magic(6) + version(2) + length(2) + dict + '\n'
+        d.append((64 - used % 64) % 64, ' ');
+        d += '\n';
+        FILE *f = std::fopen(path, "wb");
+        if (!f) {
+            g_npy_err = std::string("cannot write ") + path;
+            return false;
+        }
+        const uint16_t hl = uint16_t(d.size());
+        const unsigned char head[10] = {0x93, 'N', 'U', 'M', 'P', 'Y', 1, 0, uint8_t(hl & 0xff), uint8_t(hl >> 8)};
+        bool ok = std::fwrite(head, 1, 10, f) == 10 && std::fwrite(d.data(), 1, d.size(), f) == d.size() &&
+                  std::fwrite(data, 1, bytes, f) == bytes;
+        ok = (std::fclose(f) == 0) && ok;
+        if (!ok) g_npy_err = std::string("short write: ") + path;
+        return ok;
+    }
+
+    int or_save_npy_f64(const char *path, const double *data, const int64_t *shape, int ndim)
+    {
+        int64_t n = 1;
+        for (int i = 0; i < ndim; ++i) n *= shape[i];
+        return npy_write(path, "<f8", shape, ndim, data, size_t(n) * 8) ? 0 : -1;
+    }
+
+    int or_save_npy_i64(const char *path, const int64_t *data, int64_t n)
+    {
+        return npy_write(path, "<i8", &n, 1, data, size_t(n) * 8) ? 0 : -1;
+    }
+
+    // value of `key` in the header dict: the text after "'key':", spaces skipped
+    static bool npy_field(const std::string &h, const char *key, std::string &out)
+    {
+        const size_t k = h.find(std::string("'") + key + "'");
+        if (k == std::string::npos) return false;
+        size_t i = h.find(':', k);
+        if (i == std::string::npos) return false;
+        ++i;
+        while (i < h.size() && h[i] == ' ') ++i;
+        out = h.substr(i);
+        return true;
+    }
+
+    // Read the header of `path`: descr (up to 7 chars + NUL into descr_out[8]),
+    // shape (up to 8 dims), and the byte offset of the data.
+    static bool npy_head(const char *path, std::string &descr, std::vector<int64_t> &shape, long &offset)
+    {
+        FILE *f = std::fopen(path, "rb");
+        if (!f) {
+            g_npy_err = std::string("cannot open ") + path;
+            return false;
+        }
+        unsigned char m[8];
+        bool ok = std::fread(m, 1, 8, f) == 8 && std::memcmp(m, "\x93NUMPY", 6) == 0 && (m[6] == 1 || m[6] == 2);
+        uint32_t hl = 0;
+        if (ok) {
+            unsigned char l[4] = {0, 0, 0, 0};
+            const size_t w = m[6] == 1 ? 2 : 4;
+            ok = std::fread(l, 1, w, f) == w;
+            hl = uint32_t(l[0]) | uint32_t(l[1]) << 8 | uint32_t(l[2]) << 16 | uint32_t(l[3]) << 24;
+            offset = long(8 + w + hl);
+        }
+        std::string h(hl, '\0');
+        ok = ok && std::fread(&h[0], 1, hl, f) == hl;
+        std::fclose(f);
+        if (!ok) {
+            g_npy_err = std::string("not an npy file (or a short header): ") + path;
+            return false;
+        }
+        std::string v;
+        if (!npy_field(h, "descr", v) || v.size() < 2 || v[0] != '\'' || v.find('\'', 1) == std::string::npos) {
+            g_npy_err = "npy: no descr in the header";
+            return false;
+        }
+        descr = v.substr(1, v.find('\'', 1) - 1);
+        if (!npy_field(h, "fortran_order", v) || v.compare(0, 5, "False") != 0) {
+            g_npy_err = "npy: fortran order unsupported";
+            return false;
+        }
+        if (!npy_field(h, "shape", v) || v.empty() || v[0] != '(' || v.find(')') == std::string::npos) {
+            g_npy_err = "npy: no shape in the header";
+            return false;
+        }
+        shape.clear();
+        int64_t cur = -1;
+        for (size_t i = 1; i < v.find(')'); ++i) {
+            const char c = v[i];
+            if (c >= '0' && c <= '9') {
+                cur = (cur < 0 ? 0 : cur * 10) + (c - '0');
+            } else if (cur >= 0) {
+                shape.push_back(cur);
+                cur = -1;
+            }
+        }
+        if (cur >= 0) shape.push_back(cur);
+        return true;
+    }
+
+    // descr_out: char[8]; shape_out: int64[8]; returns 0 / -1
+    int or_npy_info(const char *path, char *descr_out, int64_t *shape_out, int *ndim_out)
+    {
+        std::string d;
+        std::vector<int64_t> sh;
+        long off = 0;
+        if (!npy_head(path, d, sh, off)) return -1;
+        if (sh.size() > 8 || d.size() > 7) {
+            g_npy_err = "npy: more than 8 dimensions or a long descr";
+            return -1;
+        }
+        std::memcpy(descr_out, d.c_str(), d.size() + 1);
+        for (size_t i = 0; i < sh.size(); ++i) shape_out[i] = sh[i];
+        *ndim_out = int(sh.size());
+        return 0;
+    }
+
+    // the data of `path`, widened to f64, into out[n] (n = the element count)
+    int or_load_npy(const char *path, double *out, int64_t n)
+    {
+        std::string d;
+        std::vector<int64_t> sh;
+        long off = 0;
+        if (!npy_head(path, d, sh, off)) return -1;
+        int64_t cnt = 1;
+        for (int64_t v : sh) cnt *= v;
+        if (cnt != n) {
+            g_npy_err = "npy: element count differs from the caller's";
+            return -1;
+        }
+        size_t w = 0;
+        if (d == "<f8" || d == "<i8") w = 8;
+        else if (d == "<f4" || d == "<i4") w = 4;
+        else if (d == "|u1") w = 1;
+        else {
+            g_npy_err = std::string("npy: unsupported descr ") + d + " in " + path;
+            return -1;
+        }
+        std::vector<unsigned char> raw(size_t(n) * w);
+        FILE *f = std::fopen(path, "rb");
+        bool ok = f && std::fseek(f, off, SEEK_SET) == 0 && std::fread(raw.data(), 1, raw.size(), f) == raw.size();
+        if (f) std::fclose(f);
+        if (!ok) {
+            g_npy_err = std::string("npy: short read ") + path;
+            return -1;
+        }
+        for (int64_t i = 0; i < n; ++i) {
+            const unsigned char *b = raw.data() + size_t(i) * w;
+            if (d == "<f8") { double v; std::memcpy(&v, b, 8); out[i] = v; }
+            else if (d == "<i8") { int64_t v; std::memcpy(&v, b, 8); out[i] = double(v); }
+            else if (d == "<f4") { float v; std::memcpy(&v, b, 4); out[i] = double(v); }
+            else if (d == "<i4") { int32_t v; std::memcpy(&v, b, 4); out[i] = double(v); }
+            else out[i] = double(b[0]);
+        }
+        return 0;
     }
 
     int or_num_threads(void)

@@ -57,9 +57,15 @@ _SIGS = {
     "or_dequant_q8_0": [_P, _P, _P, _I, _I, _INT],
     "or_quantize_q8_0": [_P, _P, _P, _I, _I],
     "or_vocab_reduce": [_P, _I, _I, _I, _P, _P, _P, _P],
+    "or_sample_dist": [_P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P],
+    "or_save_npy_f64": [ctypes.c_char_p, _P, _P, _INT],
+    "or_save_npy_i64": [ctypes.c_char_p, _P, _I],
+    "or_npy_info": [ctypes.c_char_p, ctypes.c_char_p, _P, ctypes.POINTER(_INT)],
+    "or_load_npy": [ctypes.c_char_p, _P, _I],
     "or_num_threads": [],
 }
 
+_INT_RESULT = ("or_num_threads", "or_save_npy_f64", "or_save_npy_i64", "or_npy_info", "or_load_npy")
 _lib = None
 
 
@@ -73,7 +79,9 @@ def lib():
         for name, args in _SIGS.items():
             fn = getattr(L, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_int if name == "or_num_threads" else None
+            fn.restype = ctypes.c_int if name in _INT_RESULT else None
+        L.or_last_error.argtypes = []
+        L.or_last_error.restype = ctypes.c_char_p
         _lib = L
     return _lib
 
@@ -278,6 +286,55 @@ def vocab_reduce(L, K):
     return lse, am, ti, tv
 
 
+def sample_dist(top_idx, top_val, argmax, temperature, top_p, min_p):
+    """Sampler._transformed's final distribution (serve/sampler.py:85-112) from a row's
+    top-K candidates (value desc, index asc). Returns (ids i64 [rows,K], probs f64
+    [rows,K], n i64 [rows]); slots past n[r] hold -1 / 0."""
+    ti = _c(top_idx, np.int64)
+    tv = _c(top_val)
+    am = _c(argmax, np.int64)
+    rows, K = ti.shape
+    ids = np.full((rows, K), -1, np.int64)
+    p = np.zeros((rows, K))
+    n = np.zeros(rows, np.int64)
+    lib().or_sample_dist(_p(ti), _p(tv), _p(am), rows, K, temperature, top_p, min_p, _p(ids), _p(p), _p(n))
+    return ids, p, n
+
+
+class NpyError(RuntimeError):
+    pass
+
+
+def _npy_check(rc):
+    if rc != 0:
+        raise NpyError(lib().or_last_error().decode())
+
+
+def save_npy(path, arr):
+    """save_npy / save_npy_i64 (src/tensor.cpp): float arrays as '<f8', int arrays
+    as a '<i8' vector (.npy v1.0, header padded to 64 bytes)."""
+    a = np.asarray(arr)
+    if a.dtype.kind in "iu":
+        a = np.ascontiguousarray(a.reshape(-1), np.int64)
+        _npy_check(lib().or_save_npy_i64(os.fsencode(path), _p(a), a.size))
+    else:
+        a = np.array(a, np.float64, order="C")  # keeps a 0-d shape (ascontiguousarray would not)
+        shape = np.array(a.shape, np.int64)
+        _npy_check(lib().or_save_npy_f64(os.fsencode(path), _p(a), _p(shape), a.ndim))
+
+
+def load_npy(path):
+    """load_npy (src/tensor.cpp): returns (f64 array of the file's shape, descr)."""
+    descr = ctypes.create_string_buffer(8)
+    shape = np.zeros(8, np.int64)
+    nd = _INT(0)
+    _npy_check(lib().or_npy_info(os.fsencode(path), descr, _p(shape), ctypes.byref(nd)))
+    shp = tuple(int(v) for v in shape[:nd.value])
+    out = np.empty(shp, np.float64)
+    _npy_check(lib().or_load_npy(os.fsencode(path), _p(out), out.size))
+    return out, descr.value.decode()
+
+
 def num_threads():
     return lib().or_num_threads()
 
@@ -301,6 +358,11 @@ class Ref:
         self.s.rs_rope_table.argtypes = [_D, _I, _I, _INT, _INT, _P, _P]
         self.s.rs_apply_rope.argtypes = [_P, _I, _P, _P, _I, _I, _INT]
         self.s.rs_output_tail.argtypes = [_D, _D, _P, _I, _INT]
+        self.s.rs_save_npy_f64.argtypes = [ctypes.c_char_p, _P, _P, _INT]
+        self.s.rs_save_npy_i64.argtypes = [ctypes.c_char_p, _P, _I]
+        self.s.rs_load_npy.argtypes = [ctypes.c_char_p, _P, _I]
+        for f in (self.s.rs_save_npy_f64, self.s.rs_save_npy_i64, self.s.rs_load_npy):
+            f.restype = _INT
         for f in (self.k.ok_powv, self.k.ok_meansq, self.s.rs_round, self.s.rs_f16_to_f64,
                   self.s.rs_rmsnorm_rows, self.s.rs_rope_table, self.s.rs_apply_rope,
                   self.s.rs_output_tail):
@@ -359,6 +421,26 @@ class Ref:
         cos_t, sin_t = _c(cos_t), _c(sin_t)
         self.s.rs_apply_rope(_p(x), x.size, _p(cos_t), _p(sin_t), cos_t.shape[0], pos, dt)
         return x
+
+    def save_npy(self, path, arr):
+        """the reference's save_npy ('<f8' tensor) or save_npy_i64 ('<i8' vector)"""
+        a = np.asarray(arr)
+        if a.dtype.kind in "iu":
+            a = np.ascontiguousarray(a.reshape(-1), np.int64)
+            rc = self.s.rs_save_npy_i64(os.fsencode(path), _p(a), a.size)
+        else:
+            a = np.array(a, np.float64, order="C")
+            shape = np.array(a.shape, np.int64)
+            rc = self.s.rs_save_npy_f64(os.fsencode(path), _p(a), _p(shape), a.ndim)
+        if rc != 0:
+            raise NpyError(f"reference save_npy failed on {path}")
+
+    def load_npy(self, path, shape):
+        """the reference's load_npy, widened to f64, for a file of `shape`"""
+        out = np.empty(shape, np.float64)
+        if self.s.rs_load_npy(os.fsencode(path), _p(out), out.size) != 0:
+            raise NpyError(f"reference load_npy failed on {path}")
+        return out
 
     def output_tail(self, z, mult, cap, dt):
         z = _c(z).copy()
