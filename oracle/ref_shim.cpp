@@ -3,14 +3,17 @@
 // copied). It exports the reference functions that have no C entry point in
 // the reference's own referee library (tools/oracle_kernels.cpp, built beside
 // it): storage rounding, rmsnorm_rows, the RoPE table and its application, the
-// output tail and the exact f16 decode. Used only to pin oracle/oracle.cpp
+// output tail, the exact f16 decode, and the .npy writer and reader of
+// src/tensor.cpp (compiled beside this file from where it lies). Used only to pin oracle/oracle.cpp
 // (tests/golden/make_golden.py and the CPU tests).
 #include <cstdint>
+#include <exception>
 #include <vector>
 
 #include "muse_glimmer.hpp"
 #include "rounding.hpp"
 #include "safetensors.hpp"
+#include "tensor.h"
 
 extern "C"
 {
@@ -61,6 +64,44 @@ extern "C"
         rt.cos.assign(cos_t, cos_t + T * (head_dim / 2));
         rt.sin.assign(sin_t, sin_t + T * (head_dim / 2));
         muse::apply_rope(x, rt, pos, prec::Dtype(dt));
+    }
+
+    // oracle::save_npy (tensor.cpp:59-73): an f64 tensor of `ndim` dims
+    int rs_save_npy_f64(const char *path, const double *data, const int64_t *shape, int ndim)
+    {
+        try {
+            oracle::Tensor t(std::vector<int64_t>(shape, shape + ndim));
+            for (size_t i = 0; i < t.data.size(); ++i) t.data[i] = data[i];
+            oracle::save_npy(path, t);
+            return 0;
+        } catch (const std::exception &) {
+            return -2;
+        }
+    }
+
+    // oracle::save_npy_i64 (tensor.cpp:75-89)
+    int rs_save_npy_i64(const char *path, const int64_t *data, int64_t n)
+    {
+        try {
+            oracle::save_npy_i64(path, std::vector<int64_t>(data, data + n));
+            return 0;
+        } catch (const std::exception &) {
+            return -2;
+        }
+    }
+
+    // oracle::load_npy (tensor.cpp:91-222): the widened values into out[n];
+    // -1 when n is not the file's element count, -2 when load_npy throws
+    int rs_load_npy(const char *path, double *out, int64_t n)
+    {
+        try {
+            const oracle::Tensor t = oracle::load_npy(path);
+            if (t.numel() != n) return -1;
+            for (int64_t i = 0; i < n; ++i) out[i] = t.data[size_t(i)];
+            return 0;
+        } catch (const std::exception &) {
+            return -2;
+        }
     }
 
     // muse::apply_output_tail (muse_glimmer.hpp:920-943)

@@ -1,6 +1,6 @@
 """Write the golden fixtures in this directory from the reference's own code.
 
-    make -C oracle ref && python tests/golden/make_golden.py
+    make -C oracle ref && python tests/golden/make_golden.py [part ...]
 
 Every expected output below is computed by the reference's C++ sources,
 compiled from /root/reference by oracle/Makefile into oracle/_ref:
@@ -9,7 +9,8 @@ sin/cos/pow, silu, sigmoid, the blocked-8 mean of squares) and
 oracle/ref_shim.cpp over src/rounding.hpp, src/safetensors.hpp and
 src/muse_glimmer.hpp (round_act, f16_to_f64, rmsnorm_rows, build_rope_table,
 apply_rope, apply_output_tail; rmsnorm_rows and build_rope_table also in
-their --hf-f32-compat branches). Inputs come from the oracle's portable seeded
+their --hf-f32-compat branches) and src/tensor.cpp (save_npy, save_npy_i64,
+load_npy: the .npy files under npy/ and what the reference reads from numpy's). Inputs come from the oracle's portable seeded
 generator (splitmix64 + Box-Muller), stored in the fixtures as well, so the
 tests never regenerate them. Loops the reference writes inline (the residual
 add, SwiGLU) are composed here from its round_act and ok_siluv exactly as
@@ -127,12 +128,37 @@ def tail():
     save("tail.npz", **out)
 
 
+def npy():
+    """.npy files written by the reference's own save_npy / save_npy_i64
+    (src/tensor.cpp), and the reference's load_npy of files numpy wrote in every
+    element type it reads ('<f8', '<f4', '<i8', '<i4', '|u1')."""
+    d = os.path.join(HERE, "npy")
+    os.makedirs(d, exist_ok=True)
+    # tests/test_npy.cpp:13-17's tensor: [2, 3], 0.1 i - 0.25
+    R.save_npy(os.path.join(d, "ref_f64_2x3.npy"), (0.1 * np.arange(6.0) - 0.25).reshape(2, 3))
+    R.save_npy(os.path.join(d, "ref_f64_2x1x5.npy"), O.to_f64(O.normal(50, (2, 1, 5), 0, 1, F64), F64))
+    R.save_npy(os.path.join(d, "ref_f64_7.npy"), O.to_f64(O.normal(51, (7,), 0, 1e10, F64), F64))
+    R.save_npy(os.path.join(d, "ref_i64_3.npy"), np.array([5, -1, 262143], np.int64))  # test_npy.cpp:26
+    rng = np.random.default_rng(52)
+    written = {
+        "np_f4": rng.normal(0, 3, (3, 4)).astype("<f4"),
+        "np_i4": rng.integers(-2**31, 2**31, (5,), dtype=np.int64).astype("<i4"),
+        "np_i8": rng.integers(-2**62, 2**62, (2, 2), dtype=np.int64).astype("<i8"),
+        "np_u1": rng.integers(0, 256, (4, 2, 2), dtype=np.int64).astype("|u1"),
+        "np_f8": rng.normal(0, 1, (3,)).astype("<f8"),
+    }
+    loaded = {}
+    for name, a in written.items():
+        path = os.path.join(d, name + ".npy")
+        np.save(path, a, allow_pickle=False)
+        loaded[name] = R.load_npy(path, a.shape)
+    save("npy.npz", **loaded)
+
+
 if __name__ == "__main__":
     if not O.Ref.available():
         sys.exit("oracle/_ref is not built (make -C oracle ref)")
-    rounding()
-    fmath()
-    config1()
-    norms()
-    rope()
-    tail()
+    parts = {"rounding": rounding, "fmath": fmath, "config1": config1, "norms": norms, "rope": rope,
+             "tail": tail, "npy": npy}
+    for name in sys.argv[1:] or parts:
+        parts[name]()
