@@ -3,7 +3,8 @@
 Quantizer: up_w (src/gpu/gpu_engine.cpp:2722-2755), bitwise against the oracle
 restatement (oracle/oracle.cpp or_quantize_q8_0). Its agreement with llama.cpp's
 quantize_row_q8_0, which is not vendored, is unpinned; the oracle is checked
-against the rule's own invariants (tests/test_oracle_math.py).
+against the rule's own invariants and its half-away-from-zero ties
+(tests/test_oracle_math.py), and the device against the same exact ties here.
 GEMV: k_gemv_q8 (src/gpu/gpu_engine.cpp:815-889) in f32 accumulation, so the
 gate is a bound, not bits: |y - y64| <= 1e-5 * sum_i |w_i x_i| against the f64
 sum of the same terms (each output adds at most ~90 f32 partial sums in
@@ -23,7 +24,7 @@ def bf16_weights(seed, rows, n_in):
     wf = O.to_f64(w, BF16)
     wf[0, :32] = 0.0                       # an all-zero block: d = 0, q = 0
     wf[1, :32] = 1e-7 * np.arange(1, 33)   # subnormal f16 scale
-    wf[2, :32] = np.arange(-16, 16) * 0.5  # products on .5 ties: half away from zero
+    wf[2, :32] = np.arange(-16, 16) * 0.5  # half-integer weights (products are not ties: id = 127/8)
     wf[3, 32:64] = -wf[3, 32:64]
     return O.from_f64(wf, BF16)
 
@@ -39,6 +40,28 @@ def test_quantize_bitwise(prims, rows, n_in):
     prims.quantize_q8_0(to_dev(w, BF16), dq, dd)
     assert np.array_equal(dq.cpu().numpy(), rq)
     assert np.array_equal(dd.cpu().numpy().view(np.uint16), rd)
+
+
+def test_quantize_exact_ties(prims):
+    """blocks whose products x * id land exactly on k + 1/2 (id a power of two):
+    lround's half away from zero, sign(x) (k + 1), not half-to-even"""
+    import torch
+    ks = np.array([0, 1, 2, 3, 4, 5, 62, 125, 0, 1, 2, 7, 9, 100, 126, 64,
+                   0, 3, 6, 11, 20, 40, 80, 99, 1, 2, 4, 8, 16, 32, 120], np.int64)
+    sign = np.where(np.arange(ks.size) % 3 == 1, -1, 1)
+    rows = []
+    for amax, idv in ((127.0, 1.0), (63.5, 2.0), (254.0, 0.5)):
+        x = np.concatenate([[amax], sign * (ks + 0.5) / idv]).astype(np.float32)
+        rows.append((x.view(np.uint32) >> 16).astype(np.uint16))
+    w = np.tile(np.concatenate(rows), (4, 1))  # [4, 96]: three tie blocks per row
+    dq = torch.empty((4, 96), dtype=torch.int8, device="cuda:0")
+    dd = torch.empty((4, 3), dtype=torch.int16, device="cuda:0")
+    prims.quantize_q8_0(to_dev(w, BF16), dq, dd)
+    want = np.tile(np.concatenate([[127], sign * (ks + 1)]), 3)
+    got = dq.cpu().numpy().astype(np.int64)
+    for r in range(4):
+        assert np.array_equal(got[r], want), r
+    assert np.array_equal(dd.cpu().numpy().view(np.float16).astype(np.float64), np.tile([1.0, 0.5, 2.0], (4, 1)))
 
 
 def gemv_case(prims, rows, n_in, B, blockdot, seed=52):

@@ -398,6 +398,31 @@ def test_quantize_invariants():
     assert np.all(np.abs(dd - d32) <= d32 * 2.0**-11)
 
 
+def test_quantize_ties_round_half_away_from_zero():
+    """up_w's q = (int8)lround(x * id) (src/gpu/gpu_engine.cpp:2722-2755): a product
+    that lands exactly on k + 1/2 rounds away from zero, to sign(x) (k + 1). The
+    blocks are built so that id is a power of two and x * id is exact: amax 127
+    gives d = 1, amax 63.5 gives d = 1/2 (id = 2), amax 254 gives d = 2 (id = 1/2);
+    every other element is a tie at that scale. Half-to-even (rint, np.round) would
+    give 0 for 0.5, 2 for 2.5 and -2 for -2.5 and fails here."""
+    ks = np.array([0, 1, 2, 3, 4, 5, 62, 125, 0, 1, 2, 7, 9, 100, 126, 64,
+                   0, 3, 6, 11, 20, 40, 80, 99, 1, 2, 4, 8, 16, 32, 120], np.int64)
+    sign = np.where(np.arange(ks.size) % 3 == 1, -1, 1)
+    blocks = []
+    for amax, idv in ((127.0, 1.0), (63.5, 2.0), (254.0, 0.5)):
+        x = np.concatenate([[amax], sign * (ks + 0.5) / idv]).astype(np.float32)  # x * id = sign (k + 1/2)
+        b = x.view(np.uint32)
+        assert np.all((b & 0xffff) == 0) and np.abs(x).max() == amax  # exact bf16 values
+        blocks.append((b >> 16).astype(np.uint16))
+    qs, d = O.quantize_q8_0(np.stack(blocks))
+    assert np.array_equal(d.view(np.float16).astype(np.float64).ravel(), [1.0, 0.5, 2.0])
+    away = np.concatenate([[127], sign * (ks + 1)])
+    even = np.concatenate([[127], np.round(sign * (ks + 0.5)).astype(np.int64)])
+    assert not np.array_equal(away, even)
+    for r in range(3):
+        assert np.array_equal(qs[r].astype(np.int64), away), r
+
+
 # -------------------------------------------------------------------- vocab
 def test_vocab_vs_numpy():
     from scipy.special import logsumexp
