@@ -22,8 +22,8 @@ is served from the 256 MiB Infinity Cache.
 
 `cpu_baseline` times the CPU restatement of the reference's own tensor path
 (oracle/liboracle.so: f64 twin arithmetic with OpenMP over rows, as
-src/muse_glimmer.hpp runs it) on a bounded sample of the same three ops and
-reports it in the same unit.
+src/muse_glimmer.hpp runs it) on a bounded sample (1/8 of the rows) of every
+BASELINE op, and reports the step's three in the same unit as `value`.
 """
 from __future__ import annotations
 
@@ -68,7 +68,10 @@ BYTES = {
                        + 2 * 2 * T * (HD // 2),
     # q and the K/V ring read, f32 out written (the op is bound by the matrix cores: FLOPS)
     "attn_prefill_4096": 2 * T * Q_H * HD + 2 * 2 * T * K_H * HD + 4 * T * Q_H * HD,
+    # a plain device copy (torch's copy kernel): the access-pattern ceiling the others are read against
+    "copy_256MiB": 2 * (256 << 20),
 }
+BYTES["softmax_causal_softcap30"] = BYTES["softmax_causal"]
 # matrix-core ops: q.k and p.v over the causal pairs, 2 * 2 * head_dim flops per (query, key)
 FLOPS = {"attn_prefill_4096": Q_H * (T * (T + 1) // 2) * 4 * HD}
 PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
@@ -87,6 +90,8 @@ KERNEL_OF = {
     "gemv_q8_0_decode": "k_gemv_q8_0<1>",
     "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
     "attn_prefill_4096": "k_attn_prefill<5,4,1,4>",
+    "softmax_causal_softcap30": "k_softmax_fast<cap>",
+    "copy_256MiB": "torch copy (memory-only probe)",
 }
 
 
@@ -99,8 +104,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
                     help="comma-separated ops to run --steps times each, with the cache flush before every "
-                         "launch (for profilers); 'copy' adds a plain 256 MiB device copy for counter calibration")
-    ap.add_argument("--cpu-seconds", type=float, default=5.0, help="CPU time per op in the CPU baseline")
+                         "launch (for profilers); 'copy' is the plain 256 MiB device copy (counter calibration)")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU time per op in the CPU baseline")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "pmc_traffic.txt"),
                     help="measured HBM bytes per launch (kernel  fetch_bytes  write_bytes)")
     return ap.parse_args()
@@ -157,6 +162,8 @@ def make_inputs(torch, P):
     I["pk"] = randn((T, K_H, HD))
     I["pv"] = randn((T, K_H, HD))
     I["pout"] = torch.empty((T, Q_H, HD), dtype=torch.float32, device=dev)
+    I["copy_src"] = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+    I["copy_dst"] = torch.empty_like(I["copy_src"])
     torch.cuda.synchronize()
 
     scale = 1.0 / math.sqrt(HD)
@@ -170,6 +177,8 @@ def make_inputs(torch, P):
         "residual_rmsnorm": lambda: P.residual_rmsnorm(M.PLAIN, I["h"], I["x"], I["w"], 1e-6, I["y"]),
         "swiglu": lambda: P.swiglu(I["gate"], I["up"], I["act"]),
         "softmax_causal": lambda: P.softmax_rows(I["scores"], I["probs"], scale, M.MASK_CAUSAL),
+        "softmax_causal_softcap30": lambda: P.softmax_rows(I["scores"], I["probs"], scale, M.MASK_CAUSAL, 0, 0,
+                                                           30.0),
         "rope": lambda: P.apply_rope(I["q"], I["k"], I["cos"], I["sin"]),
         "softmax_decode": lambda: P.softmax_rows(I["dscores"], I["dprobs"], scale, M.MASK_CAUSAL, 0, DEC_K - 1),
         "dequant_q8_0": lambda: P.dequant_q8_0(I["qs"], I["qd"], I["deq"]),
@@ -181,6 +190,7 @@ def make_inputs(torch, P):
         "attn_prefill_4096": lambda: P.attn_prefill(I["q"], I["pk"], I["pv"], 0, scale, 0, I["pout"]),
         "qk_norm_rope_kv": lambda: P.qk_norm_rope(I["q"], I["k"], 1e-6, 3.87, I["cos"], I["sin"], None, 0, I["v"],
                                                   I["kcache"], I["vcache"]),
+        "copy_256MiB": lambda: I["copy_dst"].copy_(I["copy_src"]),
     }
     for t in (1, 4, 16, 64):
         ops[f"residual_rmsnorm_T{t}"] = (lambda t=t: P.residual_rmsnorm(
@@ -220,33 +230,78 @@ def read_traffic(path, kernel):
     return None
 
 
+def host_isa():
+    """CPU model and the vector ISA the oracle was built for (oracle/Makefile)."""
+    model = flags = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and not model:
+                    model = line.split(":", 1)[1].strip()
+                if line.startswith("flags") and not flags:
+                    flags = line.split(":", 1)[1]
+    except OSError:
+        pass
+    have = [x for x in ("avx2", "fma", "avx512f", "avx512_bf16") if f" {x}" in flags]
+    return model, have
+
+
 def cpu_baseline(seconds):
-    """The reference's CPU tensor path (the oracle restatement, OpenMP over rows)
-    on a bounded sample of the step's three ops, in the same unit (GB/s): each
-    op runs on its sample repeatedly for about `seconds`."""
+    """The reference's CPU tensor path (the oracle restatement, f64 twin arithmetic
+    with OpenMP over rows / (token, head) pairs as src/muse_glimmer.hpp runs it, the
+    k_dequant_q8 formula as a CPU loop, the host argmax / partial_sort / lse) on a
+    bounded sample of every BASELINE op: 1/8 of the rows (heads, tokens) of each
+    config, each run repeatedly for about `seconds`, timed without the Python
+    wrappers' copies (the oracle's C entry points on preallocated arrays)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle as O
-    rows_n, rows_s, sm_h = 512, 512, 5
-    sample = {
-        "residual_rmsnorm": (rows_n, 4 * 2 * rows_n * D + 2 * D),
-        "swiglu": (rows_s, 3 * 2 * rows_s * FFN),
-        "softmax_causal": (sm_h, sm_h * (SM_Q * (SM_Q + 1) // 2) * 4 + sm_h * SM_Q * SM_K * 2),
-    }
-    h = O.to_f64(O.normal(1, (rows_n, D), 0, 1, O.BF16), O.BF16)
-    x = O.to_f64(O.normal(2, (rows_n, D), 0, 1, O.BF16), O.BF16)
+    L = O.lib()
+    p = O._p
+    rn, rs, smh, rt, q8r, vr = T // 8, T // 8, SM_H // 8, T // 8, Q8_R // 8, V_ROWS // 8
+    h = O.to_f64(O.normal(1, (rn, D), 0, 1, O.BF16), O.BF16)
+    x = O.to_f64(O.normal(2, (rn, D), 0, 1, O.BF16), O.BF16)
     w = O.to_f64(O.normal(3, (D,), 1, 0.05, O.BF16), O.BF16)
-    gt = O.to_f64(O.normal(4, (rows_s, FFN), 0, 1, O.BF16), O.BF16)
-    up = O.to_f64(O.normal(5, (rows_s, FFN), 0, 1, O.BF16), O.BF16)
-    sc = O.to_f64(O.normal(8, (sm_h, SM_Q, SM_K), 0, 3, O.F32), O.F32)
+    y = np.empty_like(h)
+    gt = O.to_f64(O.normal(4, (rs, FFN), 0, 1, O.BF16), O.BF16)
+    up = O.to_f64(O.normal(5, (rs, FFN), 0, 1, O.BF16), O.BF16)
+    act = np.empty_like(gt)
+    sc = O.to_f64(O.normal(8, (smh, SM_Q, SM_K), 0, 3, O.F32), O.F32)
+    pr = np.empty_like(sc)
+    qk = O.to_f64(O.normal(6, (rt, Q_H + K_H, HD), 0, 1, O.BF16), O.BF16)  # q and k heads of rt tokens
+    co, si = O.rope_table(1e6, HD, rt, O.BF16)
+    pos = np.arange(rt, dtype=np.int64)
+    dsc = O.to_f64(O.normal(9, (smh, 1, DEC_K), 0, 3, O.F32), O.F32)
+    dpr = np.empty_like(dsc)
+    qs = O.int8_uniform(10, (q8r, Q8_C))
+    qd = O.from_f64(O.uniform(11, (q8r, Q8_C // 32), 1e-3, 2e-2), O.F16)
+    deq = np.empty((q8r, Q8_C))
+    lg = O.to_f64(O.normal(12, (vr, VOCAB), 0, 4, O.F32), O.F32)
+    lse, am = np.empty(vr), np.empty(vr, np.int64)
+    ti, tv = np.empty((vr, TOPK), np.int64), np.empty((vr, TOPK))
+    scale = 1 / math.sqrt(HD)
+    hw = h.copy()
     fns = {
-        "residual_rmsnorm": lambda: O.residual_rmsnorm(O.PLAIN, h, x, w, 1e-6, O.BF16),
-        "swiglu": lambda: O.swiglu(gt, up, O.BF16),
-        "softmax_causal": lambda: O.softmax_rows(sc, 1 / math.sqrt(HD), O.MASK_CAUSAL, 0, 0, 0.0, O.F32, O.BF16),
+        "residual_rmsnorm": (lambda: L.or_residual_rmsnorm(O.PLAIN, p(hw), p(x), p(w), 1e-6, p(y), rn, D, O.BF16),
+                             4 * 2 * rn * D + 2 * D, f"bf16-twin [{rn},{D}]"),
+        "swiglu": (lambda: L.or_swiglu(p(gt), p(up), p(act), gt.size, O.BF16), 3 * 2 * rs * FFN,
+                   f"bf16-twin [{rs},{FFN}]"),
+        "softmax_causal": (lambda: L.or_softmax_rows(p(sc), p(pr), smh, SM_Q, SM_K, scale, O.MASK_CAUSAL, 0, 0, 0.0,
+                                                     O.F32, O.BF16),
+                           smh * (SM_Q * (SM_Q + 1) // 2) * 4 + smh * SM_Q * SM_K * 2, f"f32->bf16 [{smh},{SM_Q},{SM_K}]"),
+        "rope": (lambda: L.or_apply_rope(p(qk), rt, Q_H + K_H, HD, (Q_H + K_H) * HD, p(co), p(si), p(pos), O.BF16),
+                 2 * 2 * rt * (Q_H + K_H) * HD + 2 * 2 * rt * (HD // 2), f"bf16-twin q+k [{rt},{Q_H}+{K_H},{HD}]"),
+        "softmax_decode": (lambda: L.or_softmax_rows(p(dsc), p(dpr), smh, 1, DEC_K, scale, O.MASK_CAUSAL, 0,
+                                                     DEC_K - 1, 0.0, O.F32, O.BF16),
+                           smh * DEC_K * (4 + 2), f"f32->bf16 [{smh},1,{DEC_K}]"),
+        "dequant_q8_0": (lambda: L.or_dequant_q8_0(p(qs), p(qd), p(deq), q8r, Q8_C, O.BF16),
+                         q8r * Q8_C * 3 + q8r * (Q8_C // 32) * 2, f"[{q8r},{Q8_C}] -> bf16"),
+        "vocab_lse_argmax_top64": (lambda: L.or_vocab_reduce(p(lg), vr, VOCAB, TOPK, p(lse), p(am), p(ti), p(tv)),
+                                   vr * VOCAB * 4 + vr * (8 + 8) + vr * TOPK * 12, f"f32 [{vr},{VOCAB}], K={TOPK}"),
     }
     per = {}
-    tot_b = tot_s = 0.0
-    for name, fn in fns.items():
+    step_b = step_s = 0.0
+    for name, (fn, b, what) in fns.items():
         fn()
         reps = 0
         t0 = time.perf_counter()
@@ -254,20 +309,27 @@ def cpu_baseline(seconds):
             fn()
             reps += 1
         dt = (time.perf_counter() - t0) / reps
-        b = sample[name][1]
-        per[name] = {"us": round(dt * 1e6, 1), "GBps": round(b / dt / 1e9, 3), "reps": reps}
-        tot_b += b
-        tot_s += dt
+        per[name] = {"us": round(dt * 1e6, 1), "GBps": round(b / dt / 1e9, 3), "reps": reps, "sample": what,
+                     "bytes": b}
+        if name in STEP_OPS:
+            step_b += b
+            step_s += dt
+    model, isa = host_isa()
     del np
     return {
-        "value": round(tot_b / tot_s / 1e9, 3),
+        "value": round(step_b / step_s / 1e9, 3),
         "unit": "GB/s",
         "cores": O.num_threads(),
         "kind": "port",
-        "sample": (f"residual_rmsnorm bf16-twin [{rows_n},{D}], swiglu bf16-twin [{rows_s},{FFN}], "
-                   f"causal softmax f32->bf16 [{sm_h},{SM_Q},{SM_K}] (1/8 of the step's rows each), repeated "
-                   f"~{seconds:g} s per op; f64 arrays as src/muse_glimmer.hpp holds them; "
-                   f"OpenMP threads={O.num_threads()}, host nproc={os.cpu_count()}"),
+        "sample": (f"1/8 of each BASELINE config's rows (heads, tokens): {per['residual_rmsnorm']['sample']} "
+                   f"residual+RMSNorm, {per['swiglu']['sample']} SwiGLU, causal softmax "
+                   f"{per['softmax_causal']['sample']} (value = these three, the step); every op in `ops`; "
+                   f"each repeated ~{seconds:g} s; f64 arrays as src/muse_glimmer.hpp holds them"),
+        "threads": O.num_threads(),
+        "nproc": os.cpu_count(),
+        "cpu_model": model,
+        "build": "g++ -O3 -ffp-contract=off -fno-math-errno -fopenmp -march=x86-64-v3 (oracle/Makefile)",
+        "host_isa": isa,
         "ops": per,
     }
 
@@ -287,9 +349,7 @@ def main():
 
     if args.only:
         flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0")
-        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
-        dst = torch.empty_like(src)
-        ops["copy"] = lambda: dst.copy_(src)
+        ops["copy"] = ops["copy_256MiB"]
         for name in args.only.split(","):
             fn = ops[name]
             for _ in range(args.warmup):
