@@ -247,6 +247,22 @@ int mg_gemv_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, const uint16_
 int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, int dtype_in,
                     int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val);
 
+/* mg_vocab_reduce without a context, allocating nothing: NO COUNTERPART in the
+ * reference. For callers that cannot allocate device memory or hold a context
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same kernels and results as mg_vocab_reduce (dtype_in f32 or
+ * bf16, 0 < K <= 256, any output pointer may be NULL), launched on `stream`
+ * (hipStream_t; NULL = the default stream) of the current HIP device. The
+ * reduction partials live in a fixed 16 MiB device array (one per GPU, held
+ * until the process ends; its address is looked up once per device, which
+ * allocates nothing): a call needs rows * ceil(V / 2048) * 1128 bytes of it
+ * (K <= 64; 2152 for larger K), e.g. 64 rows x V = 201088 take 7.1 MB, and a
+ * call needing more fails with an error before launching anything. Every call
+ * on one GPU shares that array: calls that overlap on one GPU (concurrent
+ * streams) race; serialize them. */
+int mg_vocab_reduce_noalloc(void *stream, const void *logits, int64_t rows, int64_t V, int dtype_in, int64_t K,
+                            double *lse, int64_t *argmax, int64_t *top_idx, float *top_val);
+
 /* The output tail fused into the vocab pass: every logit first becomes
  * apply_output_tail's value (z = rnd(z*mult); z = rnd(cap*rnd(tanh(rnd(z/cap)))),
  * rounded to dtype_in at each step, FDLIBM tanh; src/muse_glimmer.hpp:920-943,

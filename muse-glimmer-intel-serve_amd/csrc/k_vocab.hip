@@ -37,6 +37,9 @@
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
 
+#include <mutex>
+#include <string>
+
 namespace mg
 {
     constexpr int kVLane = 32;           // keys per lane in pass 1
@@ -697,9 +700,11 @@ namespace mg
         }
     }
 
-    void launch_vocab(mg_ctx *c, const void *logits, int64_t rows, int64_t V, int dt_in, int64_t K,
-                      double *lse, int64_t *amax, int64_t *top_idx, float *top_val, bool tail_on, double mult,
-                      double cap, void *logits_out)
+    // The pass on `stream` with its partials in `work` (work_bytes long);
+    // `room` names where they live for the error raised when they do not fit.
+    static void vocab_pass(hipStream_t stream, void *work, int64_t work_bytes, const char *room, const void *logits,
+                           int64_t rows, int64_t V, int dt_in, int64_t K, double *lse, int64_t *amax,
+                           int64_t *top_idx, float *top_val, bool tail_on, double mult, double cap, void *logits_out)
     {
         need(rows >= 0 && V > 0, "vocab_reduce: bad shape");
         need(V < (int64_t(1) << 31), "vocab_reduce: V must be < 2^31");
@@ -715,8 +720,10 @@ namespace mg
         const int lcap = small ? 128 : 256; // list capacity per chunk
         const int64_t nc = rows * nch;
         const int64_t need_bytes = nc * int64_t(sizeof(VPart) + sizeof(uint64_t) * (kBlk + lcap));
-        need(need_bytes <= c->work_bytes, "vocab_reduce: partials exceed the context workspace (raise workspace_bytes at mg_open)");
-        VPart *part = static_cast<VPart *>(c->work);
+        need(need_bytes <= work_bytes, "vocab_reduce: the partials of " + std::to_string(rows) + " rows x " +
+                                           std::to_string(nch) + " chunks need " + std::to_string(need_bytes) +
+                                           " bytes, more than " + room + " (" + std::to_string(work_bytes) + ")");
+        VPart *part = static_cast<VPart *>(work);
         uint64_t *blk = reinterpret_cast<uint64_t *>(part + nc);
         uint64_t *lst = blk + nc * kBlk;
         const dim3 g1{unsigned((nch + 3) / 4), unsigned(rows), 1u};
@@ -724,9 +731,9 @@ namespace mg
         // python-float scalars are f32 opmath values outside f64 (src/muse_glimmer.hpp:924-926)
         const VTail tail{float(mult), float(cap), logits_out};
         auto go = [&](auto chunk, auto merge, const auto *x) {
-            hipLaunchKernelGGL(chunk, g1, dim3(256), 0, c->stream, x, V, int(K), nch, part, blk, lst, tail);
+            hipLaunchKernelGGL(chunk, g1, dim3(256), 0, stream, x, V, int(K), nch, part, blk, lst, tail);
             check_launch("k_vocab_chunk");
-            hipLaunchKernelGGL(merge, g2, dim3(64), 0, c->stream, x, V, int(K), nch, lcap, part, blk, lst, lse, amax,
+            hipLaunchKernelGGL(merge, g2, dim3(64), 0, stream, x, V, int(K), nch, lcap, part, blk, lst, lse, amax,
                                top_idx, top_val, tail);
             check_launch("k_vocab_merge");
         };
@@ -753,5 +760,50 @@ namespace mg
         } else {
             fail("vocab_reduce: input dtype must be f32 or bf16");
         }
+    }
+
+    void launch_vocab(mg_ctx *c, const void *logits, int64_t rows, int64_t V, int dt_in, int64_t K,
+                      double *lse, int64_t *amax, int64_t *top_idx, float *top_val, bool tail_on, double mult,
+                      double cap, void *logits_out)
+    {
+        vocab_pass(c->stream, c->work, c->work_bytes, "the context workspace (raise workspace_bytes at mg_open)",
+                   logits, rows, V, dt_in, K, lse, amax, top_idx, top_val, tail_on, mult, cap, logits_out);
+    }
+
+    // ------------------------------------------------- allocation-free variant
+    // The same pass with its partials in `scratch`, a fixed array in device
+    // memory (one copy per GPU, held until the process ends) instead of a
+    // context's workspace: nothing is allocated, on the first call or later.
+    // The kernels write every partial before they read it, so the array needs
+    // no clearing between calls; calls that overlap on one GPU (two streams)
+    // share it and race.
+    static __device__ __align__(256) unsigned char scratch[kVocabScratchBytes];
+
+    // scratch's device address on the current device, looked up once per device
+    // (hipGetSymbolAddress allocates nothing); host code passes this address,
+    // never the array's name, which on the host is a stand-in.
+    static void *scratch_address()
+    {
+        constexpr int kMaxDevices = 64;
+        static std::mutex mu;
+        static void *addr[kMaxDevices] = {};
+        int dev = -1;
+        check(hipGetDevice(&dev), "vocab_reduce_noalloc: hipGetDevice");
+        need(dev >= 0 && dev < kMaxDevices, "vocab_reduce_noalloc: device index out of range");
+        std::lock_guard<std::mutex> lock(mu);
+        if (!addr[dev]) {
+            void *p = nullptr;
+            check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "vocab_reduce_noalloc: hipGetSymbolAddress(scratch)");
+            need(p != nullptr, "vocab_reduce_noalloc: no device address for the scratch array");
+            addr[dev] = p;
+        }
+        return addr[dev];
+    }
+
+    void launch_vocab_noalloc(hipStream_t stream, const void *logits, int64_t rows, int64_t V, int dt_in, int64_t K,
+                              double *lse, int64_t *amax, int64_t *top_idx, float *top_val)
+    {
+        vocab_pass(stream, scratch_address(), kVocabScratchBytes, "the fixed scratch array", logits, rows, V, dt_in,
+                   K, lse, amax, top_idx, top_val, false, 1.0, 0.0, nullptr);
     }
 } // namespace mg

@@ -6,7 +6,9 @@
 // c_api.cpp:15-17, 35, 170-188) and nothing allocates device memory after
 // mg_open returns (c_api.cpp:9-14): the lookup tables and the reduction
 // workspace are allocated there, and a call whose partials would not fit the
-// workspace fails instead of growing it.
+// workspace fails instead of growing it. mg_vocab_reduce_noalloc takes no
+// context and allocates nothing at all (its partials live in a fixed device
+// array, k_vocab.hip).
 #include "mg_prims.h"
 
 #include "mg_internal.hpp"
@@ -268,7 +270,15 @@ int mg_vocab_reduce_tail(mg_ctx *ctx, const void *logits, int64_t rows, int64_t 
     });
 }
 
-} // extern "C"
+int mg_vocab_reduce_noalloc(void *stream, const void *logits, int64_t rows, int64_t V, int dtype_in, int64_t K,
+                            double *lse, int64_t *argmax, int64_t *top_idx, float *top_val)
+{
+    MG_GUARD(-1, {
+        mg::launch_vocab_noalloc(static_cast<hipStream_t>(stream), logits, rows, V, dtype_in, K, lse, argmax, top_idx,
+                                 top_val);
+        return 0;
+    });
+}
 
 int mg_sample_dist(mg_ctx *ctx, const int64_t *top_idx, const float *top_val, const int64_t *argmax, int64_t rows,
                    int64_t K, double temperature, double top_p, double min_p, int64_t *cand_ids, float *cand_probs,
@@ -319,3 +329,5 @@ int mg_attn_decode(mg_ctx *ctx, const uint16_t *q, const uint16_t *k_cache, cons
         return 0;
     });
 }
+
+} // extern "C"

@@ -63,6 +63,7 @@ _SIGS = {
     "mg_attn_prefill": ([_P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _D, _P, _I], _INT),
     "mg_sample_dist": ([_P, _P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P], _INT),
     "mg_vocab_reduce_tail": ([_P, _P, _I, _I, _INT, _D, _D, _I, _P, _P, _P, _P, _P], _INT),
+    "mg_vocab_reduce_noalloc": ([_P, _P, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
 }
 
 _lib = None
@@ -289,6 +290,16 @@ class Prims:
                                              _ptr(argmax), _ptr(top_idx) if K > 0 else None,
                                              _ptr(top_val) if K > 0 else None))
         return lse, argmax, top_idx, top_val
+
+    def vocab_reduce_noalloc(self, logits, K, lse, argmax, top_idx, top_val, stream=None):
+        """vocab_reduce through mg_vocab_reduce_noalloc: no context workspace, the
+        library's fixed scratch array instead; outputs must be given (nothing is
+        allocated). `stream` defaults to this context's stream."""
+        rows, V = logits.shape
+        s = self.stream() if stream is None else stream
+        rc = self.lib.mg_vocab_reduce_noalloc(ctypes.c_void_p(s), _ptr(logits), rows, V, _dtype_code(logits), K,
+                                              _ptr(lse), _ptr(argmax), _ptr(top_idx), _ptr(top_val))
+        self._check(rc)
 
     def sample_dist(self, top_idx, top_val, argmax, temperature, top_p, min_p):
         """serve/sampler.py's candidate distribution (ids, probs, count per row) from a vocab pass."""
