@@ -24,16 +24,20 @@
 // same XCD in both passes) and writes the probabilities.
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
+#include "mg_softcap_fast.hpp"
 
 namespace mg
 {
     constexpr int kSplitChunk = 4096; // keys per work-group in the split path (256 x 16)
+    constexpr unsigned kLdsPerCu = 160u * 1024u; // gfx950
+    constexpr unsigned kFastWavesNoCap = 4;      // waves per SIMD of the fast path without a cap
     constexpr float kNegInf = -__builtin_huge_valf();
 
     struct SmArgs
     {
         int64_t nrows, q, kc;
         float scale, cap;
+        float rcap; // RN(1 / cap): the fast path's quotient (mg_softcap_fast.hpp)
         int mask;
         int64_t window, q_pos0;
     };
@@ -57,6 +61,38 @@ namespace mg
             s = SI::dec(SI::enc32(s * a.cap));
         }
         return s;
+    }
+
+    // the plain capped-score chain for the keys the fast one does not certify;
+    // out of line, so the unrolled per-key code stays small
+    __attribute__((noinline)) __device__ float capped_score_slow(float x, float scale, float cap)
+    {
+        const float s = (x * scale) / cap; // f32 operations: the twin's f64 ones rounded to f32
+        return float(mgm::tanh(double(s))) * cap;
+    }
+
+    // 8 raw f32 scores of a row -> capped scores (bit e of vis set: key e is
+    // visible, else it becomes -inf). Each key takes mgm::softcap_score_fast;
+    // the few it does not certify (|s / cap| >= 2^-5, or a rounding too close
+    // to call) are redone by the plain chain, behind one wave-uniform branch.
+    MG_DEV void cap8(const SmArgs &a, float *v, uint32_t vis)
+    {
+        float x[8];
+        uint32_t slow = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            x[e] = v[e];
+            bool ok;
+            const float c = mgm::softcap_score_fast(x[e], a.scale, a.cap, a.rcap, ok);
+            const bool in = (vis >> e) & 1u;
+            v[e] = in ? c : kNegInf;
+            slow |= uint32_t(in && !ok) << e;
+        }
+        if (__builtin_amdgcn_ballot_w64(slow != 0u)) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if ((slow >> e) & 1u) v[e] = capped_score_slow(x[e], a.scale, a.cap);
+        }
     }
 
     // 8 consecutive values -> f32 (two 16-byte loads for f32, one for 16-bit)
@@ -201,55 +237,103 @@ namespace mg
     // normalisation; relative error a few 1e-7, well inside the 16-bit
     // output's half-ulp of 2e-3, so outputs stay within 1 ulp of the twin.
     // With a softcap (CAP) each visible key first becomes the twin's capped
-    // score, bit for bit (score<SF32, true>: the scaled score, the f32
-    // quotient by cap, tanh_stored, the product by cap), and c2 = log2 e.
+    // score, bit for bit (cap8: mgm::softcap_score_fast, and the plain chain
+    // for the keys it does not certify), and c2 = log2 e.
     // Key indices are 32-bit (rows of at most 2048 keys); chunks entirely
     // visible skip the per-key mask, chunks entirely masked skip the
     // arithmetic and store zeros. A row whose sum is not finite (NaN or
     // infinite scores) is redone on the accurate path.
+    //
+    // One row of the fast path in a wave's registers: lane `lane` holds keys
+    // 512 c + 8 lane + e, raw scores until fast_finish transforms them.
+    template <int CH>
+    struct FastRow
+    {
+        float v[CH][8];
+        int64_t lo64, hi64;
+        bool live;
+    };
+
+    // issue the loads of a row's visible 512-key chunks (nothing waits on them
+    // here; the finish waits for each chunk's own loads).
+    // VEC (rows of a multiple of 8 keys, 16-byte aligned): every lane issues
+    // its two 16-byte loads per chunk as raw buffer loads over the row's
+    // visible prefix [0, hi]; loads of keys past hi (and lanes wholly below lo,
+    // sent past the end) are out of range, return zeros and touch no memory.
+    // With no branch around them the compiler counts the loads exactly and a
+    // chunk waits only for its own data. Otherwise keys load one by one.
+    template <int CH, bool VEC>
+    MG_DEV void fast_load(const SmArgs &a, const float *__restrict__ x, int64_t row, int lane, FastRow<CH> &r)
+    {
+        // a row past the end gets the empty range, so its loads (out of
+        // range) touch nothing; no branch, so the load count stays exact
+        r.live = row < a.nrows;
+        row_range(a, row, r.lo64, r.hi64);
+        r.lo64 = r.live ? r.lo64 : 0;
+        r.hi64 = r.live ? r.hi64 : -1;
+        const int lo = int(r.lo64), hi = int(r.hi64); // 0 <= lo <= kc, -1 <= hi < kc <= 2048
+        const float *xr = x + row * a.kc;
+        if constexpr (VEC) {
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+            // word 3 of a gfx9 raw buffer descriptor (32-bit data, no swizzle)
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(xr), short(0), (hi + 1) * 4, 0x00020000);
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int j0 = c * 512 + lane * 8;
+                const int off = j0 + 7 >= lo ? j0 * 4 : 0x40000000;
+                const u32x4 p = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2); // 2: non-temporal
+                const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, 2);
+                // (element to a prvalue first: this clang lowers bit_cast of an
+                // ext_vector element lvalue to a read of element 0)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    r.v[c][e] = __builtin_bit_cast(float, uint32_t(p[e]));
+                    r.v[c][e + 4] = __builtin_bit_cast(float, uint32_t(q[e]));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int j0 = c * 512 + lane * 8;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) r.v[c][e] = (j0 + e >= lo && j0 + e <= hi) ? xr[j0 + e] : 0.0f;
+            }
+        }
+    }
+
+    // transform, normalise and store a loaded row; returns true (nothing
+    // stored) for a row whose sum is not finite (NaN or infinite scores),
+    // which the caller redoes on the accurate path
     template <class SO, int CH, bool CAP>
-    __global__ __launch_bounds__(64) void k_softmax_fast(const float *__restrict__ x,
-                                                          typename SO::raw *__restrict__ y, SmArgs a,
-                                                          float c2, bool vec)
+    MG_DEV bool fast_finish(const SmArgs &a, typename SO::raw *__restrict__ y, int64_t row, float c2, bool vec,
+                            int lane, FastRow<CH> &r)
     {
         using ro = typename SO::raw;
-        const int64_t row = blockIdx.x; // one wave per work-group (measured: 3-4 % over four)
-        const int lane = threadIdx.x & 63;
-        if (row >= a.nrows) return;
-        int64_t lo64, hi64;
-        row_range(a, row, lo64, hi64);
-        const int kc = int(a.kc);
-        const int lo = int(lo64 < 0 ? 0 : lo64), hi = int(hi64 >= kc ? kc - 1 : hi64); // visible: lo..hi
-        const float *xr = x + row * a.kc;
-        ro *yr = y + row * a.kc;
-        float v[CH][8];
+        if (!r.live) return false;
+        const int kc = int(a.kc), lo = int(r.lo64), hi = int(r.hi64);
         float m = kNegInf;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int cb = c * 512, j0 = cb + lane * 8;
-            if (cb > hi || cb + 511 < lo) continue; // nothing of this chunk visible
-            if (vec && cb >= lo && cb + 511 <= hi) {
-                load8_stream(xr + j0, v[c]);
-                if constexpr (CAP)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) v[c][e] = score<SF32, true>(a, v[c][e]);
+            if (cb > hi || cb + 511 < lo) continue;
+            if (cb >= lo && cb + 511 <= hi) {
+                if constexpr (CAP) cap8(a, r.v[c], 0xffu);
             } else {
-                if (vec && j0 + 8 <= kc && j0 <= hi && j0 + 7 >= lo)
-                    load8_stream(xr + j0, v[c]);
-                else
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) v[c][e] = (j0 + e >= lo && j0 + e <= hi) ? xr[j0 + e] : 0.0f;
                 // a row without visible keys (lo = 0, hi = -1, mask_range)
                 // skipped every chunk above, so here 0 <= hi - lo < kc
+                uint32_t vis = 0;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const bool vis = unsigned(j0 + e - lo) <= unsigned(hi - lo);
-                    if constexpr (CAP) v[c][e] = vis ? score<SF32, true>(a, v[c][e]) : kNegInf;
-                    else v[c][e] = vis ? v[c][e] : kNegInf;
+                for (int e = 0; e < 8; ++e) vis |= uint32_t(unsigned(j0 + e - lo) <= unsigned(hi - lo)) << e;
+                if constexpr (CAP) {
+                    cap8(a, r.v[c], vis);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) r.v[c][e] = (vis >> e) & 1u ? r.v[c][e] : kNegInf;
                 }
             }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) m = __builtin_fmaxf(m, v[c][e]);
+            for (int e = 0; e < 8; ++e) m = __builtin_fmaxf(m, r.v[c][e]);
         }
         m = dpp_max(m);
         float sum = 0.0f;
@@ -261,16 +345,14 @@ namespace mg
                 if (cb > hi || cb + 511 < lo) continue;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    v[c][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[c][e], c2, -mc)); // masked: exp2(-inf) = 0
-                    sum += v[c][e];
+                    r.v[c][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(r.v[c][e], c2, -mc)); // masked: exp2(-inf) = 0
+                    sum += r.v[c][e];
                 }
             }
         }
         sum = dpp_sum_f32(sum);
-        if (m != kNegInf && !(sum < __builtin_huge_valf())) { // NaN / infinite scores
-            softmax_row_accurate<SF32, SO, CH, CAP>(a, xr, yr, lo64, hi64, vec, lane);
-            return;
-        }
+        ro *yr = y + row * a.kc;
+        if (m != kNegInf && !(sum < __builtin_huge_valf())) return true; // NaN / infinite scores
         const float inv = m == kNegInf ? 0.0f : __builtin_amdgcn_rcpf(sum);
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
@@ -279,7 +361,7 @@ namespace mg
             const bool none = m == kNegInf || cb > hi || cb + 511 < lo;
             Vec<ro, 8> o;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o.v[e] = none ? ro(0) : SO::enc_finite(v[c][e] * inv);
+            for (int e = 0; e < 8; ++e) o.v[e] = none ? ro(0) : SO::enc_finite(r.v[c][e] * inv);
             if (vec && j0 + 8 <= kc) {
                 st16_stream<ro, 8>(yr + j0, o);
             } else {
@@ -288,6 +370,22 @@ namespace mg
                     if (j0 + e < kc) yr[j0 + e] = o.v[e];
             }
         }
+        return false;
+    }
+
+    // One row per one-wave work-group. All of the row's loads are issued
+    // before the first is used, and the compiler waits for each chunk's own.
+    template <class SO, int CH, bool CAP, bool VEC>
+    __global__ __launch_bounds__(64) void k_softmax_fast(const float *__restrict__ x,
+                                                          typename SO::raw *__restrict__ y, SmArgs a, float c2)
+    {
+        const int lane = threadIdx.x & 63;
+        const int64_t row = blockIdx.x;
+        FastRow<CH> r;
+        fast_load<CH, VEC>(a, x, row, lane, r);
+        // a row with non-finite sums is redone on the accurate path
+        if (fast_finish<SO, CH, CAP>(a, y, row, c2, VEC, lane, r))
+            softmax_row_accurate<SF32, SO, CH, CAP>(a, x + row * a.kc, y + row * a.kc, r.lo64, r.hi64, VEC, lane);
     }
 
     // ------------------------------------------------------------- split rows
@@ -500,16 +598,29 @@ namespace mg
         if (a.kc <= 2048) {
             const unsigned blocks = unsigned((a.nrows + 3) / 4);
             need(a.nrows < (int64_t(1) << 31), "softmax: too many rows");
-            if constexpr (SI::dt == F32 && sizeof(ro) == 2) if (CAP || a.scale > 0.0) {
+            // the fast capped score takes 1 <= |cap| <= 2^60 (mg_softcap_fast.hpp);
+            // other caps take the accurate kernel
+            const float acap = __builtin_fabsf(a.cap);
+            const bool cap_ok = !CAP || (acap >= 1.0f && acap <= 0x1p60f);
+            if constexpr (SI::dt == F32 && sizeof(ro) == 2) if (cap_ok && (CAP || a.scale > 0.0)) {
                 // log2-domain factor: the scale folds in unless the cap comes after it
                 const float c2 = float((CAP ? 1.0 : double(a.scale)) * 1.4426950408889634);
-                const unsigned rows1 = unsigned(a.nrows); // < 2^31: checked above
+                const unsigned wgs = unsigned(a.nrows); // < 2^31: checked above
+                // Without the cap the kernel needs few registers (8 waves per SIMD
+                // would fit) but streams fastest at 4: the LDS each work-group
+                // reserves (and never touches) holds a CU at 16 of them (measured:
+                // 124.8 us at 8 waves, 121.8 at 4-5, config 4). With the cap its
+                // registers allow 5, which the extra arithmetic uses.
+                const unsigned lds = CAP ? 0u : kLdsPerCu / (4u * kFastWavesNoCap);
+                auto go = [&](auto kern) {
+                    hipLaunchKernelGGL(kern, dim3(wgs), dim3(64), lds, c->stream, xi, yo, a, c2);
+                };
                 if (a.kc <= 512)
-                    hipLaunchKernelGGL((k_softmax_fast<SO, 1, CAP>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
+                    vec ? go(k_softmax_fast<SO, 1, CAP, true>) : go(k_softmax_fast<SO, 1, CAP, false>);
                 else if (a.kc <= 1024)
-                    hipLaunchKernelGGL((k_softmax_fast<SO, 2, CAP>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
+                    vec ? go(k_softmax_fast<SO, 2, CAP, true>) : go(k_softmax_fast<SO, 2, CAP, false>);
                 else
-                    hipLaunchKernelGGL((k_softmax_fast<SO, 4, CAP>), dim3(rows1), dim3(64), 0, c->stream, xi, yo, a, c2, vec);
+                    vec ? go(k_softmax_fast<SO, 4, CAP, true>) : go(k_softmax_fast<SO, 4, CAP, false>);
                 check_launch("k_softmax_fast");
                 return;
             }
@@ -568,6 +679,7 @@ namespace mg
         a.kc = kc;
         a.scale = float(scale);
         a.cap = float(softcap);
+        a.rcap = a.cap != 0.0f ? float(1.0 / double(a.cap)) : 0.0f;
         a.mask = mask;
         a.window = window;
         a.q_pos0 = q_pos0;

@@ -34,18 +34,22 @@ namespace mgm
 {
     constexpr double kTanhFastMargin = 0x1p-40;
 
+    // the branch of tanh_fast_abs for 0 <= a < 2^-5
+    MG_TF double tanh_series_abs(double a)
+    {
+        const double u = a * a;
+        // tanh x / x - 1 = u (-1/3 + u (2/15 + u (-17/315 + u (62/2835 + u (-1382/155925)))))
+        double p = -1382.0 / 155925.0;
+        p = __builtin_fma(p, u, 62.0 / 2835.0);
+        p = __builtin_fma(p, u, -17.0 / 315.0);
+        p = __builtin_fma(p, u, 2.0 / 15.0);
+        p = __builtin_fma(p, u, -1.0 / 3.0);
+        return __builtin_fma(a * u, p, a);
+    }
+
     MG_TF double tanh_fast_abs(double a)
     {
-        if (a < 0x1p-5) {
-            const double u = a * a;
-            // tanh x / x - 1 = u (-1/3 + u (2/15 + u (-17/315 + u (62/2835 + u (-1382/155925)))))
-            double p = -1382.0 / 155925.0;
-            p = __builtin_fma(p, u, 62.0 / 2835.0);
-            p = __builtin_fma(p, u, -17.0 / 315.0);
-            p = __builtin_fma(p, u, 2.0 / 15.0);
-            p = __builtin_fma(p, u, -1.0 / 3.0);
-            return __builtin_fma(a * u, p, a);
-        }
+        if (a < 0x1p-5) return tanh_series_abs(a);
         if (a >= 22.0) return 1.0;
         const double y = a + a;
         constexpr double kLog2e = 1.4426950408889634;     // 1 / ln 2
