@@ -70,7 +70,9 @@ int mg_open(int device, void *stream, int64_t workspace_bytes, mg_ctx **out);
 int mg_close(mg_ctx *ctx);
 /* Wait for all work queued on the context's stream. */
 int mg_sync(mg_ctx *ctx);
-/* Point the context at another stream (hipStream_t; NULL = the default stream). */
+/* Point the context at another stream (hipStream_t; NULL = the default stream).
+ * The new stream first waits (on the device, through an event) for the work
+ * already queued on the old one, since both use the context's workspace. */
 int mg_set_stream(mg_ctx *ctx, void *stream);
 void *mg_get_stream(mg_ctx *ctx);
 
@@ -98,9 +100,10 @@ int mg_norm_rows_mixed(mg_ctx *ctx, int kind, const void *x, int64_t ldx, int x_
  * then y[r,:] = norm(h[r,:]). Replaces the residual loop
  * (src/muse_glimmer.hpp:1023-1024, 1048-1049; src/bf16exec.hpp:608-610, 641-643;
  * GPU k_residual src/gpu/gpu_engine.cpp:1886-1893) followed by the next
- * rmsnorm_rows call on the updated stream (src/muse_glimmer.hpp:1028-1031). */
-int mg_residual_rmsnorm(mg_ctx *ctx, int kind, void *h, const void *x, const void *w, double eps,
-                        void *y, int64_t rows, int64_t dim, int dtype);
+ * rmsnorm_rows call on the updated stream (src/muse_glimmer.hpp:1028-1031).
+ * ldh/ldx/ldy: row strides in elements (0 = dim). */
+int mg_residual_rmsnorm(mg_ctx *ctx, int kind, void *h, int64_t ldh, const void *x, int64_t ldx, const void *w,
+                        double eps, void *y, int64_t ldy, int64_t rows, int64_t dim, int dtype);
 
 /* h = rnd(h + x), elementwise (src/muse_glimmer.hpp:1023-1024). */
 int mg_residual_add(mg_ctx *ctx, void *h, const void *x, int64_t n, int dtype);
@@ -157,7 +160,7 @@ int mg_qk_norm_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k,
                     int64_t pos0, const void *v, int64_t ldv, void *k_cache, void *v_cache,
                     int64_t cache_slots, int dtype);
 
-/* Scaled, masked row softmax over a contiguous [heads, q, k] score block — the
+/* Scaled, masked row softmax over a [heads, q, k] score block — the
  * softmax of attention_forward (src/muse_glimmer.hpp:828-885) as a row operator:
  * s = x*scale (f32 opmath), optional tanh softcap s = cap*tanh(s/cap) in
  * apply_output_tail's op order (src/muse_glimmer.hpp:920-943; cap 0 = off),
@@ -171,8 +174,10 @@ int mg_qk_norm_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k,
  * double(float(e) / sum)); no softcap.
  * Rows longer than one work-group's registers are split across work-groups
  * and merged in chunk order (the k_attn_decode_combine rule,
- * src/gpu/gpu_engine.cpp:1816-1857). */
-int mg_softmax_rows(mg_ctx *ctx, const void *x, void *y, int64_t heads, int64_t q_rows,
+ * src/gpu/gpu_engine.cpp:1816-1857). Row r of the block (r = head * q_rows +
+ * query) starts at x + r * ldx and y + r * ldy; ldx/ldy are row strides in
+ * elements (0 = k_cols, the contiguous block). */
+int mg_softmax_rows(mg_ctx *ctx, const void *x, int64_t ldx, void *y, int64_t ldy, int64_t heads, int64_t q_rows,
                     int64_t k_cols, double scale, int mask, int64_t window, int64_t q_pos0,
                     double softcap, int dtype_in, int dtype_out);
 

@@ -36,6 +36,7 @@ namespace mg
     struct SmArgs
     {
         int64_t nrows, q, kc;
+        int64_t ldx, ldy; // row strides of scores and probabilities, in elements
         float scale, cap;
         float rcap; // RN(1 / cap): the fast path's quotient (mg_softcap_fast.hpp)
         int mask;
@@ -226,7 +227,7 @@ namespace mg
         if (row >= a.nrows) return; // whole wave leaves; no block barrier below
         int64_t lo, hi;
         row_range(a, row, lo, hi);
-        softmax_row_accurate<SI, SO, CH, CAP>(a, x + row * a.kc, y + row * a.kc, lo, hi, vec, threadIdx.x & 63);
+        softmax_row_accurate<SI, SO, CH, CAP>(a, x + row * a.ldx, y + row * a.ldy, lo, hi, vec, threadIdx.x & 63);
     }
 
     // Lean row for f32 scores and 16-bit probabilities (the attention-score
@@ -272,7 +273,7 @@ namespace mg
         r.lo64 = r.live ? r.lo64 : 0;
         r.hi64 = r.live ? r.hi64 : -1;
         const int lo = int(r.lo64), hi = int(r.hi64); // 0 <= lo <= kc, -1 <= hi < kc <= 2048
-        const float *xr = x + row * a.kc;
+        const float *xr = x + row * a.ldx;
         if constexpr (VEC) {
             typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
             // word 3 of a gfx9 raw buffer descriptor (32-bit data, no swizzle)
@@ -351,7 +352,7 @@ namespace mg
             }
         }
         sum = dpp_sum_f32(sum);
-        ro *yr = y + row * a.kc;
+        ro *yr = y + row * a.ldy;
         if (m != kNegInf && !(sum < __builtin_huge_valf())) return true; // NaN / infinite scores
         const float inv = m == kNegInf ? 0.0f : __builtin_amdgcn_rcpf(sum);
 #pragma unroll
@@ -385,7 +386,7 @@ namespace mg
         fast_load<CH, VEC>(a, x, row, lane, r);
         // a row with non-finite sums is redone on the accurate path
         if (fast_finish<SO, CH, CAP>(a, y, row, c2, VEC, lane, r))
-            softmax_row_accurate<SF32, SO, CH, CAP>(a, x + row * a.kc, y + row * a.kc, r.lo64, r.hi64, VEC, lane);
+            softmax_row_accurate<SF32, SO, CH, CAP>(a, x + row * a.ldx, y + row * a.ldy, r.lo64, r.hi64, VEC, lane);
     }
 
     // ------------------------------------------------------------- split rows
@@ -420,7 +421,7 @@ namespace mg
         const int64_t row = blockIdx.y;
         int64_t lo, hi;
         row_range(a, row, lo, hi);
-        const typename SI::raw *xr = x + row * a.kc;
+        const typename SI::raw *xr = x + row * a.ldx;
         const int64_t base = int64_t(blockIdx.x) * kSplitChunk;
         float s[2][8];
         float m = kNegInf;
@@ -458,8 +459,8 @@ namespace mg
         // this chunk's scores first, so their latency overlaps the merge
         int64_t lo, hi;
         row_range(a, row, lo, hi);
-        const typename SI::raw *xr = x + row * a.kc;
-        typename SO::raw *yr = y + row * a.kc;
+        const typename SI::raw *xr = x + row * a.ldx;
+        typename SO::raw *yr = y + row * a.ldy;
         const int64_t base = int64_t(blockIdx.x) * kSplitChunk;
         float s[2][8];
 #pragma unroll
@@ -530,7 +531,7 @@ namespace mg
         const int64_t row = blockIdx.y;
         int64_t lo, hi;
         row_range(a, row, lo, hi);
-        const float *xr = x + row * a.kc;
+        const float *xr = x + row * a.ldx;
         const int64_t base = int64_t(blockIdx.x) * kSplitChunk;
         float t[2][8];
         float m = kNegInf;
@@ -563,8 +564,8 @@ namespace mg
         const float2 *pr = part + row * nch;
         int64_t lo, hi;
         row_range(a, row, lo, hi);
-        const float *xr = x + row * a.kc;
-        typename SO::raw *yr = y + row * a.kc;
+        const float *xr = x + row * a.ldx;
+        typename SO::raw *yr = y + row * a.ldy;
         const int64_t base = int64_t(blockIdx.x) * kSplitChunk;
         // this chunk's scores first, so their latency overlaps the merge
         float t[2][8];
@@ -592,7 +593,7 @@ namespace mg
     {
         using ri = typename SI::raw;
         using ro = typename SO::raw;
-        const bool vec = a.kc % 8 == 0 && aligned16(x) && aligned16(y);
+        const bool vec = a.kc % 8 == 0 && a.ldx % 8 == 0 && a.ldy % 8 == 0 && aligned16(x) && aligned16(y);
         const ri *xi = static_cast<const ri *>(x);
         ro *yo = static_cast<ro *>(y);
         if (a.kc <= 2048) {
@@ -664,11 +665,14 @@ namespace mg
         }
     }
 
-    void launch_softmax(mg_ctx *c, const void *x, void *y, int64_t heads, int64_t q, int64_t kc,
-                        double scale, int mask, int64_t window, int64_t q_pos0, double softcap,
+    void launch_softmax(mg_ctx *c, const void *x, int64_t ldx, void *y, int64_t ldy, int64_t heads, int64_t q,
+                        int64_t kc, double scale, int mask, int64_t window, int64_t q_pos0, double softcap,
                         int dt_in, int dt_out)
     {
         need(heads >= 0 && q >= 0 && kc >= 0, "softmax: bad shape");
+        ldx = ldx ? ldx : kc;
+        ldy = ldy ? ldy : kc;
+        need(ldx >= kc && ldy >= kc, "softmax: row strides smaller than the row length");
         need(x && y, "softmax: NULL tensor");
         need(mask >= 0 && mask <= 3, "softmax: unknown mask kind");
         need(mask < 2 || window > 0, "softmax: window masks need window > 0");
@@ -677,6 +681,8 @@ namespace mg
         a.nrows = heads * q;
         a.q = q;
         a.kc = kc;
+        a.ldx = ldx;
+        a.ldy = ldy;
         a.scale = float(scale);
         a.cap = float(softcap);
         a.rcap = a.cap != 0.0f ? float(1.0 / double(a.cap)) : 0.0f;
@@ -685,7 +691,8 @@ namespace mg
         a.q_pos0 = q_pos0;
         if (dt_in == F64 || dt_in == (F64 | kF32Compat)) {
             need(dt_out == F64, "softmax: f64 scores give f64 probabilities");
-            launch_softmax_f64(c, x, y, heads * q, q, kc, scale, mask, window, q_pos0, softcap, dt_in != F64);
+            launch_softmax_f64(c, x, ldx, y, ldy, heads * q, q, kc, scale, mask, window, q_pos0, softcap,
+                               dt_in != F64);
             return;
         }
         switch (dt_in) {

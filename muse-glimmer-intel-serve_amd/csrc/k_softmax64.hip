@@ -30,6 +30,7 @@ namespace mg
     struct Sm64Args
     {
         int64_t q, kc, window, q_pos0;
+        int64_t ldx, ldy; // row strides, in elements
         double scale, cap;
         int mask;
     };
@@ -57,8 +58,8 @@ namespace mg
         __shared__ float redf[4];
         __shared__ float sum32_sh;
         const int64_t row = blockIdx.x;
-        const double *xr = x + row * a.kc;
-        double *yr = y + row * a.kc;
+        const double *xr = x + row * a.ldx;
+        double *yr = y + row * a.ldy;
         int64_t lo, hi;
         mask_range(a.mask, a.q_pos0 + row % a.q, a.kc, a.window, lo, hi);
         const int tid = threadIdx.x;
@@ -120,12 +121,13 @@ namespace mg
         }
     }
 
-    void launch_softmax_f64(mg_ctx *c, const void *x, void *y, int64_t rows, int64_t q, int64_t kc, double scale,
-                            int mask, int64_t window, int64_t q_pos0, double softcap, bool compat)
+    void launch_softmax_f64(mg_ctx *c, const void *x, int64_t ldx, void *y, int64_t ldy, int64_t rows, int64_t q,
+                            int64_t kc, double scale, int mask, int64_t window, int64_t q_pos0, double softcap,
+                            bool compat)
     {
         need(rows < (int64_t(1) << 31), "softmax: too many rows");
         need(!compat || softcap == 0.0, "softmax: the f32-compat chain has no softcap");
-        const Sm64Args a{q, kc, window, q_pos0, scale, softcap, mask};
+        const Sm64Args a{q, kc, window, q_pos0, ldx, ldy, scale, softcap, mask};
         const double *xi = static_cast<const double *>(x);
         double *yo = static_cast<double *>(y);
         const dim3 grid{unsigned(rows)};

@@ -59,6 +59,7 @@ namespace
         note(hipStreamSynchronize(c->stream));
         if (c->lut) note(hipFree(c->lut));
         if (c->work) note(hipFree(c->work));
+        if (c->handoff) note(hipEventDestroy(c->handoff));
         delete c;
         return first;
     }
@@ -87,6 +88,7 @@ int mg_open(int device, void *stream, int64_t workspace_bytes, mg_ctx **out)
             c->work_bytes = workspace_bytes > 0 ? workspace_bytes : kDefaultWorkspace;
             mg::check(hipMalloc(&c->work, size_t(c->work_bytes)), "hipMalloc(workspace)");
             mg::check(hipMalloc(reinterpret_cast<void **>(&c->lut), 4 * 65536 * sizeof(uint16_t)), "hipMalloc(lut)");
+            mg::check(hipEventCreateWithFlags(&c->handoff, hipEventDisableTiming), "hipEventCreate");
             mg::build_luts(c);
             mg::check(hipStreamSynchronize(c->stream), "building lookup tables");
         } catch (...) {
@@ -114,10 +116,19 @@ int mg_sync(mg_ctx *ctx)
     });
 }
 
+// Work queued on the old stream may still use the context's workspace, which
+// the next call on the new stream reuses: the new stream waits for the old
+// one's queued work (an event, no host wait) before anything runs on it.
 int mg_set_stream(mg_ctx *ctx, void *stream)
 {
     MG_GUARD(-1, {
-        ctx_of(ctx)->stream = static_cast<hipStream_t>(stream);
+        mg_ctx *c = ctx_of(ctx);
+        const hipStream_t next = static_cast<hipStream_t>(stream);
+        if (next != c->stream) {
+            mg::check(hipEventRecord(c->handoff, c->stream), "mg_set_stream: hipEventRecord");
+            mg::check(hipStreamWaitEvent(next, c->handoff, 0), "mg_set_stream: hipStreamWaitEvent");
+            c->stream = next;
+        }
         return 0;
     });
 }
@@ -143,12 +154,13 @@ int mg_norm_rows_mixed(mg_ctx *ctx, int kind, const void *x, int64_t ldx, int x_
     });
 }
 
-int mg_residual_rmsnorm(mg_ctx *ctx, int kind, void *h, const void *x, const void *w, double eps,
-                        void *y, int64_t rows, int64_t dim, int dtype)
+int mg_residual_rmsnorm(mg_ctx *ctx, int kind, void *h, int64_t ldh, const void *x, int64_t ldx, const void *w,
+                        double eps, void *y, int64_t ldy, int64_t rows, int64_t dim, int dtype)
 {
     MG_GUARD(-1, {
         if (!x) mg::fail("residual_rmsnorm: NULL residual operand");
-        mg::launch_norm(ctx_of(ctx), kind, h, x, dim, dim, w, eps, y, dim, rows, dim, dtype);
+        mg::launch_norm(ctx_of(ctx), kind, h, x, ldh ? ldh : dim, ldx ? ldx : dim, w, eps, y, ldy ? ldy : dim, rows,
+                        dim, dtype);
         return 0;
     });
 }
@@ -221,12 +233,12 @@ int mg_qk_norm_rope(mg_ctx *ctx, void *q, int64_t q_heads, int64_t ldq, void *k,
     });
 }
 
-int mg_softmax_rows(mg_ctx *ctx, const void *x, void *y, int64_t heads, int64_t q_rows,
+int mg_softmax_rows(mg_ctx *ctx, const void *x, int64_t ldx, void *y, int64_t ldy, int64_t heads, int64_t q_rows,
                     int64_t k_cols, double scale, int mask, int64_t window, int64_t q_pos0,
                     double softcap, int dtype_in, int dtype_out)
 {
     MG_GUARD(-1, {
-        mg::launch_softmax(ctx_of(ctx), x, y, heads, q_rows, k_cols, scale, mask, window, q_pos0, softcap,
+        mg::launch_softmax(ctx_of(ctx), x, ldx, y, ldy, heads, q_rows, k_cols, scale, mask, window, q_pos0, softcap,
                            dtype_in, dtype_out);
         return 0;
     });

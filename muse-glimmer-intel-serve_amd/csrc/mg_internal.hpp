@@ -19,6 +19,7 @@ struct mg_ctx
     uint16_t *lut = nullptr;
     void *work = nullptr; // reduction partials (softmax split rows, vocab chunks)
     int64_t work_bytes = 0;
+    hipEvent_t handoff = nullptr; // orders a new stream after the old one (mg_set_stream)
 };
 
 namespace mg
@@ -70,12 +71,13 @@ namespace mg
                      int64_t ldk, int64_t tokens, int64_t dim, const void *co, const void *si,
                      int64_t table_rows, const int64_t *pos, int64_t pos0, int dt);
     // k_softmax.hip
-    void launch_softmax(mg_ctx *c, const void *x, void *y, int64_t heads, int64_t q,
-                        int64_t kc, double scale, int mask, int64_t window, int64_t q_pos0,
-                        double softcap, int dt_in, int dt_out);
+    void launch_softmax(mg_ctx *c, const void *x, int64_t ldx, void *y, int64_t ldy, int64_t heads, int64_t q,
+                        int64_t kc, double scale, int mask, int64_t window, int64_t q_pos0, double softcap,
+                        int dt_in, int dt_out);
     // k_softmax64.hip (f64 scores: the pure f64 and the f32-compat chains)
-    void launch_softmax_f64(mg_ctx *c, const void *x, void *y, int64_t rows, int64_t q, int64_t kc, double scale,
-                            int mask, int64_t window, int64_t q_pos0, double softcap, bool compat);
+    void launch_softmax_f64(mg_ctx *c, const void *x, int64_t ldx, void *y, int64_t ldy, int64_t rows, int64_t q,
+                            int64_t kc, double scale, int mask, int64_t window, int64_t q_pos0, double softcap,
+                            bool compat);
     // k_q8.hip
     void launch_dequant_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, void *out,
                              int64_t rows, int64_t in, int dt_out);

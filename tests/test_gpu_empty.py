@@ -27,8 +27,9 @@ def test_zero_sized_calls(prims, guard):
     p = ctypes.c_void_p(guard.data_ptr())
     calls = {
         "mg_rmsnorm_rows": lambda: L.mg_rmsnorm_rows(h, 1, p, 64, p, 1e-6, p, 64, 0, 64, BF16),
-        "mg_residual_rmsnorm": lambda: L.mg_residual_rmsnorm(h, 0, p, p, p, 1e-6, p, 0, 64, BF16),
-        "mg_residual_rmsnorm_f64_compat": lambda: L.mg_residual_rmsnorm(h, 0, p, p, p, 1e-6, p, 0, 64, 0x100),
+        "mg_residual_rmsnorm": lambda: L.mg_residual_rmsnorm(h, 0, p, 0, p, 0, p, 1e-6, p, 0, 0, 64, BF16),
+        "mg_residual_rmsnorm_f64_compat": lambda: L.mg_residual_rmsnorm(h, 0, p, 0, p, 0, p, 1e-6, p, 0, 0, 64,
+                                                                         0x100),
         "mg_residual_add": lambda: L.mg_residual_add(h, p, p, 0, BF16),
         "mg_swiglu": lambda: L.mg_swiglu(h, p, p, p, 0, BF16),
         "mg_sigmoid_gate": lambda: L.mg_sigmoid_gate(h, p, p, p, 0, F16),
@@ -37,9 +38,9 @@ def test_zero_sized_calls(prims, guard):
         "mg_rope": lambda: L.mg_rope(h, p, 4, 0, p, 1, 0, 0, 64, p, p, 8, None, 0, BF16),
         "mg_qk_norm_rope": lambda: L.mg_qk_norm_rope(h, p, 4, 0, p, 1, 0, 0, 64, 1e-6, 3.87, p, p, 8, None, 0,
                                                      p, 0, p, p, 8, BF16),
-        "mg_softmax_rows_heads": lambda: L.mg_softmax_rows(h, p, p, 0, 4, 64, 0.1, 1, 0, 0, 0.0, F32, BF16),
-        "mg_softmax_rows_q": lambda: L.mg_softmax_rows(h, p, p, 4, 0, 64, 0.1, 1, 0, 0, 0.0, F32, BF16),
-        "mg_softmax_rows_k": lambda: L.mg_softmax_rows(h, p, p, 4, 4, 0, 0.1, 0, 0, 0, 0.0, F64, F64),
+        "mg_softmax_rows_heads": lambda: L.mg_softmax_rows(h, p, 0, p, 0, 0, 4, 64, 0.1, 1, 0, 0, 0.0, F32, BF16),
+        "mg_softmax_rows_q": lambda: L.mg_softmax_rows(h, p, 0, p, 0, 4, 0, 64, 0.1, 1, 0, 0, 0.0, F32, BF16),
+        "mg_softmax_rows_k": lambda: L.mg_softmax_rows(h, p, 0, p, 0, 4, 4, 0, 0.1, 0, 0, 0, 0.0, F64, F64),
         "mg_dequant_q8_0": lambda: L.mg_dequant_q8_0(h, p, p, p, 0, 64, BF16),
         "mg_quantize_q8_0": lambda: L.mg_quantize_q8_0(h, p, 0, 64, p, p),
         "mg_gemv_q8_0": lambda: L.mg_gemv_q8_0(h, p, p, p, 1, 0, 64, 0, p, 0, 0),

@@ -156,6 +156,8 @@ def test_errors(prims):
     q = torch.zeros((2, 4, 128), dtype=torch.bfloat16, device="cuda:0")
     k = torch.zeros((2, 1, 128), dtype=torch.bfloat16, device="cuda:0")
     with pytest.raises(Exception, match="head_dim"):
+        prims.qk_norm_rope(q[:, :, :127].contiguous(), k[:, :, :127].contiguous(), EPS, QK)
+    with pytest.raises(Exception, match="heads contiguous"):  # refused by the binding
         prims.qk_norm_rope(q[:, :, :127], k[:, :, :127], EPS, QK)
     with pytest.raises(Exception, match="v_cache"):
         prims.qk_norm_rope(q, k, EPS, QK, v_cache=k)
