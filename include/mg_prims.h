@@ -240,7 +240,8 @@ int mg_quantize_q8_0(mg_ctx *ctx, const uint16_t *w, int64_t rows, int64_t in, i
 int mg_gemv_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, const uint16_t *x, int64_t batch, int64_t rows,
                  int64_t in, int64_t ldx, float *y, int64_t ldy, int blockdot);
 
-/* Per row of logits [rows, V] (dtype_in f32 or bf16), one fused pass:
+/* Per row of logits [rows, V] (dtype_in f32 or bf16; row r at logits + r * ld,
+ * ld the row stride in elements, 0 = V), one fused pass:
  *   lse[r]     = m + log(sum exp(x - m)) over finite entries, m their max
  *                (serve/sampler.py:168-171); -inf for a row with none
  *   argmax[r]  = first index of the maximum, the strict '>' scan from index 0
@@ -249,35 +250,36 @@ int mg_gemv_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, const uint16_
  *                (src/main.cpp:604-615 and serve/sampler.py:84-89, whose tie
  *                order is unspecified; this one is total), 0 < K <= 256.
  * Any output pointer may be NULL to skip it (all device pointers). */
-int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, int dtype_in,
+int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t V, int dtype_in,
                     int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val);
 
 /* mg_vocab_reduce without a context, allocating nothing: NO COUNTERPART in the
  * reference. For callers that cannot allocate device memory or hold a context
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Same kernels and results as mg_vocab_reduce (dtype_in f32 or
- * bf16, 0 < K <= 256, any output pointer may be NULL), launched on `stream`
- * (hipStream_t; NULL = the default stream) of the current HIP device. The
- * reduction partials live in a fixed 16 MiB device array (one per GPU, held
- * until the process ends; its address is looked up once per device, which
- * allocates nothing): a call needs rows * ceil(V / 2048) * 1128 bytes of it
- * (K <= 64; 2152 for larger K), e.g. 64 rows x V = 201088 take 7.1 MB, and a
- * call needing more fails with an error before launching anything. Every call
- * on one GPU shares that array: calls that overlap on one GPU (concurrent
- * streams) race; serialize them. */
-int mg_vocab_reduce_noalloc(void *stream, const void *logits, int64_t rows, int64_t V, int dtype_in, int64_t K,
-                            double *lse, int64_t *argmax, int64_t *top_idx, float *top_val);
+ * bf16, 0 < K <= 256, ld the row stride (0 = V), any output pointer may be
+ * NULL), launched on `stream` (hipStream_t; NULL = the default stream) of the
+ * current HIP device. The reduction partials live in a fixed 16 MiB device
+ * array (one per GPU, held until the process ends; its address is looked up
+ * once per device, which allocates nothing): a call needs
+ * rows * ceil(V / 4096) * 2216 bytes of it, e.g. 64 rows x V = 201088 take
+ * 7.1 MB, and a call needing more fails with an error before launching
+ * anything. Every call on one GPU shares that array: calls that overlap on
+ * one GPU (concurrent streams) race; serialize them. */
+int mg_vocab_reduce_noalloc(void *stream, const void *logits, int64_t ld, int64_t rows, int64_t V, int dtype_in,
+                            int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val);
 
 /* The output tail fused into the vocab pass: every logit first becomes
  * apply_output_tail's value (z = rnd(z*mult); z = rnd(cap*rnd(tanh(rnd(z/cap)))),
  * rounded to dtype_in at each step, FDLIBM tanh; src/muse_glimmer.hpp:920-943,
  * GPU k_softcap src/gpu/gpu_engine.cpp:1906-1919), then lse / argmax / top-K are
  * taken over the transformed logits exactly as mg_vocab_reduce does; top_val
- * holds transformed values. logits_out (optional, [rows, V] at dtype_in)
- * receives the transformed logits; the input is not modified. */
-int mg_vocab_reduce_tail(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, int dtype_in, double mult,
-                         double cap, int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val,
-                         void *logits_out);
+ * holds transformed values. logits_out (optional, contiguous [rows, V] at
+ * dtype_in) receives the transformed logits; the input (row stride ld,
+ * 0 = V) is not modified. */
+int mg_vocab_reduce_tail(mg_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t V, int dtype_in,
+                         double mult, double cap, int64_t K, double *lse, int64_t *argmax, int64_t *top_idx,
+                         float *top_val, void *logits_out);
 
 /* The sampler's final candidate distribution from a vocab pass's output
  * (serve/sampler.py:43-112, Sampler._transformed / dist after the logit edits):

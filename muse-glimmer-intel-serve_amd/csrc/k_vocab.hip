@@ -13,27 +13,28 @@
 //           NaN entries rank below -inf.
 //
 // Every (value, index) packs into one 64-bit key: an order-preserving image of
-// the f32 value (NaN -> 0, -0 -> +0) above the complement of the index. Keys
+// the f32 value (NaN -> 1, -0 -> +0) above the complement of the index. Keys
 // are unique and "the K largest keys" is exactly the order above, so every
 // selection below is deterministic however the work is split.
 //
-// Pass 1 (k_vocab_chunk): one wave per 2048-key chunk, 32 keys per lane held
-// in registers, no block barriers and no shuffles in the per-element work:
-// counts are ballot popcounts, reductions are DPP. Per chunk: the finite max,
-// the sum of exp(x - max) (f32 terms and lane sums, f64 across lanes), the
-// first index of the max, a candidate list that contains the chunk's top-K,
-// and the chunk's top-8 keys (the "block"). For K <= 64 the list is every
-// element at or above a bound that cannot miss: each lane keeps its two
-// largest values, and the K-th largest of those 128 values has at least K
-// elements at or above it (about K + K/8 pass for random logits). When that
-// bound is -inf or lets more than 128 through, and for every chunk when
-// K > 64, the list is the exact top-K, selected by bit-by-bit bisection on the
-// keys.
+// Pass 1 (k_vocab_chunk): one wave per 4096-key chunk, 64 keys per lane held
+// in registers (a row of 201088 keys is 50 chunks; 64 rows fill the chip's
+// wave slots once). Per chunk: the finite max, the sum of exp(x - max) (f32
+// terms, f64 across lanes), and the chunk's top D = min(16, K) keys in order
+// (the "block"), whose first is the chunk's argmax. The block costs little:
+// t, the D-th largest of the 64 lane maxima, has at least D keys at or above
+// it, so the keys >= t (about D + 1 for random logits) hold the block; they
+// are compacted through ballots and ranked by a count over the others. Chunks
+// where that set is empty of meaning (more than 64 keys >= t, or NaN needed
+// to fill the block) select their block exactly by radix selection.
 // Pass 2 (k_vocab_merge): one wave per row. lse and argmax fold the chunk
-// partials (f64, FDLIBM exp/log). The row's K-th key is first selected from
-// the blocks alone; that is exact when every chunk whose list runs past its
-// block has its 8th key at or below the selected one (everything deeper is
-// smaller still). Otherwise the selection runs over the full lists.
+// partials (f64, FDLIBM exp/log). The row's K-th key kap is selected from the
+// blocks; it is the answer when no chunk's D-th key lies above kap (every key
+// outside a block is below that chunk's D-th key). Otherwise the chunks that
+// fail the check are re-read and their exact top-K computed, and the
+// selection runs again over those lists and the other chunks' blocks: exact
+// for any input, slower only where one chunk holds more than D of the row's
+// top K.
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
 
@@ -42,23 +43,23 @@
 
 namespace mg
 {
-    constexpr int kVLane = 32;           // keys per lane in pass 1
-    constexpr int kVChunk = 64 * kVLane; // 2048 keys per wave-chunk
+    constexpr int kVLane = 64;           // keys per lane in pass 1
+    constexpr int kVChunk = 64 * kVLane; // 4096 keys per wave-chunk
     constexpr int kMaxK = 256;
-    constexpr int kFastK = 64;           // pass 1 bound-based selection up to this K
-    constexpr int kBlk = 8;              // keys per chunk block
-    constexpr int kMergeRegs = 16;       // pass 2: block keys per lane (1024 per row)
+    constexpr int kBlk = 16;             // keys per chunk block
+    constexpr int kCand = 64;            // candidates a chunk ranks (one per lane)
+    constexpr int kMergeRegs = 16;       // pass 2: block keys per lane (the blocks of 64 chunks)
+    constexpr int kUnionCap = 4096;      // pass 2 fallback: keys staged in LDS
 
     struct VPart
     {
         double l;      // sum over the chunk's finite x of exp(x - m)
-        uint64_t kd;   // the block's smallest key if keys outside the block can
-                       // reach the row's top-K, else 0
+        uint64_t kd;   // the block's last key when the chunk holds more keys than
+                       // its block (every other key is below it), else 0
         uint64_t top;  // the chunk's largest key: its argmax (first maximum, NaN lowest)
         float m;       // max of the chunk's finite x
         int32_t fin;   // 1 if the chunk holds a finite entry
-        int32_t nlist; // keys in the chunk's candidate list
-        int32_t pad;
+        int32_t pad0, pad1;
     };
 
     // apply_output_tail (src/muse_glimmer.hpp:920-943) on one stored logit:
@@ -244,30 +245,17 @@ namespace mg
         return (uint64_t(th) << 32) | lw;
     }
 
-    template <class SI, int VW, int SL, bool TAIL>
-    __global__ __launch_bounds__(256) void k_vocab_chunk(const typename SI::raw *__restrict__ L, int64_t V, int K,
-                                                         int nch, VPart *__restrict__ part,
-                                                         uint64_t *__restrict__ blk, uint64_t *__restrict__ lst,
-                                                         VTail tail)
+    // ------------------------------------------------------------------ pass 1
+
+    // A chunk's logits as f32 bit patterns (past V: -inf, which no sum, max or
+    // candidate takes), tail-transformed and optionally written back
+    template <class SI, int VW, bool TAIL>
+    MG_DEV void chunk_load(const typename SI::raw *__restrict__ xr, int nvalid, const VTail &tail,
+                           typename SI::raw *orow, uint32_t (&xb)[kVLane])
     {
         using raw = typename SI::raw;
-        constexpr int CAP = 64 * SL; // list capacity
-        __shared__ uint32_t sbits[4][CAP];
-        __shared__ uint32_t soff[4][CAP];
-        __shared__ __align__(16) uint32_t shist[4][256];
-        const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-        const int ch = int(blockIdx.x) * 4 + wv;
-        const int64_t row = blockIdx.y;
-        if (ch >= nch) return; // the whole wave leaves; nothing below syncs the block
-        const int64_t cb = int64_t(ch) * kVChunk;
-        const int nvalid = int(V - cb < kVChunk ? V - cb : kVChunk);
+        const int lane = threadIdx.x & 63;
         const bool full = nvalid == kVChunk;
-        const raw *xr = L + row * V + cb;
-
-        // the chunk as f32 bit patterns; the exact selection overwrites them
-        // with the keys' high words
-        uint32_t xb[kVLane];
-        auto x = [&](int s) { return __builtin_bit_cast(float, xb[s]); };
         bool loaded = false;
         if constexpr (VW > 1) {
             if (full) {
@@ -281,22 +269,18 @@ namespace mg
             }
         }
         if (!loaded) {
-            // tail chunk (or unaligned rows): -inf placeholders past V never
-            // reach a sum, a max or the candidates, and are kept out of the
-            // argmax and the exact selection by offset
 #pragma unroll
             for (int s = 0; s < kVLane; ++s) {
                 const int o = voff<VW>(lane, s);
                 xb[s] = __builtin_bit_cast(uint32_t, o < nvalid ? float(SI::dec(xr[o])) : -__builtin_huge_valf());
             }
         }
-
         if constexpr (TAIL) {
 #pragma unroll
             for (int s = 0; s < kVLane; ++s)
-                if (full || voff<VW>(lane, s) < nvalid) xb[s] = __builtin_bit_cast(uint32_t, vtail<SI>(x(s), tail));
-            if (tail.out) {
-                raw *orow = static_cast<raw *>(tail.out) + row * V + cb;
+                if (full || voff<VW>(lane, s) < nvalid)
+                    xb[s] = __builtin_bit_cast(uint32_t, vtail<SI>(__builtin_bit_cast(float, xb[s]), tail));
+            if (orow) {
                 bool stored = false;
                 if constexpr (VW > 1) {
                     if (full) {
@@ -304,7 +288,7 @@ namespace mg
                         for (int i = 0; i < kVLane / VW; ++i) {
                             Vec<raw, VW> w;
 #pragma unroll
-                            for (int e = 0; e < VW; ++e) w.v[e] = SI::enc32(x(VW * i + e));
+                            for (int e = 0; e < VW; ++e) w.v[e] = SI::enc32(__builtin_bit_cast(float, xb[VW * i + e]));
                             st16_stream<raw, VW>(orow + VW * lane + 64 * VW * i, w);
                         }
                         stored = true;
@@ -314,20 +298,77 @@ namespace mg
 #pragma unroll
                     for (int s = 0; s < kVLane; ++s) {
                         const int o = voff<VW>(lane, s);
-                        if (o < nvalid) orow[o] = SI::enc32(x(s));
+                        if (o < nvalid) orow[o] = SI::enc32(__builtin_bit_cast(float, xb[s]));
                     }
                 }
             }
         }
+    }
 
-        // lane maximum and second maximum (two distinct elements)
-        float m1 = -__builtin_huge_valf(), m2 = -__builtin_huge_valf();
+    // Exact top-nk keys of a loaded chunk (nk <= 16), largest first, into
+    // sb (high words) and so (offsets): xb becomes the keys' high words (0
+    // past nvalid), and each of nk rounds takes the largest remaining key —
+    // the largest high word, at its lowest offset — and clears it. Register
+    // only; the chunk kernel's rare path (ties at t, NaN in a block).
+    template <int VW>
+    MG_DEV void chunk_exact_top(uint32_t (&xb)[kVLane], int nvalid, int nk, uint32_t *sb, uint32_t *so)
+    {
+        const int lane = threadIdx.x & 63;
+        const bool full = nvalid == kVChunk;
 #pragma unroll
-        for (int s = 0; s < kVLane; ++s) {
-            m2 = __builtin_fmaxf(m2, __builtin_fminf(m1, x(s)));
-            m1 = __builtin_fmaxf(m1, x(s));
+        for (int s = 0; s < kVLane; ++s)
+            xb[s] = (full || voff<VW>(lane, s) < nvalid) ? vhi(__builtin_bit_cast(float, xb[s])) : 0u;
+        for (int i = 0; i < nk; ++i) {
+            uint32_t hm = 0;
+#pragma unroll
+            for (int s = 0; s < kVLane; ++s) hm = xb[s] > hm ? xb[s] : hm;
+            hm = dpp_max_u32(hm);
+            // within a lane offsets grow with s: the lane's first slot holding hm
+            int first = kVLane;
+#pragma unroll
+            for (int s = kVLane - 1; s >= 0; --s) first = xb[s] == hm ? s : first;
+            const uint32_t of = first < kVLane ? uint32_t(VW * lane + 64 * VW * (first / VW) + first % VW) : 0xffffffffu;
+            const uint32_t om = dpp_min_u32(of);
+            const int clear = of == om ? first : kVLane; // in the one lane holding it
+#pragma unroll
+            for (int s = 0; s < kVLane; ++s) xb[s] = s == clear ? 0u : xb[s];
+            if (lane == 0) {
+                sb[i] = hm;
+                so[i] = om;
+            }
         }
-        const float MX = dpp_max(m1); // max over the non-NaN entries
+    }
+
+    MG_DEV uint64_t readlane64(uint64_t v, int l)
+    {
+        const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v)), l));
+        const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v >> 32)), l));
+        return (uint64_t(hi) << 32) | lo;
+    }
+
+    template <class SI, int VW, bool TAIL>
+    __global__ __launch_bounds__(64) void k_vocab_chunk(const typename SI::raw *__restrict__ L, int64_t ld,
+                                                        int64_t V, int K, int nch, VPart *__restrict__ part,
+                                                        uint64_t *__restrict__ blk, VTail tail)
+    {
+        using raw = typename SI::raw;
+        __shared__ uint32_t sb[kCand], so[kCand];
+        __shared__ uint64_t sel[kCand];
+        const int lane = threadIdx.x & 63;
+        const int ch = int(blockIdx.x);
+        const int64_t row = blockIdx.y;
+        const int64_t cb = int64_t(ch) * kVChunk;
+        const int nvalid = int(V - cb < kVChunk ? V - cb : kVChunk);
+        uint32_t xb[kVLane];
+        auto x = [&](int s) { return __builtin_bit_cast(float, xb[s]); };
+        chunk_load<SI, VW, TAIL>(L + row * ld + cb, nvalid, tail,
+                                 tail.out ? static_cast<raw *>(tail.out) + row * V + cb : nullptr, xb);
+
+        // lane maximum over the non-NaN entries (fmax passes NaN's partner on)
+        float m1 = -__builtin_huge_valf();
+#pragma unroll
+        for (int s = 0; s < kVLane; ++s) m1 = __builtin_fmaxf(m1, x(s));
+        const float MX = dpp_max(m1);
 
         // lse partial, first assuming every entry finite or -inf
         constexpr float c = 1.44269504088896341f;
@@ -347,9 +388,8 @@ namespace mg
             special = S != S; // a NaN logit
         }
         if (special) {
-            // NaN or +inf present, or no finite entry: the finite max, the sum
-            // over finite entries, and m1/m2 with NaN taken as -inf (fminf
-            // would otherwise pass NaN's partner through as a second element)
+            // NaN or +inf present, or no finite entry: the finite max and the
+            // sum over the finite entries
             float fm = -__builtin_huge_valf();
 #pragma unroll
             for (int s = 0; s < kVLane; ++s)
@@ -361,217 +401,167 @@ namespace mg
                 for (int s = 0; s < kVLane; ++s)
                     acc += __builtin_isfinite(x(s)) ? __builtin_amdgcn_exp2f((x(s) - FM) * c) : 0.0f;
             l = dpp_sum(double(acc));
-            m1 = m2 = -__builtin_huge_valf();
-#pragma unroll
-            for (int s = 0; s < kVLane; ++s) {
-                const float v = x(s) == x(s) ? x(s) : -__builtin_huge_valf();
-                m2 = __builtin_fmaxf(m2, __builtin_fminf(m1, v));
-                m1 = __builtin_fmaxf(m1, v);
-            }
         }
         const bool fin = FM > -__builtin_huge_valf();
 
-        // ---- candidates
-        const int nk = nvalid < K ? nvalid : K;
-        bool exact = SL > 2;
-        float tau = -__builtin_huge_valf();
-        if (!exact) {
-            // tau: the K-th largest of the 128 lane top-2 values
-            const uint32_t k2[2] = {f32_key(m1 + 0.0f), f32_key(m2 + 0.0f)}; // >= key(-inf) > 0
-            int unused = 0;
-            tau = key_f32(wave_select<2>(k2, K, shist[wv], unused));
-            exact = !(tau > -__builtin_huge_valf());
-        }
-        // exact: candidates are hk > th, or hk == th at offsets <= to
-        uint32_t th = 0;
-        int to = kVChunk;
-        auto select_exact = [&]() {
-            // the keys' high words replace the values (0 past V)
-#pragma unroll
-            for (int s = 0; s < kVLane; ++s) xb[s] = (full || voff<VW>(lane, s) < nvalid) ? vhi(x(s)) : 0u;
-            int need = 0; // entries with hk == th to take, lowest offsets first
-            th = wave_select<kVLane>(xb, nk, shist[wv], need);
-            int lo = -1, hi = kVChunk - 1;
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) / 2;
-                int cnt = 0;
-#pragma unroll
-                for (int s = 0; s < kVLane; ++s) cnt += wave_count(xb[s] == th && voff<VW>(lane, s) <= mid);
-                if (cnt >= need)
-                    hi = mid;
-                else
-                    lo = mid;
+        // ---- the block: the chunk's top D keys
+        const int D = K < kBlk ? K : kBlk;
+        // t: the D-th largest lane maximum, equal values counted; at least D
+        // keys are >= t (-inf when fewer than D lanes hold a finite maximum)
+        float t = -__builtin_huge_valf();
+        {
+            float v = m1;
+            int left = D;
+            for (int i = 0; i < D; ++i) {
+                const float mx = dpp_max(v);
+                const int cnt = wave_count(v == mx);
+                if (cnt >= left || !(mx > -__builtin_huge_valf())) {
+                    t = mx;
+                    break;
+                }
+                left -= cnt;
+                v = v == mx ? -__builtin_huge_valf() : v;
             }
-            to = hi;
-        };
-        if (exact) select_exact();
-
-        // compact (bits, offset) of the candidates into this wave's LDS slots;
-        // more than CAP of them (possible only through ties at tau) sends
-        // the chunk to the exact selection
-        uint32_t *sb = sbits[wv], *so = soff[wv];
+        }
+        // candidates: the keys >= t (never NaN; the -inf placeholders past V
+        // only when t is -inf, which takes the exact path), compacted into LDS
         int n = 0;
-        for (int pass = 0; pass < 2; ++pass) {
-            n = 0;
+        if (t > -__builtin_huge_valf()) {
 #pragma unroll
             for (int s = 0; s < kVLane; ++s) {
-                const int o = voff<VW>(lane, s);
-                const uint32_t bits = xb[s];
-                const bool take = exact ? (bits > th || (bits == th && o <= to)) : x(s) >= tau;
+                const bool take = x(s) >= t;
                 const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
                 if (mk) {
                     const int p = n + lane_rank(mk);
-                    if (take && p < CAP) {
-                        sb[p] = bits;
-                        so[p] = uint32_t(o);
+                    if (take && p < kCand) {
+                        sb[p] = xb[s];
+                        so[p] = uint32_t(voff<VW>(lane, s));
                     }
                     n += __builtin_popcountll(mk);
                 }
             }
-            if (n <= CAP) break;
-            // exact selection (the keys replace the values), then compact again
-            exact = true;
-            select_exact();
+        }
+        // t = -inf (fewer than D lanes with a finite maximum), too many keys
+        // (ties at t): the exact top D instead (sb then holds high words)
+        const bool exact = !(t > -__builtin_huge_valf()) || n > kCand;
+        if (exact) {
+            n = nvalid < D ? nvalid : D;
+            wave_lds_sync();
+            chunk_exact_top<VW>(xb, nvalid, n, sb, so);
         }
         wave_lds_sync();
-        uint64_t a[SL];
-#pragma unroll
-        for (int q = 0; q < SL; ++q) {
-            const int i = SL * lane + q;
-            a[q] = 0;
-            if (i < n) {
-                const uint32_t bits = sb[i];
-                a[q] = vkey(exact ? bits : vhi(__builtin_bit_cast(float, bits)), uint32_t(cb + so[i]));
-            }
-        }
+        // rank the n <= 64 candidates (keys are unique, so ranks are distinct)
+        const uint64_t key = lane < n ? vkey(exact ? sb[lane] : vhi(__builtin_bit_cast(float, sb[lane])),
+                                             uint32_t(cb + so[lane]))
+                                      : 0;
+        int rank = 0;
+        for (int j = 0; j < n; ++j) rank += readlane64(key, j) > key ? 1 : 0;
+        if (lane < n) sel[rank] = key;
+        wave_lds_sync();
+        const int nb = n < D ? n : D; // keys in the block
         const int64_t cid = row * nch + ch;
-        uint64_t *lr = lst + cid * CAP;
-#pragma unroll
-        for (int q = 0; q < SL; ++q)
-            if (SL * lane + q < n) lr[SL * lane + q] = a[q];
-
-        // the block: the list's (= the chunk's) top D keys, D = min(8, K),
-        // taken largest first. Keys are unique, so the wave maximum of the high
-        // words, then of the low words among the slots holding that high word,
-        // is the largest remaining key; it is cleared and lane i keeps the i-th.
-        // Slots past the list's end hold 0 and make the block's tail 0.
-        const int D = K < kBlk ? K : kBlk;
-        uint64_t *br = blk + cid * kBlk;
-        uint64_t kd = 0; // the D-th key when the list is longer than the block
-        uint64_t top = 0; // the first key taken, the list's (= the chunk's) largest: its argmax
-        {
-            uint64_t r[SL];
-#pragma unroll
-            for (int q = 0; q < SL; ++q) r[q] = a[q];
-            uint64_t mine = 0;
-            for (int i = 0; i < D; ++i) {
-                uint32_t hm = 0;
-#pragma unroll
-                for (int q = 0; q < SL; ++q) hm = uint32_t(r[q] >> 32) > hm ? uint32_t(r[q] >> 32) : hm;
-                hm = dpp_max_u32(hm);
-                uint32_t lm = 0;
-#pragma unroll
-                for (int q = 0; q < SL; ++q)
-                    lm = (uint32_t(r[q] >> 32) == hm && uint32_t(r[q]) > lm) ? uint32_t(r[q]) : lm;
-                lm = dpp_max_u32(lm);
-                const uint64_t mk = (uint64_t(hm) << 32) | lm;
-#pragma unroll
-                for (int q = 0; q < SL; ++q) r[q] = r[q] == mk ? 0 : r[q];
-                mine = lane == i ? mk : mine;
-                top = i == 0 ? mk : top;
-                kd = mk;
-            }
-            if (lane < kBlk) br[lane] = mine;
-        }
-        if (n <= D) kd = 0;
+        if (lane < kBlk) blk[cid * kBlk + lane] = lane < nb ? sel[lane] : 0;
         if (lane == 0) {
             VPart p;
             p.l = l;
-            p.kd = (D < K && n > D) ? kd : 0;
+            p.kd = nvalid > nb ? sel[nb - 1] : 0;
+            p.top = sel[0];
             p.m = fin ? FM : 0.0f;
-            p.top = top;
             p.fin = fin ? 1 : 0;
-            p.nlist = n;
-            p.pad = 0;
+            p.pad0 = p.pad1 = 0;
             part[cid] = p;
         }
     }
 
     // ------------------------------------------------------------------ pass 2
-    // K-th largest key over every chunk's candidate list, read from memory
-    MG_DEV uint64_t lists_kth(const VPart *pr, const uint64_t *ls, int nch, int cap, int K)
+    // The K-th largest key over a key source, by 8-bit radix selection with an
+    // LDS histogram: each pass counts the keys that match the digits fixed so
+    // far, per value of the next digit. `each(f)` calls f(key) for every key
+    // of the source held by this lane (0 = no key); at least K keys exist.
+    template <class EACH>
+    MG_DEV uint64_t source_kth(EACH each, int K, uint32_t *hist)
     {
         const int lane = threadIdx.x & 63;
-        auto count = [&](auto pred) {
-            int c = 0;
-            for (int ch = 0; ch < nch; ++ch) {
-                const int nl = pr[ch].nlist < cap ? pr[ch].nlist : cap;
-                for (int p0 = 0; p0 < nl; p0 += 64) {
-                    const int p = p0 + lane;
-                    const uint64_t k = p < nl ? ls[int64_t(ch) * cap + p] : 0;
-                    c += wave_count(k != 0 && pred(k));
+        uint64_t prefix = 0;
+        int need = K;
+        for (int sh = 56; sh >= 0; sh -= 8) {
+            const uint64_t fixed = sh == 56 ? 0 : ~((uint64_t(1) << (sh + 8)) - 1);
+            wave_lds_sync();
+            *reinterpret_cast<Vec<uint32_t, 4> *>(hist + 4 * lane) = Vec<uint32_t, 4>{{0u, 0u, 0u, 0u}};
+            wave_lds_sync();
+            each([&](uint64_t k) {
+                if (k && (k & fixed) == prefix) atomicAdd(hist + int((k >> sh) & 0xff), 1u);
+            });
+            wave_lds_sync();
+            const Vec<uint32_t, 4> cv = *reinterpret_cast<const Vec<uint32_t, 4> *>(hist + 4 * lane);
+            const int sl = int(cv.v[0] + cv.v[1] + cv.v[2] + cv.v[3]);
+            const int incl = wave_prefix_sum(sl);
+            const int above_lane = __builtin_amdgcn_readlane(incl, 63) - incl; // in higher bins
+            const bool mine = above_lane < need && need <= above_lane + sl;
+            int dg = 0, above = 0;
+            if (mine) {
+                int acc = above_lane;
+                for (int e = 3; e >= 0; --e) {
+                    if (acc + int(cv.v[e]) >= need) {
+                        dg = 4 * lane + e;
+                        above = acc;
+                        break;
+                    }
+                    acc += int(cv.v[e]);
                 }
             }
-            return c;
-        };
-        uint32_t th = 0;
-        for (int b = 31; b >= 0; --b) {
-            const uint32_t t = th | (1u << b);
-            if (count([&](uint64_t k) { return uint32_t(k >> 32) >= t; }) >= K) th = t;
+            const int src = int(__builtin_ctzll(__builtin_amdgcn_ballot_w64(mine)));
+            dg = __builtin_amdgcn_readlane(dg, src);
+            above = __builtin_amdgcn_readlane(above, src);
+            prefix |= uint64_t(dg) << sh;
+            need -= above;
         }
-        const int need = K - count([&](uint64_t k) { return uint32_t(k >> 32) > th; });
-        uint32_t lw = 0;
-        for (int b = 31; b >= 0; --b) {
-            const uint32_t t = lw | (1u << b);
-            if (count([&](uint64_t k) { return uint32_t(k >> 32) == th && uint32_t(k) >= t; }) >= need) lw = t;
-        }
-        return (uint64_t(th) << 32) | lw;
+        return prefix;
     }
 
-    template <class SI, int SL, bool TAIL>
-    __global__ __launch_bounds__(64) void k_vocab_merge(const typename SI::raw *__restrict__ L, int64_t V, int K,
-                                                        int nch, int cap, const VPart *__restrict__ part,
-                                                        const uint64_t *__restrict__ blk,
-                                                        const uint64_t *__restrict__ lst, double *lse,
-                                                        int64_t *amax, int64_t *top_idx, float *top_val, VTail tail)
+    template <class SI, int VW, int SL, bool TAIL>
+    __global__ __launch_bounds__(64) void k_vocab_merge(const typename SI::raw *__restrict__ L, int64_t ld,
+                                                        int64_t V, int K, int nch, const VPart *__restrict__ part,
+                                                        const uint64_t *__restrict__ blk, uint64_t *__restrict__ lst,
+                                                        double *lse, int64_t *amax, int64_t *top_idx, float *top_val,
+                                                        VTail tail)
     {
-        __shared__ uint64_t sel[64 * SL];
+        __shared__ uint64_t sel[kMaxK];
+        __shared__ uint64_t ukeys[kUnionCap];
         __shared__ __align__(16) uint32_t hist[256];
         const int lane = threadIdx.x;
         const int64_t row = blockIdx.x;
         const VPart *pr = part + row * nch;
-        const uint64_t *bk = blk + row * nch * int64_t(kBlk);
-        const uint64_t *ls = lst + row * nch * int64_t(cap);
-        float x0 = float(SI::dec(L[row * V]));
+        const uint64_t *bk = blk + row * int64_t(nch) * kBlk;
+        uint64_t *ls = lst + row * int64_t(nch) * kMaxK;
+        float x0 = float(SI::dec(L[row * ld]));
         if constexpr (TAIL) x0 = vtail<SI>(x0, tail);
         const bool want_top = top_idx || top_val;
         const int D = K < kBlk ? K : kBlk;
-        const bool regs = want_top && nch * D <= 64 * kMergeRegs;
+        const bool regs = want_top && nch * kBlk <= 64 * kMergeRegs;
 
         // the lane's chunk partials (up to two: rows of up to 128 chunks) and
-        // the blocks' keys, all requested before any is used, so one round
-        // trip serves the fold, the blocks and the block check
+        // the blocks' keys, all requested before any is used
         constexpr int PPL = 2;
         const bool pregs = nch <= 64 * PPL;
         VPart pv[PPL];
 #pragma unroll
         for (int k = 0; k < PPL; ++k) {
-            const int c = lane + 64 * k;
-            if (pregs && c < nch) {
-                pv[k] = pr[c];
+            const int cc = lane + 64 * k;
+            if (pregs && cc < nch) {
+                pv[k] = pr[cc];
             } else {
                 pv[k].l = 0.0;
                 pv[k].kd = pv[k].top = 0;
                 pv[k].m = -__builtin_huge_valf();
-                pv[k].fin = pv[k].nlist = pv[k].pad = 0;
+                pv[k].fin = pv[k].pad0 = pv[k].pad1 = 0;
             }
         }
         uint64_t r[kMergeRegs];
 #pragma unroll
         for (int q = 0; q < kMergeRegs; ++q) {
             const int i = lane + 64 * q;
-            const int c = D == kBlk ? i / kBlk : i / D, p = D == kBlk ? i % kBlk : i - c * D;
-            r[q] = regs && c < nch ? bk[int64_t(c) * kBlk + p] : 0;
+            r[q] = regs && i / kBlk < nch ? bk[i] : 0;
         }
 
         // lse and argmax: fold the chunk partials; the largest chunk key is
@@ -590,7 +580,7 @@ namespace mg
 #pragma unroll
             for (int k = 0; k < PPL; ++k) fold_max(pv[k]); // absent ones: fin 0, top 0
         } else {
-            for (int c = lane; c < nch; c += 64) fold_max(pr[c]);
+            for (int cc = lane; cc < nch; cc += 64) fold_max(pr[cc]);
         }
         M = dpp_max(M);
         ak = dpp_reduce(ak, uint64_t(0), [](uint64_t u, uint64_t v) { return u > v ? u : v; });
@@ -606,7 +596,7 @@ namespace mg
 #pragma unroll
                 for (int k = 0; k < PPL; ++k) fold_sum(pv[k]);
             } else {
-                for (int c = lane; c < nch; c += 64) fold_sum(pr[c]);
+                for (int cc = lane; cc < nch; cc += 64) fold_sum(pr[cc]);
             }
         }
         S = dpp_sum(S);
@@ -617,58 +607,142 @@ namespace mg
         }
         if (!want_top) return;
 
-        // first try: the blocks alone
-        bool done = false;
+        auto nvalid_of = [&](int cc) {
+            const int64_t cb = int64_t(cc) * kVChunk;
+            return int(V - cb < kVChunk ? V - cb : kVChunk);
+        };
+        // the blocks as a key source (kBlk slots per chunk, 0 past a block's end)
+        auto each_block = [&](auto f) {
+            for (int i0 = 0; i0 < nch * kBlk; i0 += 64) {
+                const int i = i0 + lane;
+                f(i < nch * kBlk ? bk[i] : uint64_t(0));
+            }
+        };
+
+        // first try: kap from the blocks, proved by every chunk's D-th key
+        uint64_t kap = 0;
+        int have = 0;
         if (regs) {
-            int have = 0;
 #pragma unroll
             for (int q = 0; q < kMergeRegs; ++q) have += wave_count(r[q] != 0);
-            if (have >= K) {
-                const uint64_t kap = wave_kth<kMergeRegs>(r, K, hist);
-                bool bad = false;
-                if (pregs) {
+            if (have >= K) kap = wave_kth<kMergeRegs>(r, K, hist);
+        } else {
+            each_block([&](uint64_t k) { have += wave_count(k != 0); });
+            if (have >= K) kap = source_kth(each_block, K, hist);
+        }
+        // chunk cc fails when keys outside its block may reach the top K
+        auto fails = [&](int cc) { return kap == 0 || pr[cc].kd > kap; };
+        bool bad = false;
+        if (kap != 0) {
+            if (pregs) {
 #pragma unroll
-                    for (int k = 0; k < PPL; ++k) bad |= pv[k].kd != 0 && pv[k].kd > kap;
-                } else {
-                    for (int c = lane; c < nch; c += 64) {
-                        const uint64_t kd = pr[c].kd;
-                        bad |= kd != 0 && kd > kap;
-                    }
-                }
-                done = __builtin_amdgcn_ballot_w64(bad) == 0;
-                if (done) {
-                    int n = 0;
-#pragma unroll
-                    for (int q = 0; q < kMergeRegs; ++q) {
-                        const bool take = r[q] != 0 && r[q] >= kap;
-                        const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
-                        if (mk) {
-                            if (take && n + lane_rank(mk) < 64 * SL) sel[n + lane_rank(mk)] = r[q];
-                            n += __builtin_popcountll(mk);
-                        }
-                    }
-                }
+                for (int k = 0; k < PPL; ++k) bad |= pv[k].kd > kap;
+            } else {
+                for (int cc = lane; cc < nch; cc += 64) bad |= pr[cc].kd > kap;
             }
         }
-        if (!done) {
-            const uint64_t kap = lists_kth(pr, ls, nch, cap, K);
-            int n = 0;
-            for (int c = 0; c < nch; ++c) {
-                const int nl = pr[c].nlist < cap ? pr[c].nlist : cap;
-                for (int p0 = 0; p0 < nl; p0 += 64) {
-                    const int p = p0 + lane;
-                    const uint64_t k = p < nl ? ls[int64_t(c) * cap + p] : 0;
-                    const bool take = k != 0 && k >= kap;
-                    const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
-                    if (mk) {
-                        if (take && n + lane_rank(mk) < 64 * SL) sel[n + lane_rank(mk)] = k;
-                        n += __builtin_popcountll(mk);
-                    }
+        bad = kap == 0 || __builtin_amdgcn_ballot_w64(bad) != 0;
+
+        int n = 0; // keys selected into sel
+        if (!bad && regs) {
+            // the K keys >= kap are all in the blocks held in registers
+#pragma unroll
+            for (int q = 0; q < kMergeRegs; ++q) {
+                const bool take = r[q] != 0 && r[q] >= kap;
+                const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
+                if (mk) {
+                    if (take && n + lane_rank(mk) < kMaxK) sel[n + lane_rank(mk)] = r[q];
+                    n += __builtin_popcountll(mk);
                 }
             }
+        } else {
+            // failing chunks: re-read into LDS as keys, exact top min(K, nvalid)
+            // by radix selection there, written to the list area
+            if (bad) {
+                for (int cc = 0; cc < nch; ++cc) {
+                    if (!fails(cc)) continue;
+                    const int nv = nvalid_of(cc);
+                    const int64_t cb = int64_t(cc) * kVChunk;
+                    const typename SI::raw *xr = L + row * ld + cb;
+                    wave_lds_sync();
+#pragma unroll 16
+                    for (int p0 = 0; p0 < kVChunk; p0 += 64) {
+                        const int p = p0 + lane;
+                        uint64_t k = 0;
+                        if (p < nv) {
+                            float v = float(SI::dec(xr[p]));
+                            if constexpr (TAIL) v = vtail<SI>(v, tail);
+                            k = vkey(vhi(v), uint32_t(cb + p));
+                        }
+                        ukeys[p] = k;
+                    }
+                    wave_lds_sync();
+                    auto each_chunk = [&](auto f) {
+                        for (int p0 = 0; p0 < nv; p0 += 64) f(ukeys[p0 + lane]);
+                    };
+                    const int nk = nv < K ? nv : K;
+                    const uint64_t kth = source_kth(each_chunk, nk, hist);
+                    int m = 0;
+                    each_chunk([&](uint64_t k) {
+                        const bool take = k != 0 && k >= kth;
+                        const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
+                        if (take) ls[cb / kVChunk * kMaxK + m + lane_rank(mk)] = k;
+                        m += __builtin_popcountll(mk);
+                    });
+                }
+                // the lists are read back by other lanes of this wave
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+                wave_lds_sync();
+            }
+            // the source: failing chunks' lists, the other chunks' blocks
+            auto each_src = [&](auto f) {
+                for (int cc = 0; cc < nch; ++cc) {
+                    const bool fl = bad && fails(cc);
+                    const int nv = nvalid_of(cc);
+                    const int cnt = fl ? (nv < K ? nv : K) : kBlk;
+                    const uint64_t *src = fl ? ls + int64_t(cc) * kMaxK : bk + int64_t(cc) * kBlk;
+                    for (int p0 = 0; p0 < cnt; p0 += 64) {
+                        const int p = p0 + lane;
+                        f(p < cnt ? src[p] : uint64_t(0));
+                    }
+                }
+            };
+            // staged in LDS when it fits, so the radix passes read LDS
+            int total = 0;
+            for (int cc = 0; cc < nch; ++cc) {
+                const int nv = nvalid_of(cc);
+                total += (bad && fails(cc)) ? (nv < K ? nv : K) : kBlk;
+            }
+            const bool staged = total <= kUnionCap;
+            int nu = 0;
+            if (staged) {
+                each_src([&](uint64_t k) {
+                    const uint64_t mk = __builtin_amdgcn_ballot_w64(k != 0);
+                    if (k) ukeys[nu + lane_rank(mk)] = k;
+                    nu += __builtin_popcountll(mk);
+                });
+                wave_lds_sync();
+            }
+            auto each_lds = [&](auto f) {
+                for (int i0 = 0; i0 < nu; i0 += 64) {
+                    const int i = i0 + lane;
+                    f(i < nu ? ukeys[i] : uint64_t(0));
+                }
+            };
+            const uint64_t kap2 = staged ? source_kth(each_lds, K, hist) : source_kth(each_src, K, hist);
+            auto pick = [&](uint64_t k) {
+                const bool take = k != 0 && k >= kap2;
+                const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
+                if (take && n + lane_rank(mk) < kMaxK) sel[n + lane_rank(mk)] = k;
+                n += __builtin_popcountll(mk);
+            };
+            if (staged)
+                each_lds(pick);
+            else
+                each_src(pick);
         }
         wave_lds_sync();
-        // exactly K keys were selected (keys are unique)
+        // exactly K keys were selected (keys are unique); SL per lane
         uint64_t a[SL];
 #pragma unroll
         for (int q = 0; q < SL; ++q) {
@@ -692,7 +766,7 @@ namespace mg
                     tv = key_f32(hk);
                 } else if (ok) {
                     // NaN and +-0 share a key per class: read the value back
-                    tv = float(SI::dec(L[row * V + j]));
+                    tv = float(SI::dec(L[row * ld + j]));
                     if constexpr (TAIL) tv = vtail<SI>(tv, tail);
                 }
                 if (top_val) top_val[row * K + i] = tv;
@@ -703,12 +777,14 @@ namespace mg
     // The pass on `stream` with its partials in `work` (work_bytes long);
     // `room` names where they live for the error raised when they do not fit.
     static void vocab_pass(hipStream_t stream, void *work, int64_t work_bytes, const char *room, const void *logits,
-                           int64_t rows, int64_t V, int dt_in, int64_t K, double *lse, int64_t *amax,
+                           int64_t ld, int64_t rows, int64_t V, int dt_in, int64_t K, double *lse, int64_t *amax,
                            int64_t *top_idx, float *top_val, bool tail_on, double mult, double cap, void *logits_out)
     {
         need(rows >= 0 && V > 0, "vocab_reduce: bad shape");
         need(V < (int64_t(1) << 31), "vocab_reduce: V must be < 2^31");
         need(logits != nullptr, "vocab_reduce: NULL logits");
+        ld = ld ? ld : V;
+        need(ld >= V, "vocab_reduce: row stride smaller than V");
         const bool want_top = top_idx || top_val;
         if (!want_top) K = 1;
         need(K >= 1 && K <= kMaxK, "vocab_reduce: K must be in [1, 256]");
@@ -716,44 +792,47 @@ namespace mg
         need(rows <= 65535, "vocab_reduce: at most 65535 rows per call");
         if (rows == 0) return;
         const int nch = int((V + kVChunk - 1) / kVChunk);
-        const bool small = K <= kFastK;
-        const int lcap = small ? 128 : 256; // list capacity per chunk
         const int64_t nc = rows * nch;
-        const int64_t need_bytes = nc * int64_t(sizeof(VPart) + sizeof(uint64_t) * (kBlk + lcap));
+        const int64_t need_bytes = nc * int64_t(sizeof(VPart) + sizeof(uint64_t) * (kBlk + kMaxK));
         need(need_bytes <= work_bytes, "vocab_reduce: the partials of " + std::to_string(rows) + " rows x " +
                                            std::to_string(nch) + " chunks need " + std::to_string(need_bytes) +
                                            " bytes, more than " + room + " (" + std::to_string(work_bytes) + ")");
         VPart *part = static_cast<VPart *>(work);
         uint64_t *blk = reinterpret_cast<uint64_t *>(part + nc);
         uint64_t *lst = blk + nc * kBlk;
-        const dim3 g1{unsigned((nch + 3) / 4), unsigned(rows), 1u};
+        const dim3 g1{unsigned(nch), unsigned(rows), 1u};
         const dim3 g2{unsigned(rows), 1u, 1u};
         // python-float scalars are f32 opmath values outside f64 (src/muse_glimmer.hpp:924-926)
         const VTail tail{float(mult), float(cap), logits_out};
         auto go = [&](auto chunk, auto merge, const auto *x) {
-            hipLaunchKernelGGL(chunk, g1, dim3(256), 0, stream, x, V, int(K), nch, part, blk, lst, tail);
+            hipLaunchKernelGGL(chunk, g1, dim3(64), 0, stream, x, ld, V, int(K), nch, part, blk, tail);
             check_launch("k_vocab_chunk");
-            hipLaunchKernelGGL(merge, g2, dim3(64), 0, stream, x, V, int(K), nch, lcap, part, blk, lst, lse, amax,
+            hipLaunchKernelGGL(merge, g2, dim3(64), 0, stream, x, ld, V, int(K), nch, part, blk, lst, lse, amax,
                                top_idx, top_val, tail);
             check_launch("k_vocab_merge");
         };
         auto pick = [&](auto si, auto vw, const auto *x) {
             using SI = decltype(si);
             constexpr int VW = decltype(vw)::value;
-            if (small && tail_on) go(k_vocab_chunk<SI, VW, 2, true>, k_vocab_merge<SI, 1, true>, x);
-            else if (small) go(k_vocab_chunk<SI, VW, 2, false>, k_vocab_merge<SI, 1, false>, x);
-            else if (tail_on) go(k_vocab_chunk<SI, VW, 4, true>, k_vocab_merge<SI, 4, true>, x);
-            else go(k_vocab_chunk<SI, VW, 4, false>, k_vocab_merge<SI, 4, false>, x);
+            if (K <= 64 && tail_on)
+                go(k_vocab_chunk<SI, VW, true>, k_vocab_merge<SI, VW, 1, true>, x);
+            else if (K <= 64)
+                go(k_vocab_chunk<SI, VW, false>, k_vocab_merge<SI, VW, 1, false>, x);
+            else if (tail_on)
+                go(k_vocab_chunk<SI, VW, true>, k_vocab_merge<SI, VW, 4, true>, x);
+            else
+                go(k_vocab_chunk<SI, VW, false>, k_vocab_merge<SI, VW, 4, false>, x);
         };
+        const bool out_ok = !logits_out || aligned16(logits_out);
         if (dt_in == F32) {
             const float *x = static_cast<const float *>(logits);
-            if (V % 4 == 0 && aligned16(x) && (!logits_out || aligned16(logits_out)))
+            if (V % 4 == 0 && ld % 4 == 0 && aligned16(x) && out_ok)
                 pick(SF32{}, std::integral_constant<int, 4>{}, x);
             else
                 pick(SF32{}, std::integral_constant<int, 1>{}, x);
         } else if (dt_in == BF16) {
             const uint16_t *x = static_cast<const uint16_t *>(logits);
-            if (V % 8 == 0 && aligned16(x) && (!logits_out || aligned16(logits_out)))
+            if (V % 8 == 0 && ld % 8 == 0 && aligned16(x) && out_ok)
                 pick(SBf16{}, std::integral_constant<int, 8>{}, x);
             else
                 pick(SBf16{}, std::integral_constant<int, 1>{}, x);
@@ -762,12 +841,12 @@ namespace mg
         }
     }
 
-    void launch_vocab(mg_ctx *c, const void *logits, int64_t rows, int64_t V, int dt_in, int64_t K,
+    void launch_vocab(mg_ctx *c, const void *logits, int64_t ld, int64_t rows, int64_t V, int dt_in, int64_t K,
                       double *lse, int64_t *amax, int64_t *top_idx, float *top_val, bool tail_on, double mult,
                       double cap, void *logits_out)
     {
         vocab_pass(c->stream, c->work, c->work_bytes, "the context workspace (raise workspace_bytes at mg_open)",
-                   logits, rows, V, dt_in, K, lse, amax, top_idx, top_val, tail_on, mult, cap, logits_out);
+                   logits, ld, rows, V, dt_in, K, lse, amax, top_idx, top_val, tail_on, mult, cap, logits_out);
     }
 
     // ------------------------------------------------- allocation-free variant
@@ -800,10 +879,10 @@ namespace mg
         return addr[dev];
     }
 
-    void launch_vocab_noalloc(hipStream_t stream, const void *logits, int64_t rows, int64_t V, int dt_in, int64_t K,
-                              double *lse, int64_t *amax, int64_t *top_idx, float *top_val)
+    void launch_vocab_noalloc(hipStream_t stream, const void *logits, int64_t ld, int64_t rows, int64_t V,
+                              int dt_in, int64_t K, double *lse, int64_t *amax, int64_t *top_idx, float *top_val)
     {
-        vocab_pass(stream, scratch_address(), kVocabScratchBytes, "the fixed scratch array", logits, rows, V, dt_in,
-                   K, lse, amax, top_idx, top_val, false, 1.0, 0.0, nullptr);
+        vocab_pass(stream, scratch_address(), kVocabScratchBytes, "the fixed scratch array", logits, ld, rows, V,
+                   dt_in, K, lse, amax, top_idx, top_val, false, 1.0, 0.0, nullptr);
     }
 } // namespace mg

@@ -261,33 +261,33 @@ int mg_dequant_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, void *out,
     });
 }
 
-int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, int dtype_in,
+int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t V, int dtype_in,
                     int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val)
 {
     MG_GUARD(-1, {
-        mg::launch_vocab(ctx_of(ctx), logits, rows, V, dtype_in, K, lse, argmax, top_idx, top_val, false, 1.0, 0.0,
+        mg::launch_vocab(ctx_of(ctx), logits, ld, rows, V, dtype_in, K, lse, argmax, top_idx, top_val, false, 1.0, 0.0,
                          nullptr);
         return 0;
     });
 }
 
-int mg_vocab_reduce_tail(mg_ctx *ctx, const void *logits, int64_t rows, int64_t V, int dtype_in, double mult,
-                         double cap, int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val,
-                         void *logits_out)
+int mg_vocab_reduce_tail(mg_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t V, int dtype_in,
+                         double mult, double cap, int64_t K, double *lse, int64_t *argmax, int64_t *top_idx,
+                         float *top_val, void *logits_out)
 {
     MG_GUARD(-1, {
-        mg::launch_vocab(ctx_of(ctx), logits, rows, V, dtype_in, K, lse, argmax, top_idx, top_val, true, mult, cap,
+        mg::launch_vocab(ctx_of(ctx), logits, ld, rows, V, dtype_in, K, lse, argmax, top_idx, top_val, true, mult, cap,
                          logits_out);
         return 0;
     });
 }
 
-int mg_vocab_reduce_noalloc(void *stream, const void *logits, int64_t rows, int64_t V, int dtype_in, int64_t K,
-                            double *lse, int64_t *argmax, int64_t *top_idx, float *top_val)
+int mg_vocab_reduce_noalloc(void *stream, const void *logits, int64_t ld, int64_t rows, int64_t V, int dtype_in,
+                            int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val)
 {
     MG_GUARD(-1, {
-        mg::launch_vocab_noalloc(static_cast<hipStream_t>(stream), logits, rows, V, dtype_in, K, lse, argmax, top_idx,
-                                 top_val);
+        mg::launch_vocab_noalloc(static_cast<hipStream_t>(stream), logits, ld, rows, V, dtype_in, K, lse, argmax,
+                                 top_idx, top_val);
         return 0;
     });
 }

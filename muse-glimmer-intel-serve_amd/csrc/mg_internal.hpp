@@ -94,12 +94,12 @@ namespace mg
     void launch_attn_decode(mg_ctx *c, const uint16_t *q, const uint16_t *kc, const uint16_t *vc, int64_t nq,
                             int64_t nkv, int64_t D, int64_t slots, int64_t qpos, int64_t window, double scaling,
                             float *out);
-    void launch_vocab(mg_ctx *c, const void *logits, int64_t rows, int64_t V, int dt_in, int64_t K,
+    void launch_vocab(mg_ctx *c, const void *logits, int64_t ld, int64_t rows, int64_t V, int dt_in, int64_t K,
                       double *lse, int64_t *amax, int64_t *top_idx, float *top_val, bool tail_on, double mult,
                       double cap, void *logits_out);
     // the vocab pass without a context: partials in a fixed device array of
     // kVocabScratchBytes (k_vocab.hip), on `stream` of the current device
     constexpr int64_t kVocabScratchBytes = int64_t(16) << 20;
-    void launch_vocab_noalloc(hipStream_t stream, const void *logits, int64_t rows, int64_t V, int dt_in, int64_t K,
-                              double *lse, int64_t *amax, int64_t *top_idx, float *top_val);
+    void launch_vocab_noalloc(hipStream_t stream, const void *logits, int64_t ld, int64_t rows, int64_t V,
+                              int dt_in, int64_t K, double *lse, int64_t *amax, int64_t *top_idx, float *top_val);
 } // namespace mg

@@ -56,14 +56,14 @@ _SIGS = {
     "mg_softmax_rows": ([_P, _P, _I, _P, _I, _I, _I, _I, _D, _INT, _I, _I, _D, _INT, _INT], _INT),
     "mg_softcap": ([_P, _P, _I, _D, _D, _INT], _INT),
     "mg_dequant_q8_0": ([_P, _P, _P, _P, _I, _I, _INT], _INT),
-    "mg_vocab_reduce": ([_P, _P, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
+    "mg_vocab_reduce": ([_P, _P, _I, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
     "mg_quantize_q8_0": ([_P, _P, _I, _I, _P, _P], _INT),
     "mg_gemv_q8_0": ([_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _INT], _INT),
     "mg_attn_decode": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _D, _P], _INT),
     "mg_attn_prefill": ([_P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _D, _P, _I], _INT),
     "mg_sample_dist": ([_P, _P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P], _INT),
-    "mg_vocab_reduce_tail": ([_P, _P, _I, _I, _INT, _D, _D, _I, _P, _P, _P, _P, _P], _INT),
-    "mg_vocab_reduce_noalloc": ([_P, _P, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
+    "mg_vocab_reduce_tail": ([_P, _P, _I, _I, _I, _INT, _D, _D, _I, _P, _P, _P, _P, _P], _INT),
+    "mg_vocab_reduce_noalloc": ([_P, _P, _I, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
 }
 
 _lib = None
@@ -427,7 +427,7 @@ class Prims:
         """Per row: logsumexp, first argmax, top-K (value desc, index asc)."""
         import torch
         self._dev(logits)
-        self._contig("vocab_reduce", logits)
+        ld = self._rows("vocab_reduce", logits)
         rows, V = logits.shape
         dev = logits.device
         if lse is None:
@@ -439,7 +439,7 @@ class Prims:
         if K > 0 and top_val is None:
             top_val = torch.empty((rows, K), dtype=torch.float32, device=dev)
         self._vocab_outs("vocab_reduce", rows, K, lse, argmax, top_idx, top_val)
-        self._check(self.lib.mg_vocab_reduce(self.h, _ptr(logits), rows, V, _dtype_code(logits), K, _ptr(lse),
+        self._check(self.lib.mg_vocab_reduce(self.h, _ptr(logits), ld, rows, V, _dtype_code(logits), K, _ptr(lse),
                                              _ptr(argmax), _ptr(top_idx) if K > 0 else None,
                                              _ptr(top_val) if K > 0 else None))
         return lse, argmax, top_idx, top_val
@@ -449,11 +449,11 @@ class Prims:
         library's fixed scratch array instead; outputs must be given (nothing is
         allocated). `stream` defaults to this context's stream."""
         self._dev(logits)
-        self._contig("vocab_reduce_noalloc", logits)
+        ld = self._rows("vocab_reduce_noalloc", logits)
         rows, V = logits.shape
         self._vocab_outs("vocab_reduce_noalloc", rows, K, lse, argmax, top_idx, top_val)
         s = self.stream() if stream is None else stream
-        rc = self.lib.mg_vocab_reduce_noalloc(ctypes.c_void_p(s), _ptr(logits), rows, V, _dtype_code(logits), K,
+        rc = self.lib.mg_vocab_reduce_noalloc(ctypes.c_void_p(s), _ptr(logits), ld, rows, V, _dtype_code(logits), K,
                                               _ptr(lse), _ptr(argmax), _ptr(top_idx), _ptr(top_val))
         self._check(rc)
 
@@ -484,7 +484,8 @@ class Prims:
         receives them (the input is left as it is)."""
         import torch
         self._dev(logits, logits_out)
-        self._contig("vocab_reduce_tail", logits, logits_out)
+        ld = self._rows("vocab_reduce_tail", logits)
+        self._contig("vocab_reduce_tail", logits_out)
         self._same("vocab_reduce_tail", logits, logits_out)
         rows, V = logits.shape
         self._numel("vocab_reduce_tail logits_out", logits_out, rows * V)
@@ -493,7 +494,7 @@ class Prims:
         argmax = torch.empty(rows, dtype=torch.int64, device=dev)
         top_idx = torch.empty((rows, K), dtype=torch.int64, device=dev)
         top_val = torch.empty((rows, K), dtype=torch.float32, device=dev)
-        self._check(self.lib.mg_vocab_reduce_tail(self.h, _ptr(logits), rows, V, _dtype_code(logits), mult, cap, K,
+        self._check(self.lib.mg_vocab_reduce_tail(self.h, _ptr(logits), ld, rows, V, _dtype_code(logits), mult, cap, K,
                                                   _ptr(lse), _ptr(argmax), _ptr(top_idx), _ptr(top_val),
                                                   _ptr(logits_out)))
         return lse, argmax, top_idx, top_val

@@ -26,7 +26,7 @@ def noalloc(lib, stream, logits, K):
     ti = torch.full((rows, K), -7, dtype=torch.int64, device=dev)
     tv = torch.full((rows, K), np.nan, dtype=torch.float32, device=dev)
     code = {torch.float32: 3, torch.bfloat16: 1}[logits.dtype]
-    rc = lib.mg_vocab_reduce_noalloc(ctypes.c_void_p(stream), ctypes.c_void_p(logits.data_ptr()), rows, V, code, K,
+    rc = lib.mg_vocab_reduce_noalloc(ctypes.c_void_p(stream), ctypes.c_void_p(logits.data_ptr()), 0, rows, V, code, K,
                                      ctypes.c_void_p(lse.data_ptr()), ctypes.c_void_p(am.data_ptr()),
                                      ctypes.c_void_p(ti.data_ptr()), ctypes.c_void_p(tv.data_ptr()))
     return rc, lse, am, ti, tv
@@ -61,7 +61,7 @@ def test_noalloc_rejects_partials_beyond_the_scratch(prims):
     import torch
     lib = prims.lib
     stream = torch.cuda.current_stream().cuda_stream
-    # 1024 rows x 99 chunks need 1024 * 99 * 1128 bytes (114 MB) > 16 MiB: refused, nothing launched
+    # 1024 rows x 50 chunks need 1024 * 50 * 2216 bytes (113 MB) > 16 MiB: refused, nothing launched
     big = torch.zeros((1024, 201088), dtype=torch.float32, device="cuda:0")
     rc, *_ = noalloc(lib, stream, big, 64)
     assert rc == -1 and b"fixed scratch array" in lib.mg_last_error()
