@@ -105,39 +105,102 @@ namespace mg
         return 0xffffffffu - uint32_t(k);
     }
 
-    // Descending bitonic sort of the 64*SL values a wave holds SL per lane
-    // (slot SL*lane + q in a[q]). Ascending/descending runs of the network are
-    // chosen per slot; partners at distance >= SL live in lane ^ (j / SL).
-    template <typename T, int SL>
-    MG_DEV void wave_sort_desc(T (&a)[SL])
+    // ------------------------------------------------ wave bitonic networks
+    // A 32-bit word and its copy from lane ^ J, in either order (the
+    // compare-exchange below is symmetric in them). J = 1, 2: quad
+    // permutes; J = 4: within each row of 16, rotations by 12 on the banks
+    // whose lane bit 2 is clear and by 4 on the others; J = 8: rotation by 8;
+    // J = 16, 32: v_permlane16_swap / v_permlane32_swap, whose two results hold
+    // own and partner word in every lane. No LDS traffic.
+    template <int J>
+    MG_DEV void xor_pair(uint32_t v, uint32_t &a, uint32_t &b)
+    {
+        if constexpr (J == 1) {
+            a = v;
+            b = dpp32<0xB1, 0xf>(0u, v);
+        } else if constexpr (J == 2) {
+            a = v;
+            b = dpp32<0x4E, 0xf>(0u, v);
+        } else if constexpr (J == 4) {
+            a = v;
+            b = dpp32<0x124, 0xf, 0xa>(dpp32<0x12C, 0xf, 0x5>(0u, v), v);
+        } else if constexpr (J == 8) {
+            a = v;
+            b = dpp32<0x128, 0xf>(0u, v);
+        } else if constexpr (J == 16) {
+            const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+            a = uint32_t(q[0]);
+            b = uint32_t(q[1]);
+        } else {
+            static_assert(J == 32, "xor_pair: J in 1 .. 32");
+            const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+            a = uint32_t(q[0]);
+            b = uint32_t(q[1]);
+        }
+    }
+    // compare-exchange of v with lane ^ J: the larger of the two if keep_max,
+    // else the smaller (32- or 64-bit unsigned words)
+    template <int J, typename T>
+    MG_DEV T cx(T v, bool keep_max)
+    {
+        T a, b;
+        if constexpr (sizeof(T) == 4) {
+            xor_pair<J>(v, a, b);
+        } else {
+            uint32_t al, bl, ah, bh;
+            xor_pair<J>(uint32_t(v), al, bl);
+            xor_pair<J>(uint32_t(v >> 32), ah, bh);
+            a = (uint64_t(ah) << 32) | al;
+            b = (uint64_t(bh) << 32) | bl;
+        }
+        return (a > b) == keep_max ? a : b;
+    }
+    template <typename T>
+    MG_DEV T cx_j(int j, T v, bool keep_max)
+    {
+        switch (j) {
+        case 1: return cx<1>(v, keep_max);
+        case 2: return cx<2>(v, keep_max);
+        case 4: return cx<4>(v, keep_max);
+        case 8: return cx<8>(v, keep_max);
+        case 16: return cx<16>(v, keep_max);
+        default: return cx<32>(v, keep_max);
+        }
+    }
+
+    // Descending bitonic sort of the 64*R words a wave holds in a[0..R-1],
+    // slot 64*r + lane in a[r]. Runs of the network ascend or descend by
+    // slot; partners 64 or more slots apart sit in the same lane. TOP64: only
+    // the largest 64 are wanted (in a[0], sorted): the last merge stage,
+    // after its cross-register step, sorts a[0] alone.
+    template <typename T, int R, bool TOP64 = false>
+    MG_DEV void wave_bitonic_desc(T (&a)[R])
     {
         const int lane = threadIdx.x & 63;
-        constexpr int N = 64 * SL;
+        constexpr int N = 64 * R;
 #pragma unroll
         for (int k = 2; k <= N; k <<= 1) {
 #pragma unroll
             for (int j = k >> 1; j > 0; j >>= 1) {
-                if (j < SL) {
+                if (j >= 64) {
+                    const int rj = j / 64;
 #pragma unroll
-                    for (int q = 0; q < SL; ++q) {
-                        const int p = q ^ j;
-                        if (p > q) {
-                            const bool desc = ((SL * lane + q) & k) == 0;
-                            const T x = a[q], y = a[p];
+                    for (int r = 0; r < R; ++r) {
+                        const int p = r ^ rj;
+                        if (p > r) {
+                            const bool desc = ((64 * r) & k) == 0;
+                            const T x = a[r], y = a[p];
                             const bool sw = desc ? (x < y) : (x > y);
-                            a[q] = sw ? y : x;
+                            a[r] = sw ? y : x;
                             a[p] = sw ? x : y;
                         }
                     }
                 } else {
-                    const int lj = j / SL;
-                    const bool lower = (lane & lj) == 0;
 #pragma unroll
-                    for (int q = 0; q < SL; ++q) {
-                        const T o = __shfl_xor(a[q], lj, 64);
-                        const bool desc = ((SL * lane + q) & k) == 0;
-                        const bool keep_max = lower == desc;
-                        a[q] = keep_max ? (a[q] > o ? a[q] : o) : (a[q] < o ? a[q] : o);
+                    for (int r = 0; r < R; ++r) {
+                        if (TOP64 && k == N && N > 64 && r > 0) continue;
+                        const bool desc = ((64 * r + lane) & k) == 0;
+                        a[r] = cx_j<T>(j, a[r], ((lane & j) == 0) == desc);
                     }
                 }
             }
@@ -406,22 +469,15 @@ namespace mg
 
         // ---- the block: the chunk's top D keys
         const int D = K < kBlk ? K : kBlk;
-        // t: the D-th largest lane maximum, equal values counted; at least D
-        // keys are >= t (-inf when fewer than D lanes hold a finite maximum)
-        float t = -__builtin_huge_valf();
+        // t: the D-th largest lane maximum, equal values counted (the lane
+        // maxima sorted by a bitonic network, read at lane D-1); at least D
+        // keys are >= t (-inf when fewer than D lanes hold a finite maximum).
+        // m1 is never NaN (fmax drops NaN operands) and -0 sorts as +0.
+        float t;
         {
-            float v = m1;
-            int left = D;
-            for (int i = 0; i < D; ++i) {
-                const float mx = dpp_max(v);
-                const int cnt = wave_count(v == mx);
-                if (cnt >= left || !(mx > -__builtin_huge_valf())) {
-                    t = mx;
-                    break;
-                }
-                left -= cnt;
-                v = v == mx ? -__builtin_huge_valf() : v;
-            }
+            uint32_t mk[1] = {f32_key(m1 + 0.0f)};
+            wave_bitonic_desc<uint32_t, 1>(mk);
+            t = key_f32(uint32_t(__builtin_amdgcn_readlane(int(mk[0]), D - 1)));
         }
         // candidates: the keys >= t (never NaN; the -inf placeholders past V
         // only when t is -inf, which takes the exact path), compacted into LDS
@@ -519,7 +575,11 @@ namespace mg
         return prefix;
     }
 
-    template <class SI, int VW, int SL, bool TAIL>
+    // Pass 2, one wave per row. FAST (K <= 64, at most 64 chunks, at least K
+    // block keys): lane c first holds chunk c's block and tries the threshold
+    // selection below; the general selection runs only where that cannot
+    // prove its answer.
+    template <class SI, int VW, int SL, bool TAIL, bool FAST>
     __global__ __launch_bounds__(64) void k_vocab_merge(const typename SI::raw *__restrict__ L, int64_t ld,
                                                         int64_t V, int K, int nch, const VPart *__restrict__ part,
                                                         const uint64_t *__restrict__ blk, uint64_t *__restrict__ lst,
@@ -558,11 +618,51 @@ namespace mg
             }
         }
         uint64_t r[kMergeRegs];
+        auto load_r = [&]() {
 #pragma unroll
-        for (int q = 0; q < kMergeRegs; ++q) {
-            const int i = lane + 64 * q;
-            r[q] = regs && i / kBlk < nch ? bk[i] : 0;
+            for (int q = 0; q < kMergeRegs; ++q) {
+                const int i = lane + 64 * q;
+                r[q] = regs && i / kBlk < nch ? bk[i] : 0;
+            }
+        };
+        uint64_t b[kBlk]; // FAST: chunk `lane`'s block
+        if constexpr (FAST) {
+#pragma unroll
+            for (int i = 0; i < kBlk; i += 2) {
+                Vec<uint64_t, 2> w{{0, 0}};
+                if (lane < nch) w = *reinterpret_cast<const Vec<uint64_t, 2> *>(bk + lane * kBlk + i);
+                b[i] = w.v[0];
+                b[i + 1] = w.v[1];
+            }
+        } else {
+            load_r();
         }
+
+        // the K keys in a[] (sorted, slot 64*q + lane) to the outputs
+        auto emit = [&](const uint64_t *a) {
+#pragma unroll
+            for (int q = 0; q < SL; ++q) {
+                const int i = 64 * q + lane;
+                if (i < K) {
+                    // a[q] is one of the K selected keys; an empty slot would be a
+                    // bug, reported as index -1 rather than read out of bounds
+                    const uint32_t j = vkey_index(a[q]);
+                    const bool ok = a[q] != 0 && int64_t(j) < V;
+                    if (top_idx) top_idx[row * K + i] = ok ? int64_t(j) : -1;
+                    float tv = -__builtin_huge_valf();
+                    const uint32_t hk = uint32_t(a[q] >> 32);
+                    if (ok && hk != 1u && hk != f32_key(0.0f)) {
+                        // the key's high word is the (transformed) value itself
+                        tv = key_f32(hk);
+                    } else if (ok) {
+                        // NaN and +-0 share a key per class: read the value back
+                        tv = float(SI::dec(L[row * ld + j]));
+                        if constexpr (TAIL) tv = vtail<SI>(tv, tail);
+                    }
+                    if (top_val) top_val[row * K + i] = tv;
+                }
+            }
+        };
 
         // lse and argmax: fold the chunk partials; the largest chunk key is
         // the row's first maximum
@@ -606,6 +706,59 @@ namespace mg
             if (amax) amax[row] = (x0 != x0 || ak == 0) ? 0 : int64_t(vkey_index(ak));
         }
         if (!want_top) return;
+
+        if constexpr (FAST) {
+            // T: the K-th largest high word among the first h keys of every
+            // block (h * nch >= K heads, 128 at most), by a bitonic sort of
+            // two registers. At least K keys have high word >= T, so the
+            // union's K-th key kap has high word >= T too, and the keys whose
+            // high word reaches T (a prefix of each sorted block) hold the
+            // union's top K. When at most 128 of them exist they are sorted;
+            // kap is the K-th, and the answer holds when no chunk's D-th key
+            // (kd: every key outside its block lies below it) exceeds kap.
+            const int h0 = (K + nch - 1) / nch;
+            const int h = h0 < D ? h0 : D;
+#pragma unroll
+            for (int i = 0; i < kBlk; ++i)
+                if (i < h && lane < nch) hist[lane * h + i] = uint32_t(b[i] >> 32);
+            wave_lds_sync();
+            uint32_t hv[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) hv[q] = 64 * q + lane < nch * h ? hist[64 * q + lane] : 0u;
+            wave_bitonic_desc<uint32_t, 2, true>(hv);
+            const uint32_t T = uint32_t(__builtin_amdgcn_readlane(int(hv[0]), K - 1));
+            int c = 0;
+#pragma unroll
+            for (int i = 0; i < kBlk; ++i) c += uint32_t(b[i] >> 32) >= T ? 1 : 0;
+            const int incl = wave_prefix_sum(c);
+            const int ns = __builtin_amdgcn_readlane(incl, 63);
+            if (T != 0 && ns <= 128) {
+                const int off = incl - c;
+#pragma unroll
+                for (int i = 0; i < kBlk; ++i) {
+                    if (__builtin_amdgcn_ballot_w64(i < c) == 0) break;
+                    if (i < c) sel[off + i] = b[i];
+                }
+                wave_lds_sync();
+                uint64_t v[2];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) v[q] = 64 * q + lane < ns ? sel[64 * q + lane] : 0;
+                if (ns <= 64) {
+                    uint64_t v1[1] = {v[0]};
+                    wave_bitonic_desc<uint64_t, 1>(v1);
+                    v[0] = v1[0];
+                } else {
+                    wave_bitonic_desc<uint64_t, 2, true>(v);
+                }
+                const uint64_t kap = readlane64(v[0], K - 1);
+                if (__builtin_amdgcn_ballot_w64(pv[0].kd > kap) == 0) {
+                    emit(v);
+                    return;
+                }
+            }
+            wave_lds_sync(); // sel and hist are reused below
+            load_r();
+        }
 
         auto nvalid_of = [&](int cc) {
             const int64_t cb = int64_t(cc) * kVChunk;
@@ -742,36 +895,15 @@ namespace mg
                 each_src(pick);
         }
         wave_lds_sync();
-        // exactly K keys were selected (keys are unique); SL per lane
+        // exactly K keys were selected (keys are unique), slot 64*q + lane
         uint64_t a[SL];
 #pragma unroll
         for (int q = 0; q < SL; ++q) {
-            const int i = SL * lane + q;
+            const int i = 64 * q + lane;
             a[q] = i < K ? sel[i] : 0;
         }
-        wave_sort_desc<uint64_t, SL>(a);
-#pragma unroll
-        for (int q = 0; q < SL; ++q) {
-            const int i = SL * lane + q;
-            if (i < K) {
-                // a[q] is one of the K selected keys; an empty slot would be a
-                // bug, reported as index -1 rather than read out of bounds
-                const uint32_t j = vkey_index(a[q]);
-                const bool ok = a[q] != 0 && int64_t(j) < V;
-                if (top_idx) top_idx[row * K + i] = ok ? int64_t(j) : -1;
-                float tv = -__builtin_huge_valf();
-                const uint32_t hk = uint32_t(a[q] >> 32);
-                if (ok && hk != 1u && hk != f32_key(0.0f)) {
-                    // the key's high word is the (transformed) value itself
-                    tv = key_f32(hk);
-                } else if (ok) {
-                    // NaN and +-0 share a key per class: read the value back
-                    tv = float(SI::dec(L[row * ld + j]));
-                    if constexpr (TAIL) tv = vtail<SI>(tv, tail);
-                }
-                if (top_val) top_val[row * K + i] = tv;
-            }
-        }
+        wave_bitonic_desc<uint64_t, SL>(a);
+        emit(a);
     }
 
     // The pass on `stream` with its partials in `work` (work_bytes long);
@@ -811,17 +943,24 @@ namespace mg
                                top_idx, top_val, tail);
             check_launch("k_vocab_merge");
         };
+        // the threshold merge needs lane = chunk and at least K block keys
+        const int D = K < kBlk ? int(K) : kBlk;
+        const bool fast = K <= 64 && nch <= 64 && int64_t(nch) * D >= K;
         auto pick = [&](auto si, auto vw, const auto *x) {
             using SI = decltype(si);
             constexpr int VW = decltype(vw)::value;
-            if (K <= 64 && tail_on)
-                go(k_vocab_chunk<SI, VW, true>, k_vocab_merge<SI, VW, 1, true>, x);
+            if (fast && tail_on)
+                go(k_vocab_chunk<SI, VW, true>, k_vocab_merge<SI, VW, 1, true, true>, x);
+            else if (fast)
+                go(k_vocab_chunk<SI, VW, false>, k_vocab_merge<SI, VW, 1, false, true>, x);
+            else if (K <= 64 && tail_on)
+                go(k_vocab_chunk<SI, VW, true>, k_vocab_merge<SI, VW, 1, true, false>, x);
             else if (K <= 64)
-                go(k_vocab_chunk<SI, VW, false>, k_vocab_merge<SI, VW, 1, false>, x);
+                go(k_vocab_chunk<SI, VW, false>, k_vocab_merge<SI, VW, 1, false, false>, x);
             else if (tail_on)
-                go(k_vocab_chunk<SI, VW, true>, k_vocab_merge<SI, VW, 4, true>, x);
+                go(k_vocab_chunk<SI, VW, true>, k_vocab_merge<SI, VW, 4, true, false>, x);
             else
-                go(k_vocab_chunk<SI, VW, false>, k_vocab_merge<SI, VW, 4, false>, x);
+                go(k_vocab_chunk<SI, VW, false>, k_vocab_merge<SI, VW, 4, false, false>, x);
         };
         const bool out_ok = !logits_out || aligned16(logits_out);
         if (dt_in == F32) {
