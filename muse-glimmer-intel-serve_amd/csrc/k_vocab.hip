@@ -168,14 +168,16 @@ namespace mg
         }
     }
 
-    // Descending bitonic sort of the 64*R words a wave holds in a[0..R-1],
-    // slot 64*r + lane in a[r]. Runs of the network ascend or descend by
-    // slot; partners 64 or more slots apart sit in the same lane. TOP64: only
-    // the largest 64 are wanted (in a[0], sorted): the last merge stage,
-    // after its cross-register step, sorts a[0] alone.
-    template <typename T, int R, bool TOP64 = false>
-    MG_DEV void wave_bitonic_desc(T (&a)[R])
+    // Bitonic sort of the 64*R words a wave holds in a[0..R-1], slot 64*r +
+    // lane in a[r], descending (DESC) or ascending. Runs of the network ascend
+    // or descend by slot; partners 64 or more slots apart sit in the same
+    // lane. TOP64 (descending only): only the largest 64 are wanted, in a[0],
+    // sorted: the last merge stage, after its cross-register step, sorts a[0]
+    // alone.
+    template <typename T, int R, bool DESC, bool TOP64 = false>
+    MG_DEV void wave_bitonic(T (&a)[R])
     {
+        static_assert(DESC || !TOP64, "wave_bitonic: TOP64 sorts descending");
         const int lane = threadIdx.x & 63;
         constexpr int N = 64 * R;
 #pragma unroll
@@ -188,7 +190,7 @@ namespace mg
                     for (int r = 0; r < R; ++r) {
                         const int p = r ^ rj;
                         if (p > r) {
-                            const bool desc = ((64 * r) & k) == 0;
+                            const bool desc = (((64 * r) & k) == 0) == DESC;
                             const T x = a[r], y = a[p];
                             const bool sw = desc ? (x < y) : (x > y);
                             a[r] = sw ? y : x;
@@ -199,12 +201,29 @@ namespace mg
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
                         if (TOP64 && k == N && N > 64 && r > 0) continue;
-                        const bool desc = ((64 * r + lane) & k) == 0;
+                        const bool desc = (((64 * r + lane) & k) == 0) == DESC;
                         a[r] = cx_j<T>(j, a[r], ((lane & j) == 0) == desc);
                     }
                 }
             }
         }
+    }
+    template <typename T, int R, bool TOP64 = false>
+    MG_DEV void wave_bitonic_desc(T (&a)[R])
+    {
+        wave_bitonic<T, R, true, TOP64>(a);
+    }
+
+    // top: the 64 largest of two sorted runs, a (descending) and b
+    // (ascending): their slot-wise maxima form a bitonic sequence holding the
+    // 64 largest, which the half-cleaners sort (descending)
+    MG_DEV uint64_t top64_merge(uint64_t a, uint64_t b)
+    {
+        const int lane = threadIdx.x & 63;
+        uint64_t v = a > b ? a : b;
+#pragma unroll
+        for (int j = 32; j > 0; j >>= 1) v = cx_j<uint64_t>(j, v, (lane & j) == 0);
+        return v;
     }
 
     // ------------------------------------------------------------------ pass 1
@@ -409,17 +428,15 @@ namespace mg
         return (uint64_t(hi) << 32) | lo;
     }
 
+    // Pass 1 on chunk `ch` of `row`, one wave: the chunk's partial and block.
+    // sb, so and sel are LDS arrays of kCand entries.
     template <class SI, int VW, bool TAIL>
-    __global__ __launch_bounds__(64) void k_vocab_chunk(const typename SI::raw *__restrict__ L, int64_t ld,
-                                                        int64_t V, int K, int nch, VPart *__restrict__ part,
-                                                        uint64_t *__restrict__ blk, VTail tail)
+    MG_DEV void chunk_pass(const typename SI::raw *__restrict__ L, int64_t ld, int64_t V, int K, int nch,
+                           VPart *__restrict__ part, uint64_t *__restrict__ blk, const VTail &tail, int ch,
+                           int64_t row, uint32_t *sb, uint32_t *so, uint64_t *sel)
     {
         using raw = typename SI::raw;
-        __shared__ uint32_t sb[kCand], so[kCand];
-        __shared__ uint64_t sel[kCand];
         const int lane = threadIdx.x & 63;
-        const int ch = int(blockIdx.x);
-        const int64_t row = blockIdx.y;
         const int64_t cb = int64_t(ch) * kVChunk;
         const int nvalid = int(V - cb < kVChunk ? V - cb : kVChunk);
         uint32_t xb[kVLane];
@@ -529,6 +546,16 @@ namespace mg
         }
     }
 
+    template <class SI, int VW, bool TAIL>
+    __global__ __launch_bounds__(64) void k_vocab_chunk(const typename SI::raw *__restrict__ L, int64_t ld,
+                                                        int64_t V, int K, int nch, VPart *__restrict__ part,
+                                                        uint64_t *__restrict__ blk, VTail tail)
+    {
+        __shared__ uint32_t sb[kCand], so[kCand];
+        __shared__ uint64_t sel[kCand];
+        chunk_pass<SI, VW, TAIL>(L, ld, V, K, nch, part, blk, tail, int(blockIdx.x), blockIdx.y, sb, so, sel);
+    }
+
     // ------------------------------------------------------------------ pass 2
     // The K-th largest key over a key source, by 8-bit radix selection with an
     // LDS histogram: each pass counts the keys that match the digits fixed so
@@ -573,6 +600,134 @@ namespace mg
             need -= above;
         }
         return prefix;
+    }
+
+    // lse and argmax of a row from its chunk partials: each(f) calls f on
+    // every partial this lane holds. The largest chunk key is the row's first
+    // maximum; x0 is the row's first logit (tail-transformed).
+    template <class EACH>
+    MG_DEV void fold_row(EACH each, float x0, int64_t row, double *lse, int64_t *amax)
+    {
+        const int lane = threadIdx.x & 63;
+        float M = -__builtin_huge_valf();
+        uint64_t ak = 0;
+        bool any = false;
+        each([&](const VPart &p) {
+            if (p.fin) {
+                M = p.m > M ? p.m : M;
+                any = true;
+            }
+            ak = p.top > ak ? p.top : ak;
+        });
+        M = dpp_max(M);
+        ak = dpp_reduce(ak, uint64_t(0), [](uint64_t u, uint64_t v) { return u > v ? u : v; });
+        any = __builtin_amdgcn_ballot_w64(any) != 0;
+        // sum of l_c * e^(m_c - M): the f32 difference and hardware exp2 keep
+        // each term within a few ulp of f32, far inside the lse tolerance
+        double S = 0.0;
+        if (any)
+            each([&](const VPart &p) {
+                if (p.fin) S += p.l * double(__builtin_amdgcn_exp2f((p.m - M) * 1.44269504088896341f));
+            });
+        S = dpp_sum(S);
+        if (lane == 0) {
+            if (lse) lse[row] = any ? double(M) + mgm::log(S) : -__builtin_huge_val();
+            // the scan starts at index 0: a NaN there is never beaten
+            if (amax) amax[row] = (x0 != x0 || ak == 0) ? 0 : int64_t(vkey_index(ak));
+        }
+    }
+
+    // The K selected keys, sorted, slot 64*q + lane of a[q], to the outputs
+    template <class SI, bool TAIL, int SL>
+    MG_DEV void emit_top(const typename SI::raw *__restrict__ L, int64_t ld, int64_t V, int K, int64_t row,
+                         const uint64_t *a, int64_t *top_idx, float *top_val, const VTail &tail)
+    {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int q = 0; q < SL; ++q) {
+            const int i = 64 * q + lane;
+            if (i < K) {
+                // a[q] is one of the K selected keys; an empty slot would be a
+                // bug, reported as index -1 rather than read out of bounds
+                const uint32_t j = vkey_index(a[q]);
+                const bool ok = a[q] != 0 && int64_t(j) < V;
+                if (top_idx) top_idx[row * K + i] = ok ? int64_t(j) : -1;
+                float tv = -__builtin_huge_valf();
+                const uint32_t hk = uint32_t(a[q] >> 32);
+                if (ok && hk != 1u && hk != f32_key(0.0f)) {
+                    // the key's high word is the (transformed) value itself
+                    tv = key_f32(hk);
+                } else if (ok) {
+                    // NaN and +-0 share a key per class: read the value back
+                    tv = float(SI::dec(L[row * ld + j]));
+                    if constexpr (TAIL) tv = vtail<SI>(tv, tail);
+                }
+                if (top_val) top_val[row * K + i] = tv;
+            }
+        }
+    }
+
+    // Exact top nk = min(K, nvalid) keys (K <= 64) of one chunk, re-read from
+    // the logits, sorted into stage[0..63] (0 past nk). t, the K-th largest
+    // lane maximum, has at least K keys at or above it; when at most 256
+    // keys reach it they are sorted by a bitonic network, else (ties, NaN,
+    // fewer than K finite lane maxima) nk rounds of chunk_exact_top select
+    // them. stage holds 256 keys; sb and so kCand words each.
+    template <class SI, int VW, bool TAIL>
+    MG_DEV int chunk_topk(const typename SI::raw *__restrict__ xr, int nvalid, int K, const VTail &tail, int64_t cb,
+                          uint64_t *stage, uint32_t *sb, uint32_t *so)
+    {
+        const int lane = threadIdx.x & 63;
+        uint32_t xb[kVLane];
+        auto x = [&](int s) { return __builtin_bit_cast(float, xb[s]); };
+        chunk_load<SI, VW, TAIL>(xr, nvalid, tail, nullptr, xb);
+        float m1 = -__builtin_huge_valf();
+#pragma unroll
+        for (int s = 0; s < kVLane; ++s) m1 = __builtin_fmaxf(m1, x(s));
+        uint32_t mk[1] = {f32_key(m1 + 0.0f)};
+        wave_bitonic_desc<uint32_t, 1>(mk);
+        const float t = key_f32(uint32_t(__builtin_amdgcn_readlane(int(mk[0]), K - 1)));
+        const int nk = nvalid < K ? nvalid : K;
+        int n = 0;
+        wave_lds_sync();
+        if (t > -__builtin_huge_valf()) {
+#pragma unroll
+            for (int s = 0; s < kVLane; ++s) {
+                const bool take = x(s) >= t;
+                const uint64_t m = __builtin_amdgcn_ballot_w64(take);
+                if (m) {
+                    const int p = n + lane_rank(m);
+                    if (take && p < 256) stage[p] = vkey(vhi(x(s)), uint32_t(cb + voff<VW>(lane, s)));
+                    n += __builtin_popcountll(m);
+                }
+            }
+        }
+        if (t > -__builtin_huge_valf() && n <= 256) {
+            wave_lds_sync();
+            uint64_t v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = 64 * q + lane < n ? stage[64 * q + lane] : 0;
+            if (n <= 64) {
+                uint64_t v1[1] = {v[0]};
+                wave_bitonic_desc<uint64_t, 1>(v1);
+                v[0] = v1[0];
+            } else if (n <= 128) {
+                uint64_t v2[2] = {v[0], v[1]};
+                wave_bitonic_desc<uint64_t, 2, true>(v2);
+                v[0] = v2[0];
+            } else {
+                wave_bitonic_desc<uint64_t, 4, true>(v);
+            }
+            wave_lds_sync();
+            stage[lane] = lane < nk ? v[0] : 0;
+        } else {
+            wave_lds_sync();
+            chunk_exact_top<VW>(xb, nvalid, nk, sb, so);
+            wave_lds_sync();
+            stage[lane] = lane < nk ? vkey(sb[lane], uint32_t(cb + so[lane])) : 0;
+        }
+        wave_lds_sync();
+        return nk;
     }
 
     // Pass 2, one wave per row. FAST (K <= 64, at most 64 chunks, at least K
@@ -638,73 +793,17 @@ namespace mg
             load_r();
         }
 
-        // the K keys in a[] (sorted, slot 64*q + lane) to the outputs
-        auto emit = [&](const uint64_t *a) {
-#pragma unroll
-            for (int q = 0; q < SL; ++q) {
-                const int i = 64 * q + lane;
-                if (i < K) {
-                    // a[q] is one of the K selected keys; an empty slot would be a
-                    // bug, reported as index -1 rather than read out of bounds
-                    const uint32_t j = vkey_index(a[q]);
-                    const bool ok = a[q] != 0 && int64_t(j) < V;
-                    if (top_idx) top_idx[row * K + i] = ok ? int64_t(j) : -1;
-                    float tv = -__builtin_huge_valf();
-                    const uint32_t hk = uint32_t(a[q] >> 32);
-                    if (ok && hk != 1u && hk != f32_key(0.0f)) {
-                        // the key's high word is the (transformed) value itself
-                        tv = key_f32(hk);
-                    } else if (ok) {
-                        // NaN and +-0 share a key per class: read the value back
-                        tv = float(SI::dec(L[row * ld + j]));
-                        if constexpr (TAIL) tv = vtail<SI>(tv, tail);
-                    }
-                    if (top_val) top_val[row * K + i] = tv;
-                }
-            }
-        };
+        auto emit = [&](const uint64_t *a) { emit_top<SI, TAIL, SL>(L, ld, V, K, row, a, top_idx, top_val, tail); };
 
-        // lse and argmax: fold the chunk partials; the largest chunk key is
-        // the row's first maximum
-        float M = -__builtin_huge_valf();
-        uint64_t ak = 0;
-        bool any = false;
-        auto fold_max = [&](const VPart &p) {
-            if (p.fin) {
-                M = p.m > M ? p.m : M;
-                any = true;
-            }
-            ak = p.top > ak ? p.top : ak;
-        };
-        if (pregs) {
-#pragma unroll
-            for (int k = 0; k < PPL; ++k) fold_max(pv[k]); // absent ones: fin 0, top 0
-        } else {
-            for (int cc = lane; cc < nch; cc += 64) fold_max(pr[cc]);
-        }
-        M = dpp_max(M);
-        ak = dpp_reduce(ak, uint64_t(0), [](uint64_t u, uint64_t v) { return u > v ? u : v; });
-        any = __builtin_amdgcn_ballot_w64(any) != 0;
-        // sum of l_c * e^(m_c - M): the f32 difference and hardware exp2 keep
-        // each term within a few ulp of f32, far inside the lse tolerance
-        double S = 0.0;
-        auto fold_sum = [&](const VPart &p) {
-            if (p.fin) S += p.l * double(__builtin_amdgcn_exp2f((p.m - M) * 1.44269504088896341f));
-        };
-        if (any) {
+        auto each_part = [&](auto f) {
             if (pregs) {
 #pragma unroll
-                for (int k = 0; k < PPL; ++k) fold_sum(pv[k]);
+                for (int k = 0; k < PPL; ++k) f(pv[k]); // absent ones: fin 0, top 0
             } else {
-                for (int cc = lane; cc < nch; cc += 64) fold_sum(pr[cc]);
+                for (int cc = lane; cc < nch; cc += 64) f(pr[cc]);
             }
-        }
-        S = dpp_sum(S);
-        if (lane == 0) {
-            if (lse) lse[row] = any ? double(M) + mgm::log(S) : -__builtin_huge_val();
-            // the scan starts at index 0: a NaN there is never beaten
-            if (amax) amax[row] = (x0 != x0 || ak == 0) ? 0 : int64_t(vkey_index(ak));
-        }
+        };
+        fold_row(each_part, x0, row, lse, amax);
         if (!want_top) return;
 
         if constexpr (FAST) {
@@ -732,6 +831,8 @@ namespace mg
             for (int i = 0; i < kBlk; ++i) c += uint32_t(b[i] >> 32) >= T ? 1 : 0;
             const int incl = wave_prefix_sum(c);
             const int ns = __builtin_amdgcn_readlane(incl, 63);
+            uint64_t R = 0; // the running top 64 keys, sorted
+            bool have = false;
             if (T != 0 && ns <= 128) {
                 const int off = incl - c;
 #pragma unroll
@@ -746,18 +847,42 @@ namespace mg
                 if (ns <= 64) {
                     uint64_t v1[1] = {v[0]};
                     wave_bitonic_desc<uint64_t, 1>(v1);
-                    v[0] = v1[0];
+                    R = v1[0];
                 } else {
                     wave_bitonic_desc<uint64_t, 2, true>(v);
+                    R = v[0];
                 }
-                const uint64_t kap = readlane64(v[0], K - 1);
-                if (__builtin_amdgcn_ballot_w64(pv[0].kd > kap) == 0) {
-                    emit(v);
-                    return;
+                have = true;
+            }
+            if (!have) {
+                // no usable T (fewer than K heads with keys, or too many
+                // survivors): all block keys, 64 at a time
+                for (int i0 = 0; i0 < nch * kBlk; i0 += 64) {
+                    uint64_t v[1] = {i0 + lane < nch * kBlk ? bk[i0 + lane] : 0};
+                    wave_bitonic<uint64_t, 1, false>(v);
+                    R = top64_merge(R, v[0]);
                 }
             }
-            wave_lds_sync(); // sel and hist are reused below
-            load_r();
+            // R holds the blocks' top 64 (or all of their keys). A chunk whose
+            // D-th key lies above R's K-th may hold more of the row's top K:
+            // it is re-read and its top K past the block merged in. Keys
+            // outside every block and list are then below R's K-th key.
+            uint64_t fail = __builtin_amdgcn_ballot_w64(lane < nch && pv[0].kd > readlane64(R, K - 1));
+            while (fail) {
+                const int cc = int(__builtin_ctzll(fail));
+                fail &= fail - 1;
+                const int64_t cb = int64_t(cc) * kVChunk;
+                const int nv = int(V - cb < kVChunk ? V - cb : kVChunk);
+                wave_lds_sync();
+                const int nk = chunk_topk<SI, VW, TAIL>(L + row * ld + cb, nv, K, tail, cb, sel, hist, hist + kCand);
+                // its keys past the first D (the block's), ascending
+                const int i = D + 63 - lane;
+                R = top64_merge(R, i < nk ? sel[i] : 0);
+                // R only grows: chunks it now proves need no re-read
+                fail &= __builtin_amdgcn_ballot_w64(lane < nch && pv[0].kd > readlane64(R, K - 1));
+            }
+            emit(&R);
+            return;
         }
 
         auto nvalid_of = [&](int cc) {
@@ -906,6 +1031,7 @@ namespace mg
         emit(a);
     }
 
+
     // The pass on `stream` with its partials in `work` (work_bytes long);
     // `room` names where they live for the error raised when they do not fit.
     static void vocab_pass(hipStream_t stream, void *work, int64_t work_bytes, const char *room, const void *logits,
@@ -925,12 +1051,14 @@ namespace mg
         if (rows == 0) return;
         const int nch = int((V + kVChunk - 1) / kVChunk);
         const int64_t nc = rows * nch;
-        const int64_t need_bytes = nc * int64_t(sizeof(VPart) + sizeof(uint64_t) * (kBlk + kMaxK));
+        // the blocks start 256-aligned after the partials (16-byte loads)
+        const int64_t part_bytes = (nc * int64_t(sizeof(VPart)) + 255) / 256 * 256;
+        const int64_t need_bytes = part_bytes + nc * int64_t(sizeof(uint64_t) * (kBlk + kMaxK));
         need(need_bytes <= work_bytes, "vocab_reduce: the partials of " + std::to_string(rows) + " rows x " +
                                            std::to_string(nch) + " chunks need " + std::to_string(need_bytes) +
                                            " bytes, more than " + room + " (" + std::to_string(work_bytes) + ")");
         VPart *part = static_cast<VPart *>(work);
-        uint64_t *blk = reinterpret_cast<uint64_t *>(part + nc);
+        uint64_t *blk = reinterpret_cast<uint64_t *>(static_cast<char *>(work) + part_bytes);
         uint64_t *lst = blk + nc * kBlk;
         const dim3 g1{unsigned(nch), unsigned(rows), 1u};
         const dim3 g2{unsigned(rows), 1u, 1u};

@@ -195,6 +195,30 @@ def test_vocab_merge_deep_chunk(prims):
     vocab_check(prims, O.from_f64(L, F32), F32, 64)
 
 
+@pytest.mark.parametrize("dt,K", ((F32, 64), (BF16, 64), (F32, 40), (F32, 17)))
+def test_vocab_clustered_low_ids(prims, dt, K):
+    """the top candidates concentrated in the first few thousand ids, as a
+    language model's frequent tokens are: the first chunks hold more than 16
+    of the top K, so their keys past the block are re-read and merged"""
+    L = O.to_f64(O.normal(25, (6, 201088), 0.0, 2.0, F32), F32)
+    L[0, :3000] += 9.0                          # 3000 strong low ids
+    L[1, 100:164] = 30.0 + np.arange(64) / 8.0  # the whole top 64 in chunk 0
+    L[2, ::4096] = 25.0                         # one winner per chunk (50 chunks)
+    L[3, :5000] = 20.0                          # a tie block across chunks 0 and 1
+    L[4, 4000:4200] += 12.0                     # a cluster straddling a chunk edge
+    L[5, :] = np.round(L[5] * 4) / 4            # coarse values: ties everywhere
+    L[5, :8192] += 6.0
+    vocab_check(prims, O.from_f64(L, dt), dt, K)
+
+
+@pytest.mark.parametrize("V", (4 * 4096 + 1, 16 * 4096 + 5, 64 * 4096))
+def test_vocab_short_last_chunk(prims, V):
+    """a last chunk with fewer keys than the merge takes heads from (its
+    missing heads leave no threshold: every block key is merged instead),
+    and the largest row the one-lane-per-chunk merge takes"""
+    vocab_check(prims, O.normal(26, (3, V), 0.0, 4.0, F32), F32, 64)
+
+
 def test_vocab_large_V(prims):
     """more chunks than the merge holds in registers (V = 300000)"""
     vocab_check(prims, O.normal(20, (3, 300000), 0.0, 4.0, F32), F32, 64)
