@@ -70,6 +70,8 @@ BYTES = {
     "attn_prefill_4096": 2 * T * Q_H * HD + 2 * 2 * T * K_H * HD + 4 * T * Q_H * HD,
     # a plain device copy (torch's copy kernel): the access-pattern ceiling the others are read against
     "copy_256MiB": 2 * (256 << 20),
+    # one 4-byte fill (torch's fill kernel): what the timing protocol itself costs for any single launch
+    "launch_floor": 4,
 }
 BYTES["softmax_causal_softcap30"] = BYTES["softmax_causal"]
 # matrix-core ops: q.k and p.v over the causal pairs, 2 * 2 * head_dim flops per (query, key)
@@ -92,6 +94,7 @@ KERNEL_OF = {
     "attn_prefill_4096": "k_attn_prefill<5,4,1,4>",
     "softmax_causal_softcap30": "k_softmax_fast<cap>",
     "copy_256MiB": "torch copy (memory-only probe)",
+    "launch_floor": "torch fill of one float (timing-protocol probe)",
 }
 
 
@@ -164,6 +167,7 @@ def make_inputs(torch, P):
     I["pout"] = torch.empty((T, Q_H, HD), dtype=torch.float32, device=dev)
     I["copy_src"] = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
     I["copy_dst"] = torch.empty_like(I["copy_src"])
+    I["one"] = torch.empty(1, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
     scale = 1.0 / math.sqrt(HD)
@@ -191,6 +195,7 @@ def make_inputs(torch, P):
         "qk_norm_rope_kv": lambda: P.qk_norm_rope(I["q"], I["k"], 1e-6, 3.87, I["cos"], I["sin"], None, 0, I["v"],
                                                   I["kcache"], I["vcache"]),
         "copy_256MiB": lambda: I["copy_dst"].copy_(I["copy_src"]),
+        "launch_floor": lambda: I["one"].zero_(),
     }
     for t in (1, 4, 16, 64):
         ops[f"residual_rmsnorm_T{t}"] = (lambda t=t: P.residual_rmsnorm(

@@ -26,10 +26,13 @@
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
 
+#include <type_traits>
+
 namespace mg
 {
     constexpr int kOrderedMaxDim = 128;
     constexpr int kOrderedRows = 32; // 8 lanes per row, 256 threads
+    constexpr int64_t kPrefetchRows = 256; // k_norm_tree requests w up front for at most this many rows
 
     MG_DEV double norm_out(int kind, double v, double rs, double w)
     {
@@ -113,7 +116,9 @@ namespace mg
         return t;
     }
 
-    template <class S, int VEC, int CPT>
+    // WPRE (few rows, where latency rules): w is requested with h and x, so
+    // the row costs one trip to memory instead of two
+    template <class S, int VEC, int CPT, bool WPRE>
     __global__ __launch_bounds__(1024) void k_norm_tree(int kind, typename S::raw *h,
                                                         const typename S::raw *__restrict__ x,
                                                         int64_t ldh, int64_t ldx,
@@ -131,6 +136,14 @@ namespace mg
         const int nchunk = dim / VEC;
 
         comp v[CPT][VEC];
+        Vec<raw, VEC> wpre[CPT];
+        if constexpr (WPRE) {
+#pragma unroll
+            for (int c = 0; c < CPT; ++c) {
+                const int ch = threadIdx.x + c * blockDim.x;
+                if (ch < nchunk && kind != 2) wpre[c] = *reinterpret_cast<const Vec<raw, VEC> *>(w + ch * VEC);
+            }
+        }
         double ss = 0.0;
 #pragma unroll
         for (int c = 0; c < CPT; ++c) {
@@ -159,7 +172,7 @@ namespace mg
             const int ch = threadIdx.x + c * blockDim.x;
             if (ch < nchunk) {
                 Vec<raw, VEC> wv;
-                if (kind != 2) wv = *reinterpret_cast<const Vec<raw, VEC> *>(w + ch * VEC);
+                if (kind != 2) wv = WPRE ? wpre[c] : *reinterpret_cast<const Vec<raw, VEC> *>(w + ch * VEC);
                 Vec<raw, VEC> o;
 #pragma unroll
                 for (int e = 0; e < VEC; ++e)
@@ -260,13 +273,20 @@ namespace mg
                                static_cast<raw *>(h), static_cast<const raw *>(x), ldh, ldx,
                                static_cast<const raw *>(w), eps, static_cast<raw *>(y), ldy, dim);
         };
-        switch (cpt) {
-        case 1: args(k_norm_tree<S, VEC, 1>); break;
-        case 2: args(k_norm_tree<S, VEC, 2>); break;
-        case 4: args(k_norm_tree<S, VEC, 4>); break;
-        case 8: args(k_norm_tree<S, VEC, 8>); break;
-        default: args(k_norm_tree<S, VEC, 16>); break;
-        }
+        auto pick = [&](auto wpre) {
+            constexpr bool P = decltype(wpre)::value;
+            switch (cpt) {
+            case 1: args(k_norm_tree<S, VEC, 1, P>); break;
+            case 2: args(k_norm_tree<S, VEC, 2, P>); break;
+            case 4: args(k_norm_tree<S, VEC, 4, P>); break;
+            case 8: args(k_norm_tree<S, VEC, 8, P>); break;
+            default: args(k_norm_tree<S, VEC, 16, P>); break;
+            }
+        };
+        if (rows <= kPrefetchRows)
+            pick(std::true_type{});
+        else
+            pick(std::false_type{});
         check_launch("k_norm_tree");
     }
 
