@@ -117,11 +117,19 @@ def test_split_ragged_and_masked(prims):
     check(y, ref, F32, visible(2, 3, 20000, O.MASK_WINDOW, 7000, 15000))
 
 
-def test_split_two_kernel_path(prims):
-    """more split work-groups than can be resident at once (1024 rows x 2
-    chunks): the two-kernel path instead of the one-read cooperative one"""
+def test_split_many_rows(prims):
+    """many split rows at once (1024 rows x 2 chunks): more work-groups than
+    the device holds at a time"""
     y, ref = run(prims, 8, 128, 6000, q_pos0=5872)
     check(y, ref, BF16, visible(8, 128, 6000, O.MASK_CAUSAL, 0, 5872))
+
+
+def test_split_repeat(prims):
+    """split calls of different row counts and lengths in a row share the
+    partials area: each gives the results a fresh call gives"""
+    for heads, kc in ((40, 131072), (3, 9000), (40, 131072), (7, 70000), (3, 9000)):
+        y, ref = run(prims, heads, 1, kc, q_pos0=kc - 1, seed=heads + kc)
+        check(y, ref, BF16, visible(heads, 1, kc, O.MASK_CAUSAL, 0, kc - 1))
 
 
 def test_split_two_kernel_nonfinite(prims):
