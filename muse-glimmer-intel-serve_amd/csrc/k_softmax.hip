@@ -685,7 +685,7 @@ namespace mg
         a.ldy = ldy;
         a.scale = float(scale);
         a.cap = float(softcap);
-        a.rcap = a.cap != 0.0f ? float(1.0 / double(a.cap)) : 0.0f;
+        a.rcap = a.cap != 0.0f ? recip_rn(a.cap) : 0.0f;
         a.mask = mask;
         a.window = window;
         a.q_pos0 = q_pos0;
