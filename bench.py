@@ -72,6 +72,11 @@ BYTES = {
     "copy_256MiB": 2 * (256 << 20),
     # one 4-byte fill (torch's fill kernel): what the timing protocol itself costs for any single launch
     "launch_floor": 4,
+    # the library's stream probes (mg_probe_stream): the primitives' access pattern with no arithmetic
+    "probe_copy_256MiB": 2 * (256 << 20),
+    "probe_read_256MiB": 256 << 20,
+    "probe_write_256MiB": 256 << 20,
+    "probe_2r2w_norm_shape": 4 * 2 * T * D,
 }
 BYTES["softmax_causal_softcap30"] = BYTES["softmax_causal"]
 # matrix-core ops: q.k and p.v over the causal pairs, 2 * 2 * head_dim flops per (query, key)
@@ -95,6 +100,10 @@ KERNEL_OF = {
     "softmax_causal_softcap30": "k_softmax_fast<cap>",
     "copy_256MiB": "torch copy (memory-only probe)",
     "launch_floor": "torch fill of one float (timing-protocol probe)",
+    "probe_copy_256MiB": "k_probe<0> (copy)",
+    "probe_read_256MiB": "k_probe<1> (read)",
+    "probe_write_256MiB": "k_probe<2> (write)",
+    "probe_2r2w_norm_shape": "k_probe<3> (2 reads + 2 writes, the residual_rmsnorm traffic)",
 }
 
 
@@ -168,6 +177,8 @@ def make_inputs(torch, P):
     I["copy_src"] = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
     I["copy_dst"] = torch.empty_like(I["copy_src"])
     I["one"] = torch.empty(1, dtype=torch.float32, device=dev)
+    for name in ("pa", "pc", "pd"):  # the norm-shaped probe's own [T, D] bf16 buffers
+        I[name] = torch.zeros((T, D), dtype=bf, device=dev)
     torch.cuda.synchronize()
 
     scale = 1.0 / math.sqrt(HD)
@@ -196,6 +207,10 @@ def make_inputs(torch, P):
                                                   I["kcache"], I["vcache"]),
         "copy_256MiB": lambda: I["copy_dst"].copy_(I["copy_src"]),
         "launch_floor": lambda: I["one"].zero_(),
+        "probe_copy_256MiB": lambda: P.probe_stream(P.PROBE_COPY, I["copy_src"], I["copy_dst"]),
+        "probe_read_256MiB": lambda: P.probe_stream(P.PROBE_READ, I["copy_src"], I["one"]),
+        "probe_write_256MiB": lambda: P.probe_stream(P.PROBE_WRITE, None, I["copy_dst"]),
+        "probe_2r2w_norm_shape": lambda: P.probe_stream(P.PROBE_2R2W, I["pa"], None, I["pc"], I["pd"]),
     }
     for t in (1, 4, 16, 64):
         ops[f"residual_rmsnorm_T{t}"] = (lambda t=t: P.residual_rmsnorm(
@@ -223,16 +238,22 @@ def time_op(torch, fn, reps, flush):
 
 
 def read_traffic(path, kernel):
-    """Measured HBM bytes per launch for `kernel` from the rocprofv3 PMC summary, or None."""
+    """Measured HBM bytes per launch for `kernel` from the rocprofv3 PMC summary:
+    the line naming it exactly (template arguments included), else the one line
+    whose name starts with it; None when absent or ambiguous."""
+    rows = {}
     try:
         with open(path) as f:
             for line in f:
                 parts = line.split()
-                if len(parts) >= 3 and parts[0] == kernel and not line.startswith("#"):
-                    return int(float(parts[1]) + float(parts[2]))
+                if len(parts) >= 3 and not line.startswith("#"):
+                    rows[parts[0]] = int(float(parts[1]) + float(parts[2]))
     except OSError:
-        pass
-    return None
+        return None
+    if kernel in rows:
+        return rows[kernel]
+    hits = [v for k, v in rows.items() if k.startswith(kernel + "<")]
+    return hits[0] if len(hits) == 1 else None
 
 
 def host_isa():

@@ -240,6 +240,14 @@ int mg_quantize_q8_0(mg_ctx *ctx, const uint16_t *w, int64_t rows, int64_t in, i
 int mg_gemv_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, const uint16_t *x, int64_t batch, int64_t rows,
                  int64_t in, int64_t ldx, float *y, int64_t ldy, int blockdot);
 
+/* HBM stream probe: NO COUNTERPART in the reference; a measurement aid that
+ * moves `bytes` (a multiple of 16) through the primitives' access pattern
+ * (16-byte non-temporal loads and stores, one-shot grid) with no arithmetic:
+ * kind 0 copies a to b; 1 reads a (b receives at most one word); 2 writes b;
+ * 3 reads a and c and writes a = a + c and d = (a + c) ^ c, 32-bit words (the
+ * residual-add + RMSNorm traffic shape). Buffers 16-byte aligned. */
+int mg_probe_stream(mg_ctx *ctx, int kind, void *a, void *b, const void *c, void *d, int64_t bytes);
+
 /* Per row of logits [rows, V] (dtype_in f32 or bf16; row r at logits + r * ld,
  * ld the row stride in elements, 0 = V), one fused pass:
  *   lse[r]     = m + log(sum exp(x - m)) over finite entries, m their max

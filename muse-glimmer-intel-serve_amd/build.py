@@ -23,7 +23,7 @@ OBJ = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
 SOURCES = ["mg_api.cpp", "k_norm.hip", "k_elementwise.hip", "k_rope.hip", "k_qk.hip", "k_softmax.hip", "k_softmax64.hip",
-           "k_q8.hip", "k_vocab.hip", "k_sample.hip", "k_attn.hip", "k_attn_prefill.hip"]
+           "k_q8.hip", "k_vocab.hip", "k_sample.hip", "k_attn.hip", "k_attn_prefill.hip", "k_probe.hip"]
 
 FLAGS = [
     "-x", "hip", f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",

@@ -261,6 +261,14 @@ int mg_dequant_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, void *out,
     });
 }
 
+int mg_probe_stream(mg_ctx *ctx, int kind, void *a, void *b, const void *c, void *d, int64_t bytes)
+{
+    MG_GUARD(-1, {
+        mg::launch_probe(ctx_of(ctx), kind, a, b, c, d, bytes);
+        return 0;
+    });
+}
+
 int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t V, int dtype_in,
                     int64_t K, double *lse, int64_t *argmax, int64_t *top_idx, float *top_val)
 {

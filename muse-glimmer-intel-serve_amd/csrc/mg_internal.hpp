@@ -118,6 +118,8 @@ namespace mg
     // the vocab pass without a context: partials in a fixed device array of
     // kVocabScratchBytes (k_vocab.hip), on `stream` of the current device
     constexpr int64_t kVocabScratchBytes = int64_t(16) << 20;
+    // HBM stream probes (k_probe.hip): kind 0 copy, 1 read, 2 write, 3 2r2w
+    void launch_probe(mg_ctx *ctx, int kind, void *a, void *b, const void *c, void *d, int64_t bytes);
     void launch_vocab_noalloc(hipStream_t stream, const void *logits, int64_t ld, int64_t rows, int64_t V,
                               int dt_in, int64_t K, double *lse, int64_t *amax, int64_t *top_idx, float *top_val);
 } // namespace mg

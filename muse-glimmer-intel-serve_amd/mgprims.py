@@ -64,6 +64,7 @@ _SIGS = {
     "mg_sample_dist": ([_P, _P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P], _INT),
     "mg_vocab_reduce_tail": ([_P, _P, _I, _I, _I, _INT, _D, _D, _I, _P, _P, _P, _P, _P], _INT),
     "mg_vocab_reduce_noalloc": ([_P, _P, _I, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
+    "mg_probe_stream": ([_P, _INT, _P, _P, _P, _P, _I], _INT),
 }
 
 _lib = None
@@ -456,6 +457,27 @@ class Prims:
         rc = self.lib.mg_vocab_reduce_noalloc(ctypes.c_void_p(s), _ptr(logits), ld, rows, V, _dtype_code(logits), K,
                                               _ptr(lse), _ptr(argmax), _ptr(top_idx), _ptr(top_val))
         self._check(rc)
+
+    PROBE_COPY, PROBE_READ, PROBE_WRITE, PROBE_2R2W = 0, 1, 2, 3
+
+    def probe_stream(self, kind, a=None, b=None, c=None, d=None):
+        """HBM stream probe (a measurement aid, no reference counterpart): kind
+        PROBE_COPY b = a, PROBE_READ reads a (b: a sink of >= 4 bytes),
+        PROBE_WRITE fills b, PROBE_2R2W a = a + c and d = (a + c) ^ c over
+        32-bit words. The moved size is the first operand's byte count; the
+        others must hold as many bytes (contiguous, 16-byte aligned)."""
+        ts = [t for t in (a, b, c, d) if t is not None]
+        self._dev(*ts)
+        self._contig("probe_stream", *ts)
+        first = a if kind != self.PROBE_WRITE else b
+        if first is None:
+            raise MgError("probe_stream: missing operand")
+        nbytes = first.numel() * first.element_size()
+        for t in ts:
+            if t is not b or kind != self.PROBE_READ:
+                if t.numel() * t.element_size() < nbytes:
+                    raise MgError("probe_stream: operands smaller than the moved size")
+        self._check(self.lib.mg_probe_stream(self.h, kind, _ptr(a), _ptr(b), _ptr(c), _ptr(d), nbytes))
 
     def sample_dist(self, top_idx, top_val, argmax, temperature, top_p, min_p, ids=None, probs=None, n=None):
         """serve/sampler.py's candidate distribution (ids, probs, count per row) from a vocab pass.
