@@ -84,9 +84,10 @@ FLOPS = {"attn_prefill_4096": Q_H * (T * (T + 1) // 2) * 4 * HD}
 PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 STEP_OPS = ("residual_rmsnorm", "swiglu", "softmax_causal")
 KERNEL_OF = {
-    "residual_rmsnorm": "k_norm_tree",
-    "swiglu": "k_gate_lut",
-    "softmax_causal": "k_softmax_fast",
+    # the step ops name their kernel as the traffic summary does (template arguments included)
+    "residual_rmsnorm": "k_norm_tree<mg::SBf16,8,2,false>",
+    "swiglu": "k_gate_lut<mg::SBf16>",
+    "softmax_causal": "k_softmax_fast<mg::SBf16,4,false,true>",
     "rope": "k_rope",
     "softmax_decode": "k_softmax_partial_fast + k_softmax_finish_fast",
     "dequant_q8_0": "k_dequant_q8_0",
