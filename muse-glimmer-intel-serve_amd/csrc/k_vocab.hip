@@ -1032,6 +1032,24 @@ namespace mg
     }
 
 
+    // The output tail alone: out[r, j] = vtail(in[r, j]) at storage, one
+    // 16-byte vector per thread (grid: vectors of a row x rows). Run ahead of
+    // the vocab pass when the transformed logits have somewhere to go, so the
+    // pass's chunk kernel does not carry the tail's registers.
+    template <class SI, int VW>
+    __global__ __launch_bounds__(256) void k_vocab_tail_map(const typename SI::raw *__restrict__ in, int64_t ld,
+                                                            typename SI::raw *__restrict__ out, int64_t V, VTail t)
+    {
+        using raw = typename SI::raw;
+        const int64_t row = blockIdx.y;
+        const int64_t j = (int64_t(blockIdx.x) * 256 + threadIdx.x) * VW;
+        if (j >= V) return;
+        Vec<raw, VW> v = ld16_stream<raw, VW>(in + row * ld + j);
+#pragma unroll
+        for (int e = 0; e < VW; ++e) v.v[e] = SI::enc32(vtail<SI>(float(SI::dec(v.v[e])), t));
+        st16_stream<raw, VW>(out + row * V + j, v);
+    }
+
     // The pass on `stream` with its partials in `work` (work_bytes long);
     // `room` names where they live for the error raised when they do not fit.
     static void vocab_pass(hipStream_t stream, void *work, int64_t work_bytes, const char *room, const void *logits,
@@ -1057,6 +1075,32 @@ namespace mg
         need(need_bytes <= work_bytes, "vocab_reduce: the partials of " + std::to_string(rows) + " rows x " +
                                            std::to_string(nch) + " chunks need " + std::to_string(need_bytes) +
                                            " bytes, more than " + room + " (" + std::to_string(work_bytes) + ")");
+        // The tail as its own elementwise pass (k_vocab_tail_map) wherever its
+        // output has somewhere to go — logits_out, else room in the workspace
+        // past the partials — then the plain pass over the transformed logits:
+        // the same values (vtail in both), without the tail's registers in the
+        // chunk kernel. Otherwise the chunk kernel applies the tail itself.
+        if (tail_on && (dt_in == F32 || dt_in == BF16)) {
+            const int64_t esz = dt_in == F32 ? 4 : 2, vw = 16 / esz;
+            const int64_t tmp_off = (need_bytes + 255) / 256 * 256;
+            void *dst = logits_out ? logits_out
+                                   : (tmp_off + rows * V * esz <= work_bytes ? static_cast<char *>(work) + tmp_off
+                                                                              : nullptr);
+            if (dst && V % vw == 0 && ld % vw == 0 && aligned16(logits) && aligned16(dst)) {
+                const VTail t{float(mult), float(cap), nullptr};
+                const dim3 gm{unsigned((V / vw + 255) / 256), unsigned(rows), 1u};
+                if (dt_in == F32)
+                    hipLaunchKernelGGL((k_vocab_tail_map<SF32, 4>), gm, dim3(256), 0, stream,
+                                       static_cast<const float *>(logits), ld, static_cast<float *>(dst), V, t);
+                else
+                    hipLaunchKernelGGL((k_vocab_tail_map<SBf16, 8>), gm, dim3(256), 0, stream,
+                                       static_cast<const uint16_t *>(logits), ld, static_cast<uint16_t *>(dst), V, t);
+                check_launch("k_vocab_tail_map");
+                vocab_pass(stream, work, tmp_off, room, dst, V, rows, V, dt_in, K, lse, amax, top_idx, top_val, false,
+                           1.0, 0.0, nullptr);
+                return;
+            }
+        }
         VPart *part = static_cast<VPart *>(work);
         uint64_t *blk = reinterpret_cast<uint64_t *>(static_cast<char *>(work) + part_bytes);
         uint64_t *lst = blk + nc * kBlk;

@@ -252,3 +252,27 @@ def test_vocab_tail_fused(prims, dt, mult, cap, std):
     assert np.array_equal(am.cpu().numpy(), r_am)
     assert np.array_equal(ti.cpu().numpy(), r_ti)
     assert np.array_equal(tv.cpu().numpy().astype(np.float64), r_tv)
+
+
+@pytest.mark.parametrize("rows,V,out", ((4, 50001, True), (4, 50001, False), (90, 201088, False)))
+def test_vocab_tail_fused_in_the_pass(prims, rows, V, out):
+    """the tail applied inside the vocab pass's chunk kernel, where it cannot run
+    as its own pass first: a row length that is not a multiple of the 16-byte
+    vector, and (no logits_out) 90 rows whose transformed logits do not fit
+    beside the partials in the default workspace"""
+    import torch
+    Ls = O.normal(27, (rows, V), 0.0, 8.0, F32)
+    L = O.to_f64(Ls, F32)
+    Z = O.softcap(L, 1.0, 30.0, F32)
+    dL = to_dev(Ls, F32)
+    o = torch.empty_like(dL) if out else None
+    lse, am, ti, tv = prims.vocab_reduce_tail(dL, 1.0, 30.0, 64, o)
+    if out:
+        assert same_bits(from_dev(o, F32), O.from_f64(Z, F32))
+    r_lse, r_am, r_ti, r_tv = O.vocab_reduce(Z, 64)
+    rel = np.abs(lse.cpu().numpy() - r_lse) / np.abs(r_lse)
+    assert rel.max() <= 1e-6
+    assert np.array_equal(am.cpu().numpy(), r_am)
+    assert np.array_equal(ti.cpu().numpy(), r_ti)
+    assert np.array_equal(tv.cpu().numpy().astype(np.float64), r_tv)
+
