@@ -30,6 +30,7 @@ namespace mg
 {
     constexpr int kQkRows = 32;    // head rows per work-group
     constexpr int kQkWaveRows = 8; // head rows per wave (eight lanes per row for mean_sq)
+    constexpr int kQkPieces = 1;   // k_qk_pairs: 8-element pieces per lane in each half of a row
 
     struct QkArgs
     {
@@ -226,17 +227,18 @@ namespace mg
         }
     }
 
-    // 16-bit storage with head_dim 64, 128 or 256: RoPE's layout, one lane per
-    // 8-element piece of the first half and the matching piece of the second
-    // (TPR = head_dim / 16 lanes per head row), no LDS on the common path.
-    // Sum of squares: the square of a p-bit value is exact in f64, and when
-    // the row's nonzero magnitudes span few enough binades, 2 (emax - emin) +
-    // ceil(log2 D) + 2p <= 53, every partial sum in any order is exact (all
-    // are multiples of the smallest square's last bit and below 2^53 of it), so
-    // a butterfly over the row's lanes gives mean_sq's bits. A wave with a row
-    // outside that range (or holding inf or NaN) stages its rows in LDS and
-    // runs mean_sq's own order (eight interleaved accumulators, fixed tree).
-    template <class S, int TPR>
+    // 16-bit storage with head_dim 64, 128 or 256: RoPE's layout, each lane
+    // holding NV 8-element pieces of the first half and the matching pieces of
+    // the second (TPR = head_dim / (16 NV) lanes per head row), no LDS on the
+    // common path; more elements per lane spread the per-row work (the
+    // reduction, rs, addresses) over more of them.
+    // Sum of squares: the square of a stored value is exact in f64 and a
+    // multiple of the smallest nonzero square's last bit u; when the sum stays
+    // below 2^53 u every partial sum in any order is exact, so a butterfly over
+    // the row's lanes gives mean_sq's bits. A wave with a row outside that
+    // bound (or holding inf or NaN) stages its rows in LDS and runs mean_sq's
+    // own order (eight interleaved accumulators, fixed tree).
+    template <class S, int D, int NV>
     __global__ __launch_bounds__(256) void k_qk_pairs(typename S::raw *q, typename S::raw *k,
                                                       const typename S::raw *__restrict__ v, QkArgs a,
                                                       typename S::comp qs,
@@ -246,11 +248,11 @@ namespace mg
                                                       typename S::raw *vc)
     {
         using raw = typename S::raw;
-        constexpr int VEC = 8, D = 16 * TPR, half = D / 2, RPW = 64 / TPR;
-        constexpr int LOG2D = TPR == 4 ? 6 : TPR == 8 ? 7 : 8;
+        using W4 = Vec<uint32_t, 4>;
+        constexpr int VEC = 8, TPR = D / (16 * NV), half = D / 2, RPW = 64 / TPR, NH = NV * VEC;
         constexpr int MB = S::dt == BF16 ? 7 : 10;              // stored mantissa bits
-        constexpr int EALL = S::dt == BF16 ? 0xff : 0x1f;       // inf / NaN exponent field
-        constexpr int SPAN = (53 - LOG2D - 2 * (MB + 1)) / 2;   // binades the exact sum allows
+        constexpr int BIAS = S::dt == BF16 ? 127 : 15;          // exponent bias
+        static_assert(TPR >= 2 && TPR <= 16 && TPR * 16 * NV == D, "lanes per row");
         __shared__ __align__(16) raw st[4][RPW][D + 8];
         __shared__ double rsf[4][RPW];
         const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -265,43 +267,78 @@ namespace mg
         const int hh = int(rc - t * heads);
         const bool isq = hh < a.nq;
         raw *x = isq ? q + t * a.ldq + int64_t(hh) * D : k + t * a.ldk + int64_t(hh - a.nq) * D;
-        Vec<raw, VEC> lo = ldv<raw, VEC>(x + VEC * j);
-        Vec<raw, VEC> hi = ldv<raw, VEC>(x + half + VEC * j);
-        const int64_t p = pos ? pos[t] : a.pos0 + t;
-
-        double ss = 0.0;
-        int emin = 0x7fff, emax = 0;
+        const int c0 = NH * j; // the lane's first column of each half
+        Vec<raw, VEC> lo[NV], hi[NV];
 #pragma unroll
-        for (int e = 0; e < 2 * VEC; ++e) {
-            const raw b = e < VEC ? lo.v[e] : hi.v[e - VEC];
-            const double d = double(S::dec(b));
-            ss += d * d;
-            const int u = b & 0x7fff, ef = u >> MB;
-            if (u) {
-                emin = min(emin, ef > 1 ? ef : 1);
-                emax = max(emax, ef);
+        for (int i = 0; i < NV; ++i) {
+            lo[i] = ldv<raw, VEC>(x + c0 + VEC * i);
+            hi[i] = ldv<raw, VEC>(x + half + c0 + VEC * i);
+        }
+        const int64_t p = pos ? pos[t] : a.pos0 + t;
+        Vec<raw, VEC> vlo[NV], vhi[NV];
+        if (!isq && vc && p >= 0) {
+            const raw *vr = v + t * a.ldv + int64_t(hh - a.nq) * D + c0;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                vlo[i] = ldv<raw, VEC>(vr + VEC * i);
+                vhi[i] = ldv<raw, VEC>(vr + half + VEC * i);
             }
         }
-        // over the row's TPR lanes (a quad, half-row or row of the DPP
-        // network); the sum is exact in any order when it is used
+        const bool rot = co && p >= 0 && p < a.table_rows;
+        Vec<raw, VEC> cv[NV], sv[NV];
+        if (rot) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                cv[i] = *reinterpret_cast<const Vec<raw, VEC> *>(co + p * half + c0 + VEC * i);
+                sv[i] = *reinterpret_cast<const Vec<raw, VEC> *>(si + p * half + c0 + VEC * i);
+            }
+        }
+
+        double ss = 0.0;
+#pragma unroll
+        for (int e = 0; e < 2 * NH; ++e) {
+            const double d = double(S::dec(e < NH ? lo[e / VEC].v[e % VEC] : hi[(e - NH) / VEC].v[e % VEC]));
+            ss = __builtin_fma(d, d, ss); // d * d is exact: the same sum as ss + d * d
+        }
+        // smallest nonzero magnitude over the lane's values, two halves per
+        // packed step (zero wraps to 0xFFFF; an all-zero lane ends at
+        // 0x10000 >> MB, above every exponent field)
+        uint32_t umin = 0xffffffffu;
+#pragma unroll
+        for (int w = 0; w < 8 * NV; ++w) {
+            const uint32_t m =
+                (w < 4 * NV ? __builtin_bit_cast(W4, lo[w / 4]).v[w % 4] : __builtin_bit_cast(W4, hi[w / 4 - NV]).v[w % 4]) &
+                0x7fff7fffu;
+            umin = pk_min_u16(umin, pk_dec_u16(m));
+        }
+        int emin = max(int((min(umin & 0xffffu, umin >> 16) + 1) >> MB), 1);
+        // over the row's TPR lanes (a lane pair, quad, half-row or row of the
+        // DPP network); the sum is exact in any order when it is used
         auto step = [&](auto mov) {
             ss += mov(ss);
             emin = min(emin, mov(emin));
-            emax = max(emax, mov(emax));
         };
         step([](auto v) { return dpp_mov<0xB1, 0xf>(v, v); }); // quad_perm [1,0,3,2]
-        step([](auto v) { return dpp_mov<0x4E, 0xf>(v, v); }); // quad_perm [2,3,0,1]
+        if constexpr (TPR >= 4) step([](auto v) { return dpp_mov<0x4E, 0xf>(v, v); }); // quad_perm [2,3,0,1]
         if constexpr (TPR >= 8) step([](auto v) { return dpp_mov<0x141, 0xf>(v, v); }); // row_half_mirror
         if constexpr (TPR >= 16) step([](auto v) { return dpp_mov<0x140, 0xf>(v, v); }); // row_mirror
-        const bool exact = emax == 0 || (emax < EALL && emax - emin <= SPAN);
+        // every square is a multiple of u = 2^(2 (emin - bias - MB)), and so is
+        // every partial sum, which is then exact while below 2^53 u. A sum of
+        // at most 256 squares computed with any roundings is more than half
+        // the exact one, so ss <= 2^52 u bounds the exact sum below 2^53 u;
+        // inf and NaN fail the comparison
+        const bool exact = ss <= __builtin_ldexp(1.0, 52 + 2 * (emin - BIAS - MB));
         double rs;
         if (__builtin_amdgcn_ballot_w64(!exact) == 0) {
             rs = 1.0 / __builtin_sqrt(ss / double(D) + a.eps);
         } else {
             // mean_sq's order (src/muse_glimmer.hpp:509-527) over the wave's rows
             raw *sr = st[wv][lane / TPR];
-            *reinterpret_cast<Vec<raw, VEC> *>(sr + VEC * j) = lo;
-            *reinterpret_cast<Vec<raw, VEC> *>(sr + half + VEC * j) = hi;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                *reinterpret_cast<Vec<raw, VEC> *>(sr + c0 + VEC * i) = lo[i];
+                *reinterpret_cast<Vec<raw, VEC> *>(sr + half + c0 + VEC * i) = hi[i];
+            }
             wave_lds_sync();
             for (int rw = lane >> 3; rw < RPW; rw += 8) {
                 const int l = lane & 7;
@@ -319,58 +356,87 @@ namespace mg
             rs = rsf[wv][lane / TPR];
         }
 
-        const bool rot = co && p >= 0 && p < a.table_rows;
-        Vec<raw, VEC> cv, sv;
-        if (rot) {
-            cv = *reinterpret_cast<const Vec<raw, VEC> *>(co + p * half + VEC * j);
-            sv = *reinterpret_cast<const Vec<raw, VEC> *>(si + p * half + VEC * j);
-        }
         if constexpr (S::dt == BF16) {
-            // NaN propagates through every step and the twin's NaN is the one
-            // pattern 0x7FC0: the steps round without NaN checks and the
-            // outputs are made canonical once
-            auto rn = [](float f) { return SBf16::enc_finite(f); };
+            // every intermediate is held as the f32 of its bf16 value (one
+            // conversion per rounding) and the last rounding packs two
+            // elements per word. NaN propagates through every step and the
+            // twin's NaN is the one pattern 0x7FC0: the steps round without
+            // NaN checks and a lane whose outputs hold a NaN makes them
+            // canonical once
+            float fl[NH], fh[NH];
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                raw l = rn(float(double(S::dec(lo.v[e])) * rs));
-                raw h = rn(float(double(S::dec(hi.v[e])) * rs));
+            for (int e = 0; e < NH; ++e) {
+                fl[e] = bf_round(float(double(S::dec(lo[e / VEC].v[e % VEC])) * rs));
+                fh[e] = bf_round(float(double(S::dec(hi[e / VEC].v[e % VEC])) * rs));
                 if (isq) {
-                    l = rn(S::dec(l) * qs);
-                    h = rn(S::dec(h) * qs);
+                    fl[e] = bf_round(fl[e] * qs);
+                    fh[e] = bf_round(fh[e] * qs);
                 }
-                if (rot) {
-                    const float fl = S::dec(l), fh = S::dec(h), cc = S::dec(cv.v[e]), sn = S::dec(sv.v[e]);
-                    l = rn(S::dec(rn(fl * cc)) + S::dec(rn(-(fh * sn))));
-                    h = rn(S::dec(rn(fh * cc)) + S::dec(rn(fl * sn)));
+            }
+            if (rot) {
+#pragma unroll
+                for (int e = 0; e < NH; ++e) {
+                    const uint32_t cw = __builtin_bit_cast(W4, cv[e / VEC]).v[(e % VEC) / 2];
+                    const uint32_t sw = __builtin_bit_cast(W4, sv[e / VEC]).v[(e % VEC) / 2];
+                    const float cc = e & 1 ? bf_hi(cw) : bf_lo(cw), sn = e & 1 ? bf_hi(sw) : bf_lo(sw);
+                    const float l = fl[e], h = fh[e];
+                    fl[e] = bf_round(l * cc) + bf_round(-(h * sn)); // rounded by the packing below
+                    fh[e] = bf_round(h * cc) + bf_round(l * sn);
                 }
-                lo.v[e] = S::dec(l) != S::dec(l) ? raw(0x7fc0) : l;
-                hi.v[e] = S::dec(h) != S::dec(h) ? raw(0x7fc0) : h;
+            }
+            W4 l4[NV], h4[NV];
+            uint32_t mag = 0;
+#pragma unroll
+            for (int w = 0; w < 4 * NV; ++w) {
+                const uint32_t lw = bf_pack(fl[2 * w], fl[2 * w + 1]), hw = bf_pack(fh[2 * w], fh[2 * w + 1]);
+                l4[w / 4].v[w % 4] = lw;
+                h4[w / 4].v[w % 4] = hw;
+                mag = pk_max_u16(mag, pk_max_u16(lw & 0x7fff7fffu, hw & 0x7fff7fffu));
+            }
+            if (max(mag & 0xffffu, mag >> 16) > 0x7f80u) {
+#pragma unroll
+                for (int w = 0; w < 4 * NV; ++w) {
+                    l4[w / 4].v[w % 4] = bf_canon(l4[w / 4].v[w % 4]);
+                    h4[w / 4].v[w % 4] = bf_canon(h4[w / 4].v[w % 4]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                lo[i] = __builtin_bit_cast(Vec<raw, VEC>, l4[i]);
+                hi[i] = __builtin_bit_cast(Vec<raw, VEC>, h4[i]);
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                raw l = S::enc64(double(S::dec(lo.v[e])) * rs);
-                raw h = S::enc64(double(S::dec(hi.v[e])) * rs);
+            for (int e = 0; e < NH; ++e) {
+                raw &lr = lo[e / VEC].v[e % VEC], &hr = hi[e / VEC].v[e % VEC];
+                raw l = S::enc64(double(S::dec(lr)) * rs);
+                raw h = S::enc64(double(S::dec(hr)) * rs);
                 if (isq) {
                     l = S::enc(S::dec(l) * qs);
                     h = S::enc(S::dec(h) * qs);
                 }
-                if (rot) rope_pair<S>(l, h, cv.v[e], sv.v[e]);
-                lo.v[e] = l;
-                hi.v[e] = h;
+                if (rot) rope_pair<S>(l, h, cv[e / VEC].v[e % VEC], sv[e / VEC].v[e % VEC]);
+                lr = l;
+                hr = h;
             }
         }
         if (!live) return;
-        stv<raw, VEC>(x + VEC * j, lo);
-        stv<raw, VEC>(x + half + VEC * j, hi);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            stv<raw, VEC>(x + c0 + VEC * i, lo[i]);
+            stv<raw, VEC>(x + half + c0 + VEC * i, hi[i]);
+        }
         if (!isq && kc && p >= 0) {
-            const int64_t o = (p % a.slots) * (a.nkv * D) + int64_t(hh - a.nq) * D + VEC * j;
-            stv<raw, VEC>(kc + o, lo);
-            stv<raw, VEC>(kc + o + half, hi);
-            if (vc) {
-                const raw *vr = v + t * a.ldv + int64_t(hh - a.nq) * D + VEC * j;
-                stv<raw, VEC>(vc + o, ldv<raw, VEC>(vr));
-                stv<raw, VEC>(vc + o + half, ldv<raw, VEC>(vr + half));
+            const int64_t slot = p < a.slots ? p : p % a.slots;
+            const int64_t o = slot * (a.nkv * D) + int64_t(hh - a.nq) * D + c0;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                stv<raw, VEC>(kc + o + VEC * i, lo[i]);
+                stv<raw, VEC>(kc + o + half + VEC * i, hi[i]);
+                if (vc) {
+                    stv<raw, VEC>(vc + o + VEC * i, vlo[i]);
+                    stv<raw, VEC>(vc + o + half + VEC * i, vhi[i]);
+                }
             }
         }
     }
@@ -398,7 +464,7 @@ namespace mg
         };
         if constexpr (sizeof(raw) == 2) {
             if (vec && (a.D == 64 || a.D == 128 || a.D == 256)) {
-                const int tpr = a.D / 16;
+                const int tpr = a.D / (16 * kQkPieces);
                 need(rows * tpr / 256 < (int64_t(1) << 31), "qk_norm_rope: too many rows");
                 const unsigned pblocks = unsigned((rows * tpr + 255) / 256);
                 auto gp = [&](auto kern) {
@@ -407,12 +473,12 @@ namespace mg
                                        static_cast<const raw *>(co), static_cast<const raw *>(si), pos,
                                        static_cast<raw *>(kc), static_cast<raw *>(vc));
                 };
-                if (tpr == 4)
-                    gp(k_qk_pairs<S, 4>);
-                else if (tpr == 8)
-                    gp(k_qk_pairs<S, 8>);
+                if (a.D == 64)
+                    gp(k_qk_pairs<S, 64, kQkPieces>);
+                else if (a.D == 128)
+                    gp(k_qk_pairs<S, 128, kQkPieces>);
                 else
-                    gp(k_qk_pairs<S, 16>);
+                    gp(k_qk_pairs<S, 256, kQkPieces>);
                 check_launch("k_qk_pairs");
                 return;
             }

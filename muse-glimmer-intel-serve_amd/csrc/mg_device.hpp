@@ -220,6 +220,63 @@ namespace mg
         }
     }
 
+    // ------------------------------------------------- packed 16-bit pairs
+    // Two 16-bit values in one 32-bit word, element 0 in the low half: the
+    // bf16 steps round two results with one v_cvt_pk_bf16_f32, and the
+    // magnitude bounds take two halves per v_pk_max_u16 / v_pk_min_u16.
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    MG_DEV uint32_t pk_max_u16(uint32_t a, uint32_t b)
+    {
+        return __builtin_bit_cast(uint32_t,
+                                  __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+    }
+    MG_DEV uint32_t pk_min_u16(uint32_t a, uint32_t b)
+    {
+        return __builtin_bit_cast(uint32_t,
+                                  __builtin_elementwise_min(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+    }
+    // each half minus one, modulo 2^16 (zero becomes 0xFFFF)
+    MG_DEV uint32_t pk_dec_u16(uint32_t a)
+    {
+        return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - u16x2{1, 1});
+    }
+    MG_DEV float bf_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+    MG_DEV float bf_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+    // RNE of two f32 values into one word; a NaN stays a NaN of the
+    // conversion's own pattern (bf_canon makes it 0x7FC0)
+    MG_DEV uint32_t bf_pack(float a, float b)
+    {
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+        const f2 v = {opaque(a), opaque(b)};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+    }
+    // RNE of one f32 value to bf16, returned as the f32 of the same value:
+    // the conversion's high half with a zero low half, one instruction
+    MG_DEV float bf_round(float x)
+    {
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+        const f2 v = {0.0f, opaque(x)};
+        return __builtin_bit_cast(float, __builtin_convertvector(v, h2));
+    }
+    MG_DEV uint32_t bf_canon(uint32_t w)
+    {
+        const uint32_t a = w & 0xffffu, b = w >> 16;
+        return ((a & 0x7fffu) > 0x7f80u ? 0x7fc0u : a) | ((b & 0x7fffu) > 0x7f80u ? 0x7fc0u : b) << 16;
+    }
+    // rope_pair for two adjacent bf16 (lo, hi) pairs at once, in words; the
+    // same products, sums and roundings, two per conversion
+    MG_DEV void rope_bf16x2(uint32_t &l, uint32_t &h, uint32_t c, uint32_t s)
+    {
+        const float l0 = bf_lo(l), l1 = bf_hi(l), h0 = bf_lo(h), h1 = bf_hi(h);
+        const float c0 = bf_lo(c), c1 = bf_hi(c), s0 = bf_lo(s), s1 = bf_hi(s);
+        const uint32_t a = bf_pack(l0 * c0, l1 * c1), b = bf_pack(-(h0 * s0), -(h1 * s1));
+        const uint32_t d = bf_pack(h0 * c0, h1 * c1), e = bf_pack(l0 * s0, l1 * s1);
+        l = bf_pack(bf_lo(a) + bf_lo(b), bf_hi(a) + bf_hi(b));
+        h = bf_pack(bf_lo(d) + bf_lo(e), bf_hi(d) + bf_hi(e));
+    }
+
     // -------------------------------------------------------- wave64 reductions
     template <typename T>
     MG_DEV T wave_sum(T v)
