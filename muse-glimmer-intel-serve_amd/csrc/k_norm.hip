@@ -262,9 +262,12 @@ namespace mg
     {
         using raw = typename S::raw;
         const int nchunk = dim / VEC;
-        // threads per row <= 512 where possible; up to 16 chunks per thread
+        // threads per row <= 512 where possible, <= 1024 for the few rows of a
+        // decode step (each row's latency is the op's: the shortest per-thread
+        // chain wins there); up to 16 chunks per thread
         int cpt = 1;
-        while ((nchunk + cpt - 1) / cpt > 512 && cpt < 16) cpt *= 2;
+        const int lim = rows <= kPrefetchRows ? 1024 : 512;
+        while ((nchunk + cpt - 1) / cpt > lim && cpt < 16) cpt *= 2;
         int nt = (nchunk + cpt - 1) / cpt;
         need(nt <= 1024, "rmsnorm: dim " + std::to_string(dim) + " too large");
         nt = (nt + 63) / 64 * 64;

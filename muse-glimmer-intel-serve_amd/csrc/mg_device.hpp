@@ -265,17 +265,6 @@ namespace mg
         const uint32_t a = w & 0xffffu, b = w >> 16;
         return ((a & 0x7fffu) > 0x7f80u ? 0x7fc0u : a) | ((b & 0x7fffu) > 0x7f80u ? 0x7fc0u : b) << 16;
     }
-    // rope_pair for two adjacent bf16 (lo, hi) pairs at once, in words; the
-    // same products, sums and roundings, two per conversion
-    MG_DEV void rope_bf16x2(uint32_t &l, uint32_t &h, uint32_t c, uint32_t s)
-    {
-        const float l0 = bf_lo(l), l1 = bf_hi(l), h0 = bf_lo(h), h1 = bf_hi(h);
-        const float c0 = bf_lo(c), c1 = bf_hi(c), s0 = bf_lo(s), s1 = bf_hi(s);
-        const uint32_t a = bf_pack(l0 * c0, l1 * c1), b = bf_pack(-(h0 * s0), -(h1 * s1));
-        const uint32_t d = bf_pack(h0 * c0, h1 * c1), e = bf_pack(l0 * s0, l1 * s1);
-        l = bf_pack(bf_lo(a) + bf_lo(b), bf_hi(a) + bf_hi(b));
-        h = bf_pack(bf_lo(d) + bf_lo(e), bf_hi(d) + bf_hi(e));
-    }
 
     // -------------------------------------------------------- wave64 reductions
     template <typename T>
