@@ -79,6 +79,13 @@ BYTES = {
     "probe_2r2w_norm_shape": 4 * 2 * T * D,
 }
 BYTES["softmax_causal_softcap30"] = BYTES["softmax_causal"]
+# size-matched probes: an op's own byte count moved by the probe's pattern (a copy moves half
+# the bytes each way), so small ops are read against a ceiling with the same fixed costs
+SIZED_PROBES = {"probe_copy_rope_size": ("rope", "copy"), "probe_copy_qk_size": ("qk_norm_rope_kv", "copy"),
+                "probe_read_vocab_size": ("vocab_lse_argmax_top64", "read"),
+                "probe_read_gemv_size": ("gemv_q8_0_decode", "read")}
+for _p, (_op, _kind) in SIZED_PROBES.items():
+    BYTES[_p] = BYTES[_op] // 32 * 32 if _kind == "copy" else BYTES[_op] // 16 * 16
 # matrix-core ops: q.k and p.v over the causal pairs, 2 * 2 * head_dim flops per (query, key)
 FLOPS = {"attn_prefill_4096": Q_H * (T * (T + 1) // 2) * 4 * HD}
 PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
@@ -106,6 +113,8 @@ KERNEL_OF = {
     "probe_write_256MiB": "k_probe<2> (write)",
     "probe_2r2w_norm_shape": "k_probe<3> (2 reads + 2 writes, the residual_rmsnorm traffic)",
 }
+for _p, (_op, _kind) in SIZED_PROBES.items():
+    KERNEL_OF[_p] = f"k_probe<{0 if _kind == 'copy' else 1}> ({_kind}, {_op}'s bytes)"
 
 
 def parse():
@@ -213,6 +222,13 @@ def make_inputs(torch, P):
         "probe_write_256MiB": lambda: P.probe_stream(P.PROBE_WRITE, None, I["copy_dst"]),
         "probe_2r2w_norm_shape": lambda: P.probe_stream(P.PROBE_2R2W, I["pa"], None, I["pc"], I["pd"]),
     }
+    for name, (_op, kind) in SIZED_PROBES.items():
+        if kind == "copy":
+            n = BYTES[name] // 2
+            ops[name] = (lambda n: lambda: P.probe_stream(P.PROBE_COPY, I["copy_src"][:n], I["copy_dst"][:n]))(n)
+        else:
+            n = BYTES[name]
+            ops[name] = (lambda n: lambda: P.probe_stream(P.PROBE_READ, I["copy_src"][:n], I["one"]))(n)
     for t in (1, 4, 16, 64):
         ops[f"residual_rmsnorm_T{t}"] = (lambda t=t: P.residual_rmsnorm(
             M.PLAIN, I["hdec"][:t], I["xdec"][:t], I["w"], 1e-6, I["ydec"][:t]))

@@ -35,7 +35,7 @@
 
 namespace mg
 {
-    constexpr int kPfQ = 32; // query rows per work-group (two 16-row tiles)
+    constexpr int kPfTiles = 2; // 16-row query tiles per work-group (one per wave and head)
 
     struct PfArgs
     {
@@ -45,20 +45,25 @@ namespace mg
     };
 
     // HPG query heads per work-group, KB = head_dim / 32, RT 16-row tiles per
-    // wave (the work-group has HPG * 2 / RT waves), KT 16-key tiles per step
-    template <int HPG, int KB, int RT, int KT>
-    __global__ __launch_bounds__(64 * HPG * 2 / RT) void k_attn_prefill(const uint16_t *__restrict__ q,
+    // wave, KT 16-key tiles per step, QT 16-row query tiles per work-group (it
+    // has HPG * QT / RT waves)
+    template <int HPG, int KB, int RT, int KT, int QT>
+    __global__ __launch_bounds__(64 * HPG * QT / RT) void k_attn_prefill(const uint16_t *__restrict__ q,
                                                                         const uint16_t *__restrict__ kc,
                                                                         const uint16_t *__restrict__ vc, PfArgs a,
                                                                         float *__restrict__ out)
     {
         constexpr int D = 32 * KB, NT = 2 * KB; // NT output tiles of 16 dims
-        constexpr int SK = D + 8, SV = D + 16;  // LDS row strides (elements)
+        // LDS row strides (elements), D + 16 for both: the 16-byte reads of K rows
+        // and the transposing reads of V run free of bank conflicts (D + 8 for K
+        // stalled a quarter of the LDS cycles)
+        constexpr int SK = D + 16, SV = D + 16;
         constexpr int KS = 16 * KT;             // keys per step
-        constexpr int NTHR = 64 * HPG * 2 / RT;
+        constexpr int NTHR = 64 * HPG * QT / RT;
+        constexpr int QR = 16 * QT; // query rows per work-group
         constexpr int LPR = D / 8;                       // 16-byte pieces per key row
         constexpr int NPC = KS * LPR;                    // pieces per tile of K (or V)
-        constexpr int PPT = (2 * NPC + NTHR - 1) / NTHR; // staged pieces per thread
+        constexpr int PPH = (NPC + NTHR - 1) / NTHR;     // staged pieces per thread (K or V)
         __shared__ __align__(16) uint16_t lk[2][KS * SK];
         __shared__ __align__(16) uint16_t lv[2][KS * SV];
         const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
@@ -70,8 +75,8 @@ namespace mg
         const int64_t g = gs / a.nsub;
         const int64_t h = g * a.hpg + (gs - g * a.nsub) * HPG + wv % HPG;
         const int u0 = (wv / HPG) * RT;                           // this wave's first row tile
-        const int64_t q0 = qt * kPfQ;                             // the work-group's first query row
-        const int64_t qlast = (q0 + kPfQ < a.T ? q0 + kPfQ : a.T) - 1; // last live row
+        const int64_t q0 = qt * QR;                               // the work-group's first query row
+        const int64_t qlast = (q0 + QR < a.T ? q0 + QR : a.T) - 1; // last live row
         const int64_t khi = a.pos0 + qlast;                       // last key any row attends
         const int64_t p0 = a.pos0 + q0;
         const int64_t klo = a.window > 0 ? (p0 - a.window + 1 > 0 ? p0 - a.window + 1 : 0) : 0;
@@ -93,52 +98,39 @@ namespace mg
         // the wave's rows: first and last position (for the unmasked-step test)
         const int64_t wp0 = p0 + 16 * u0, wp1 = p0 + 16 * (u0 + RT) - 1;
 
-        // staging: piece i of a step is K piece i (i < NPC) or V piece i - NPC,
-        // key i / LPR (mod NPC), 16 bytes at column i % LPR
-        Vec<uint32_t, 4> stg[PPT];
-        // per piece, fixed for the whole kernel: its source row offset within a
-        // step (from the step's first ring slot) and its K or V array
-        const uint16_t *gsrc[PPT];
-#pragma unroll
-        for (int u = 0; u < PPT; ++u) {
-            const int i = tid + NTHR * u;
-            const int iv = i < NPC ? i : i - NPC;
-            const int key = iv / LPR, col = iv - key * LPR;
-            gsrc[u] = (i < NPC ? kc : vc) + key * rowstride + g * D + 8 * col;
-        }
-        auto stage = [&](int64_t jb, int64_t sb) {
+        // staging, K and V separately (one of them in registers at a time):
+        // piece i of a tile is key i / LPR, 16 bytes at column i % LPR;
+        // thread tid takes pieces tid + NTHR u
+        Vec<uint32_t, 4> stg[PPH];
+        auto stage = [&](const uint16_t *src, int64_t jb, int64_t sb) {
             if (jb + KS - 1 <= khi && sb + KS <= a.slots) {
                 // a whole step inside the ring: fixed offsets from one base
-                const int64_t off = sb * rowstride;
+                const uint16_t *base = src + sb * rowstride + g * D;
 #pragma unroll
-                for (int u = 0; u < PPT; ++u)
-                    if (tid + NTHR * u < 2 * NPC)
-                        stg[u] = *reinterpret_cast<const Vec<uint32_t, 4> *>(gsrc[u] + off);
+                for (int u = 0; u < PPH; ++u) {
+                    const int i = tid + NTHR * u;
+                    const int key = i / LPR, col = i - key * LPR;
+                    if (i < NPC) stg[u] = *reinterpret_cast<const Vec<uint32_t, 4> *>(base + key * rowstride + 8 * col);
+                }
                 return;
             }
 #pragma unroll
-            for (int u = 0; u < PPT; ++u) {
+            for (int u = 0; u < PPH; ++u) {
                 const int i = tid + NTHR * u;
-                const int iv = i < NPC ? i : i - NPC;
-                const int key = iv / LPR, col = iv - key * LPR;
+                const int key = i / LPR, col = i - key * LPR;
                 int64_t sl = sb + key;
                 sl = sl >= a.slots ? sl - a.slots : sl;
-                const uint16_t *base = i < NPC ? kc : vc;
                 stg[u] = Vec<uint32_t, 4>{{0u, 0u, 0u, 0u}};
-                if (i < 2 * NPC && jb + key <= khi)
-                    stg[u] = *reinterpret_cast<const Vec<uint32_t, 4> *>(base + sl * rowstride + g * D + 8 * col);
+                if (i < NPC && jb + key <= khi)
+                    stg[u] = *reinterpret_cast<const Vec<uint32_t, 4> *>(src + sl * rowstride + g * D + 8 * col);
             }
         };
-        auto commit = [&](int buf) {
+        auto commit = [&](uint16_t *dst, int stride) {
 #pragma unroll
-            for (int u = 0; u < PPT; ++u) {
+            for (int u = 0; u < PPH; ++u) {
                 const int i = tid + NTHR * u;
-                if (i < 2 * NPC) {
-                    const int iv = i < NPC ? i : i - NPC;
-                    const int key = iv / LPR, col = iv - key * LPR;
-                    uint16_t *dst = i < NPC ? lk[buf] + key * SK : lv[buf] + key * SV;
-                    *reinterpret_cast<Vec<uint32_t, 4> *>(dst + 8 * col) = stg[u];
-                }
+                const int key = i / LPR, col = i - key * LPR;
+                if (i < NPC) *reinterpret_cast<Vec<uint32_t, 4> *>(dst + key * stride + 8 * col) = stg[u];
             }
         };
 
@@ -155,15 +147,17 @@ namespace mg
         }
 
         int64_t sb = klo % a.slots; // ring slot of key jb
-        stage(klo, sb);
-        commit(0);
+        stage(kc, klo, sb);
+        commit(lk[0], SK);
+        stage(vc, klo, sb);
+        commit(lv[0], SV);
         __syncthreads();
         int buf = 0;
         for (int64_t jb = klo; jb <= khi; jb += KS) {
             int64_t sn = sb + KS;
             sn = sn >= a.slots ? sn - a.slots : sn;
             const bool more = jb + KS <= khi;
-            if (more) stage(jb + KS, sn); // in flight while this step computes
+            if (more) stage(kc, jb + KS, sn); // the next K tile, in flight while S and the softmax run
             const uint16_t *sk = lk[buf], *sv = lv[buf];
             // every row of the wave attends the whole step unless it reaches
             // past the wave's first row or before its last row's window
@@ -224,6 +218,12 @@ namespace mg
                 l[u] = (mn != m[u] ? l[u] * corr[u] : l[u]) + ps;
                 m[u] = mn;
             }
+            if (more) {
+                // K(j+1) goes to the other buffer (its last readers passed the
+                // previous barrier); then the next V tile is requested
+                commit(lk[buf ^ 1], SK);
+                stage(vc, jb + KS, sn);
+            }
             if (__builtin_amdgcn_ballot_w64(moved) != 0) {
                 // O rows are query rows 4c + r: their factors come from lanes 4c + r
 #pragma unroll
@@ -251,7 +251,7 @@ namespace mg
 #pragma unroll
                     for (int u = 0; u < RT; ++u) o[u][t] = mfma_bf16(pb[u][i], vb, o[u][t]);
                 }
-            if (more) commit(buf ^ 1);
+            if (more) commit(lv[buf ^ 1], SV);
             __syncthreads(); // the next buffer is written; this one is free again
             buf ^= 1;
             sb = sn;
@@ -297,7 +297,7 @@ namespace mg
         const int64_t lo0 = window > 0 ? (pos0 - window + 1 > 0 ? pos0 - window + 1 : 0) : 0;
         need(pos0 + T - 1 - lo0 + 1 <= slots,
              "attn_prefill: the attended keys do not fit the cache ring (pos0 + T - lo > cache_slots)");
-        const int64_t nqt = (T + kPfQ - 1) / kPfQ;
+        const int64_t nqt = (T + 16 * kPfTiles - 1) / (16 * kPfTiles);
         need(nqt * nkv * nsub <= int64_t(0x7fffffff), "attn_prefill: too many query tiles");
         const PfArgs a{T, nkv, ldq, ldo, slots, pos0, window, nqt, hpg, nsub,
                        float(double(float(scaling)) * 1.4426950408889634)};
@@ -305,10 +305,13 @@ namespace mg
         auto go = [&](auto kern, int waves) {
             hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * waves)), 0, c->stream, q, kc, vc, a, out);
         };
-        // one 16-row tile per wave (2 * HPG waves) for groups of up to 8 heads;
+        // one 16-row tile per wave (kPfTiles * HPG waves) for groups of up to 8 heads;
         // 64-key steps
 #define MG_PF_CASE(H)                                                                                               \
-    case H: D == 128 ? go(k_attn_prefill<H, 4, 1, 4>, 2 * H) : go(k_attn_prefill<H, 2, 1, 4>, 2 * H); break;
+    case H:                                                                                                         \
+        D == 128 ? go(k_attn_prefill<H, 4, 1, 4, kPfTiles>, kPfTiles * H)                                          \
+                 : go(k_attn_prefill<H, 2, 1, 4, kPfTiles>, kPfTiles * H);                                         \
+        break;
         switch (hw) {
             MG_PF_CASE(1)
             MG_PF_CASE(2)
