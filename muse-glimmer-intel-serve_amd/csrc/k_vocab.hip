@@ -36,6 +36,7 @@
 // for any input, slower only where one chunk holds more than D of the row's
 // top K.
 #include "mg_device.hpp"
+#include "mg_softcap_fast.hpp"
 #include "mg_internal.hpp"
 
 #include <mutex>
@@ -76,6 +77,7 @@ namespace mg
     {
         float mult, cap;
         void *out;
+        float rcap; // RN(1 / cap) for 1 <= |cap| <= 2^20, else 0 (the IEEE quotient)
     };
     template <class SI>
     MG_DEV float vtail(float x, const VTail &t)
@@ -83,7 +85,18 @@ namespace mg
         float v = x;
         if (t.mult != 1.0f) v = SI::dec(SI::enc32(v * t.mult));
         if (t.cap != 0.0f) {
-            v = SI::dec(SI::enc32(v / t.cap));
+            // v / cap correctly rounded: Markstein's correction of v * rcap
+            // (mg_softcap_fast.hpp) while no step can under- or overflow
+            // (the IEEE quotient only in waves that have a lane outside)
+            float q = mgm::softcap_quotient(v, t.cap, t.rcap);
+            const float av = __builtin_fabsf(v);
+            const bool fast = t.rcap != 0.0f && av > 0x1p-100f && av < 0x1p100f;
+            if (__builtin_amdgcn_ballot_w64(!fast) != 0 && !fast) {
+                float c = t.cap;
+                __asm__ volatile("" : "+v"(c)); // keeps the division inside the branch
+                q = v / c;
+            }
+            v = SI::dec(SI::enc32(q));
             v = tanh_stored<SI>(v);
             v = SI::dec(SI::enc32(v * t.cap));
         }
@@ -1033,21 +1046,67 @@ namespace mg
 
 
     // The output tail alone: out[r, j] = vtail(in[r, j]) at storage, one
-    // 16-byte vector per thread (grid: vectors of a row x rows). Run ahead of
-    // the vocab pass when the transformed logits have somewhere to go, so the
-    // pass's chunk kernel does not carry the tail's registers.
+    // 16-byte vector per thread (grid: vectors of a row x rows). The vector's
+    // values go through the steps side by side with no branch on the common
+    // path (|z / cap| < 1: the series or the table of tanh_fast_abs, selected,
+    // and the rounding test of tanh_stored), so their f64 chains overlap; a
+    // wave with a value outside (|z / cap| >= 1, inf, NaN, an uncertain
+    // rounding) runs vtail's own path for those values. Run ahead of the vocab
+    // pass when the transformed logits have somewhere to go, so the pass's
+    // chunk kernel does not carry the tail's registers.
     template <class SI, int VW>
     __global__ __launch_bounds__(256) void k_vocab_tail_map(const typename SI::raw *__restrict__ in, int64_t ld,
                                                             typename SI::raw *__restrict__ out, int64_t V, VTail t)
     {
         using raw = typename SI::raw;
+        __shared__ __align__(16) double tab[128]; // the tanh table, read at random: LDS, not the cache
+        if (threadIdx.x < 64)
+            *reinterpret_cast<Vec<double, 2> *>(tab + 2 * threadIdx.x) =
+                *reinterpret_cast<const Vec<double, 2> *>(mgm::kTanhTab + 2 * threadIdx.x);
+        __syncthreads();
         const int64_t row = blockIdx.y;
         const int64_t j = (int64_t(blockIdx.x) * 256 + threadIdx.x) * VW;
         if (j >= V) return;
         Vec<raw, VW> v = ld16_stream<raw, VW>(in + row * ld + j);
+        if (t.cap == 0.0f) {
 #pragma unroll
-        for (int e = 0; e < VW; ++e) v.v[e] = SI::enc32(vtail<SI>(float(SI::dec(v.v[e])), t));
+            for (int e = 0; e < VW; ++e) v.v[e] = SI::enc32(vtail<SI>(float(SI::dec(v.v[e])), t));
+        } else {
+            float z[VW], r[VW];
+            bool ok[VW];
+            uint32_t slow = 0;
+#pragma unroll
+            for (int e = 0; e < VW; ++e) {
+                z[e] = float(SI::dec(v.v[e]));
+                if (t.mult != 1.0f) z[e] = SI::dec(SI::enc32(z[e] * t.mult));
+                const float az = __builtin_fabsf(z[e]);
+                // Markstein's quotient where it is certain (see vtail)
+                const float q = SI::dec(SI::enc32(mgm::softcap_quotient(z[e], t.cap, t.rcap)));
+                const double a = __builtin_fabs(double(q));
+                const double ac = __builtin_fmin(a, 0x1.fffffffffffffp-1);
+                const double th = a < 0x1p-5 ? mgm::tanh_series_abs(a) : mgm::tanh_table_abs(ac, tab);
+                const auto lo = SI::enc64(th - th * mgm::kTanhFastMargin), hi = SI::enc64(th + th * mgm::kTanhFastMargin);
+                ok[e] = t.rcap != 0.0f && az > 0x1p-100f && az < 0x1p100f && a < 1.0 && lo == hi;
+                r[e] = SI::dec(SI::enc32(__builtin_copysignf(SI::dec(lo), q) * t.cap));
+                slow |= ok[e] ? 0u : 1u << e;
+            }
+            if (__builtin_amdgcn_ballot_w64(slow != 0) != 0) {
+#pragma unroll
+                for (int e = 0; e < VW; ++e)
+                    if ((slow >> e) & 1u) r[e] = vtail<SI>(float(SI::dec(v.v[e])), t);
+            }
+#pragma unroll
+            for (int e = 0; e < VW; ++e) v.v[e] = SI::enc32(r[e]);
+        }
         st16_stream<raw, VW>(out + row * V + j, v);
+    }
+
+    // RN(1 / cap) where the tail takes Markstein's quotient (1 <= |cap| <= 2^20:
+    // with 2^-100 < |v| < 2^100 the quotient and the remainder stay normal)
+    static float tail_rcap(double cap)
+    {
+        const float c = float(cap), ac = std::fabs(c);
+        return ac >= 1.0f && ac <= 0x1p20f ? recip_rn(c) : 0.0f;
     }
 
     // The pass on `stream` with its partials in `work` (work_bytes long);
@@ -1087,7 +1146,7 @@ namespace mg
                                    : (tmp_off + rows * V * esz <= work_bytes ? static_cast<char *>(work) + tmp_off
                                                                               : nullptr);
             if (dst && V % vw == 0 && ld % vw == 0 && aligned16(logits) && aligned16(dst)) {
-                const VTail t{float(mult), float(cap), nullptr};
+                const VTail t{float(mult), float(cap), nullptr, tail_rcap(cap)};
                 const dim3 gm{unsigned((V / vw + 255) / 256), unsigned(rows), 1u};
                 if (dt_in == F32)
                     hipLaunchKernelGGL((k_vocab_tail_map<SF32, 4>), gm, dim3(256), 0, stream,
@@ -1107,7 +1166,7 @@ namespace mg
         const dim3 g1{unsigned(nch), unsigned(rows), 1u};
         const dim3 g2{unsigned(rows), 1u, 1u};
         // python-float scalars are f32 opmath values outside f64 (src/muse_glimmer.hpp:924-926)
-        const VTail tail{float(mult), float(cap), logits_out};
+        const VTail tail{float(mult), float(cap), logits_out, tail_rcap(cap)};
         auto go = [&](auto chunk, auto merge, const auto *x) {
             hipLaunchKernelGGL(chunk, g1, dim3(64), 0, stream, x, ld, V, int(K), nch, part, blk, tail);
             check_launch("k_vocab_chunk");

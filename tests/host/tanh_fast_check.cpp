@@ -6,7 +6,8 @@
 // and f16 storage, that whenever t(1 -+ margin) round to one stored value,
 // FDLIBM's result rounds to it too.
 //
-// usage: tanh_fast_check [stride [margin]]   prints "maxrel accepted_bad fb_f32 fb_bf16 fb_f16 count"
+// usage: tanh_fast_check [stride [margin [perturb]]]   prints "maxrel accepted_bad fb_f32 fb_bf16 fb_f16 count"
+// (perturb: a relative error planted in the fast value, to show the check catches one)
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -19,6 +20,7 @@ int main(int argc, char **argv)
     const int64_t stride = argc > 1 ? std::atoll(argv[1]) : 1;
     const int64_t end = 0x41B00000; // 22.0f
     const double m = argc > 2 ? std::atof(argv[2]) : mgm::kTanhFastMargin;
+    const double perturb = argc > 3 ? std::atof(argv[3]) : 0.0;
     long long bad = 0, fb32 = 0, fbb = 0, fbh = 0, count = 0;
     double maxrel = 0.0;
 #pragma omp parallel for schedule(static, 1 << 16) reduction(+ : bad, fb32, fbb, fbh, count) reduction(max : maxrel)
@@ -27,7 +29,7 @@ int main(int argc, char **argv)
         float f;
         std::memcpy(&f, &u, 4);
         const double a = f;
-        const double t = mgm::tanh_fast_abs(a), r = orc::tanh(a);
+        const double t = mgm::tanh_fast_abs(a) * (1.0 + perturb), r = orc::tanh(a);
         const double rel = r == 0.0 ? std::fabs(t - r) : std::fabs(t - r) / r;
         if (rel > maxrel) maxrel = rel;
         const double lo = t - t * m, hi = t + t * m;

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from util import BF16, F16, F32, from_dev, same_bits, storage, to_dev
+from util import BF16, F16, F32, from_dev, same_bits, same_bits_or_nan, storage, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -276,3 +276,28 @@ def test_vocab_tail_fused_in_the_pass(prims, rows, V, out):
     assert np.array_equal(ti.cpu().numpy(), r_ti)
     assert np.array_equal(tv.cpu().numpy().astype(np.float64), r_tv)
 
+
+
+@pytest.mark.parametrize("dt", (F32, BF16))
+@pytest.mark.parametrize("mult,cap", ((1.0, 30.0), (1.0, 0.75), (1.0, 3.0e6), (0.5, 1.0), (3.0, 7.5)))
+def test_vocab_tail_map_special_values(prims, dt, mult, cap):
+    """the tail's own pass on values off its common path: inf, NaN, signed
+    zeros, subnormals, magnitudes at the quotient's 2^-100 / 2^100 guards,
+    |z / cap| at the 2^-5 and 1 branch points, and caps outside [1, 2^20]
+    (the IEEE quotient), bitwise against the oracle's output tail"""
+    import torch
+    V = 4096
+    rng = np.random.default_rng(91)
+    base = [np.inf, -np.inf, np.nan, 0.0, -0.0, 1e-45, -1e-40, 2.0**-100, 2.0**-99.5, 2.0**100, 2.0**99.5,
+            3e38, -3e38, cap * 2.0**-5, -cap * 2.0**-5, cap, -cap, cap * 0.999, cap * 1.001, cap * 21.9, cap * 22.1]
+    x = rng.normal(0.0, cap if cap else 4.0, V)
+    x[:len(base)] = base
+    x[len(base):len(base) + 512] = cap * rng.uniform(-1.2, 1.2, 512)
+    Ls = O.from_f64(x[None, :], dt)
+    Z = O.softcap(O.to_f64(Ls, dt), mult, cap, dt)
+    dL = to_dev(Ls, dt)
+    out = torch.empty_like(dL)
+    prims.vocab_reduce_tail(dL, mult, cap, 8, out)
+    got, want = from_dev(out, dt), O.from_f64(Z, dt)
+    # bf16 NaN is the one pattern 0x7FC0; an f32 NaN's sign is left open by IEEE
+    assert same_bits(got, want) if dt == BF16 else same_bits_or_nan(got, want, dt)

@@ -34,7 +34,8 @@ def run(exe, *args):
     return [float(v) if "." in v or "e" in v else int(v) for v in out.split()]
 
 
-@pytest.mark.parametrize("cap", ("30", "50", "20", "1", "3", "7.5", "0.7", "0.001", "12345.678"))
+@pytest.mark.parametrize("cap", ("30", "50", "20", "1", "3", "7.5", "0.7", "0.001", "12345.678", "1048575.9",
+                                 "1048576"))
 def test_markstein_quotient_is_correctly_rounded(checker, cap):
     bad, count = run(checker, "quot", cap)
     assert count == 0x71800000 - 0x0d800000 - 1

@@ -28,8 +28,9 @@ def checker(tmp_path_factory):
     return exe
 
 
-def run(exe, stride, margin=None):
+def run(exe, stride, margin=None, perturb=None):
     args = [str(exe), str(stride)] + ([repr(margin)] if margin is not None else [])
+    args += [repr(perturb)] if perturb is not None else []
     out = subprocess.run(args, check=True, capture_output=True, text=True).stdout.split()
     maxrel, bad, fb32, fbb, fbh, count = float(out[0]), *map(int, out[1:])
     return maxrel, bad, fb32, fbb, fbh, count
@@ -43,7 +44,13 @@ def test_every_float_below_22(checker):
     assert fb32 < count * 1e-5 and fbb < count * 1e-5 and fbh < count * 1e-5
 
 
-def test_margin_is_needed(checker):
-    """the check has teeth: without the margin, some fast roundings differ from FDLIBM's"""
-    maxrel, bad, fb32, _, _, count = run(checker, 1, 0.0)
-    assert bad > 0 and fb32 == 0
+def test_the_check_has_teeth(checker):
+    """a fast value off by 2^-34 (planted on the CPU) is caught: without a margin
+    and with a margin smaller than that error, some accepted roundings differ
+    from FDLIBM's; a margin above it accepts none wrongly"""
+    maxrel, bad, fb32, _, _, count = run(checker, 1, 0.0, 2.0**-34)
+    assert bad > 0 and fb32 == 0 and maxrel > 2.0**-35
+    _, bad, _, _, _, _ = run(checker, 1, 2.0**-40, 2.0**-34)
+    assert bad > 0
+    _, bad, _, _, _, _ = run(checker, 1, 2.0**-33, 2.0**-34)
+    assert bad == 0
