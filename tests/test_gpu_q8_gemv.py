@@ -91,6 +91,15 @@ def test_gemv(prims, B, blockdot):
     gemv_case(prims, 1000, 5120, B, blockdot)
 
 
+@pytest.mark.parametrize("n_in", (32, 96, 160, 4160, 16384, 16448))
+@pytest.mark.parametrize("blockdot", (False, True))
+def test_gemv_widths(prims, n_in, blockdot):
+    """input widths around the scale preload: rows whose scales are not whole
+    32-bit words (96, 160), a last step with a few lanes (4160), the largest
+    preloaded width (16384) and the next one (16448)"""
+    gemv_case(prims, 37, n_in, 1, blockdot, seed=61)
+
+
 def test_gemv_config5_shape(prims):
     """config 5's weight [25600, 5120] at decode (one token)"""
     gemv_case(prims, 25600, 5120, 1, False)
