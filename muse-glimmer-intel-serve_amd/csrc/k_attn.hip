@@ -234,7 +234,7 @@ namespace mg
     {
         __shared__ double redl[4];
         __shared__ float redm[4];
-        __shared__ float part[16][17];
+        __shared__ float part[4][16];
         const int64_t h = blockIdx.x;
         const int d0 = 16 * int(blockIdx.y);
         const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
@@ -250,22 +250,35 @@ namespace mg
             if (mh[s] != -__builtin_huge_valf()) L += double(__builtin_amdgcn_exp2f(mh[s] - M)) * double(lh[s]);
         L = dpp_sum(L);
         if (lane == 0) redl[wv] = L;
-        const int sg = tid >> 4, d = tid & 15;
-        float o = 0.0f;
-        for (int s = sg; s < nsplit; s += 16) {
+        // the 16 output dims: each thread takes whole splits (64 contiguous
+        // bytes of one split's partial each), so a thread has its loads in
+        // flight together; then a sum over the wave and over the four waves
+        float o[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[e] = 0.0f;
+        for (int s = tid; s < nsplit; s += 256) {
             const float ms = mh[s];
-            if (ms != -__builtin_huge_valf())
-                o = __builtin_fmaf(__builtin_amdgcn_exp2f(ms - M), pa[(h * nsplit + s) * D + d0 + d], o);
+            if (ms != -__builtin_huge_valf()) {
+                const float wgt = __builtin_amdgcn_exp2f(ms - M);
+                const Vec<float, 4> *src = reinterpret_cast<const Vec<float, 4> *>(pa + (h * nsplit + s) * D + d0);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const Vec<float, 4> v = src[k];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[4 * k + e] = __builtin_fmaf(wgt, v.v[e], o[4 * k + e]);
+                }
+            }
         }
-        part[sg][d] = o;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[e] = dpp_sum_f32(o[e]);
+        if (lane == 0)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) part[wv][e] = o[e];
         __syncthreads();
         if (tid < 16) {
             L = (redl[0] + redl[1]) + (redl[2] + redl[3]);
             const float inv = L > 0.0 ? float(1.0 / L) : 0.0f;
-            float t = 0.0f;
-#pragma unroll
-            for (int g2 = 0; g2 < 16; ++g2) t += part[g2][tid];
-            out[h * D + d0 + tid] = t * inv;
+            out[h * D + d0 + tid] = ((part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid])) * inv;
         }
     }
 
@@ -296,11 +309,14 @@ namespace mg
         int64_t per = (total + ns - 1) / ns;
         per = (per + 31) / 32 * 32;
         const int nsplit = int((total + per - 1) / per);
-        const int64_t need_bytes = nq * nsplit * int64_t(sizeof(float)) * (D + 2);
+        // maxima and sums first, then the partial outputs from a 16-byte boundary
+        // (the combine reads them as 16-byte vectors)
+        const int64_t pa_off = (2 * nq * nsplit + 3) / 4 * 4;
+        const int64_t need_bytes = (pa_off + nq * nsplit * D) * int64_t(sizeof(float));
         need(need_bytes <= c->work_bytes, "attn_decode: partials exceed the context workspace (raise workspace_bytes at mg_open)");
         float *pm = static_cast<float *>(c->work);
         float *pl = pm + nq * nsplit;
-        float *pa = pl + nq * nsplit;
+        float *pa = pm + pa_off;
         const AttnArgs a{nq, nkv, slots, qpos, lo, per, nsplit, int(hpg), int(nsub),
                          float(double(float(scaling)) * 1.4426950408889634)};
         need((nkv * nsub * nsplit + 3) / 4 < (int64_t(1) << 31), "attn_decode: too many heads");
