@@ -41,7 +41,8 @@ namespace mg
     {
         int64_t T, nkv, ldq, ldo, slots, pos0, window, nqt;
         int64_t hpg, nsub; // query heads per kv head; work-groups per (kv head, tile), HPG heads each
-        float scale2;      // scaling * log2(e)
+        float scale2;      // |scaling| * log2(e), 2^-126 in place of 0
+        uint32_t qsign;    // 0x80008000 when scaling < 0: q enters with its sign flipped
     };
 
     // HPG query heads per work-group, KB = head_dim / 32, RT 16-row tiles per
@@ -91,7 +92,12 @@ namespace mg
             const int64_t r0 = q0 + 16 * (u0 + u) + n;
             const int64_t row = r0 <= qlast ? r0 : qlast;
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) qop[u][kb] = ld_bf16x8(q + row * a.ldq + h * D + 32 * kb + 8 * c);
+            for (int kb = 0; kb < KB; ++kb) {
+                Vec<uint32_t, 4> w = __builtin_bit_cast(Vec<uint32_t, 4>, ld_bf16x8(q + row * a.ldq + h * D + 32 * kb + 8 * c));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w.v[i] ^= a.qsign;
+                qop[u][kb] = __builtin_bit_cast(bf16x8, w);
+            }
             qp[u] = a.pos0 + r0;
             ql[u] = a.window > 0 ? (qp[u] - a.window + 1 > 0 ? qp[u] - a.window + 1 : 0) : 0;
         }
@@ -162,7 +168,9 @@ namespace mg
             // every row of the wave attends the whole step unless it reaches
             // past the wave's first row or before its last row's window
             const bool full = jb + KS - 1 <= wp0 && (a.window <= 0 || jb >= wp1 - a.window + 1);
-            // S^T tiles: lane (query n, c) holds keys 16 t + 4c + r
+            // S^T tiles: lane (query n, c) holds keys 16 t + 4c + r, unscaled
+            // (scale2 > 0 multiplies inside the exponent, and the row maximum
+            // of the scaled scores is the scaled maximum)
             float s[RT][KT][4];
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
@@ -178,7 +186,7 @@ namespace mg
                     for (int kb = 0; kb < KB; ++kb) st = mfma_bf16(kt[kb], qop[u][kb], st);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        float v = st[r] * a.scale2;
+                        float v = st[r];
                         if (!full) {
                             const int64_t j = jb + 16 * t + 4 * c + r;
                             v = (j > qp[u] || j < ql[u]) ? -__builtin_huge_valf() : v;
@@ -199,7 +207,7 @@ namespace mg
                 for (int t = 0; t < KT; ++t)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) mx = __builtin_fmaxf(mx, s[u][t][r]);
-                mx = rows4_max(mx);
+                mx = rows4_max(mx) * a.scale2;
                 const float mn = __builtin_fmaxf(m[u], mx);
                 // a row with nothing attended yet keeps a zero reference: its
                 // weights are 2^-inf = 0 and nothing is rescaled into NaN
@@ -209,7 +217,7 @@ namespace mg
                 for (int t = 0; t < KT; ++t)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float e = __builtin_amdgcn_exp2f(s[u][t][r] - mref);
+                        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][r], a.scale2, -mref));
                         ps += e;
                         pb[u][t / 2][4 * (t % 2) + r] = __bf16(e);
                     }
@@ -299,8 +307,13 @@ namespace mg
              "attn_prefill: the attended keys do not fit the cache ring (pos0 + T - lo > cache_slots)");
         const int64_t nqt = (T + 16 * kPfTiles - 1) / (16 * kPfTiles);
         need(nqt * nkv * nsub <= int64_t(0x7fffffff), "attn_prefill: too many query tiles");
+        // the kernel scales inside the exponent by a positive factor: a negative
+        // scaling flips the sign of q instead (exact in bf16 and in the products),
+        // and a zero one becomes 2^-126, under which every exponent of a finite
+        // score is below 2^-100 in magnitude and exp2 returns 1 as it does at 0
+        const float s2 = float(double(float(scaling)) * 1.4426950408889634);
         const PfArgs a{T, nkv, ldq, ldo, slots, pos0, window, nqt, hpg, nsub,
-                       float(double(float(scaling)) * 1.4426950408889634)};
+                       s2 == 0.0f ? 0x1p-126f : __builtin_fabsf(s2), s2 < 0.0f ? 0x80008000u : 0u};
         const dim3 grid{unsigned(nqt * nkv * nsub), 1u, 1u};
         auto go = [&](auto kern, int waves) {
             hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * waves)), 0, c->stream, q, kc, vc, a, out);

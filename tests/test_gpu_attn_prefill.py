@@ -101,6 +101,14 @@ def test_peaked_scores(prims):
     prefill_case(prims, 300, 8, 2, 128, 512, 0, scaling=1.0, seed=140)
 
 
+@pytest.mark.parametrize("scaling", (-1.0 / math.sqrt(128), -1.0, 0.0, 1e-30))
+def test_scaling_signs(prims, scaling):
+    """the kernel multiplies by |scaling| inside the exponent: a negative
+    scaling (q enters negated, so the weights favour the least similar keys),
+    zero (every attended key weighs the same) and a tiny one"""
+    prefill_case(prims, 90, 8, 2, 128, 128, 20, scaling=scaling, seed=145)
+
+
 def test_config3_prefill_sampled(prims):
     """config 3's prompt: 4096 tokens, 40 q / 8 kv heads, causal; a sample of
     heads and rows against f64 (the full f64 check is minutes of numpy)"""
