@@ -152,26 +152,10 @@ namespace mg
             l[u] = 0.0f;
         }
 
-        int64_t sb = klo % a.slots; // ring slot of key jb
-        stage(kc, klo, sb);
-        commit(lk[0], SK);
-        stage(vc, klo, sb);
-        commit(lv[0], SV);
-        __syncthreads();
-        int buf = 0;
-        for (int64_t jb = klo; jb <= khi; jb += KS) {
-            int64_t sn = sb + KS;
-            sn = sn >= a.slots ? sn - a.slots : sn;
-            const bool more = jb + KS <= khi;
-            if (more) stage(kc, jb + KS, sn); // the next K tile, in flight while S and the softmax run
-            const uint16_t *sk = lk[buf], *sv = lv[buf];
-            // every row of the wave attends the whole step unless it reaches
-            // past the wave's first row or before its last row's window
-            const bool full = jb + KS - 1 <= wp0 && (a.window <= 0 || jb >= wp1 - a.window + 1);
-            // S^T tiles: lane (query n, c) holds keys 16 t + 4c + r, unscaled
-            // (scale2 > 0 multiplies inside the exponent, and the row maximum
-            // of the scaled scores is the scaled maximum)
-            float s[RT][KT][4];
+        // S^T tiles of one step from a K buffer: lane (query n, c) holds keys
+        // 16 t + 4c + r, unscaled (scale2 > 0 multiplies inside the exponent,
+        // and the row maximum of the scaled scores is the scaled maximum)
+        auto scores = [&](const uint16_t *sk, float (&sx)[RT][KT][4]) {
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
                 bf16x8 kt[KB]; // K as A: lane (key n, c) holds dims 32 kb + 8c.. of key 16 t + n
@@ -185,16 +169,52 @@ namespace mg
 #pragma unroll
                     for (int kb = 0; kb < KB; ++kb) st = mfma_bf16(kt[kb], qop[u][kb], st);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        float v = st[r];
-                        if (!full) {
-                            const int64_t j = jb + 16 * t + 4 * c + r;
-                            v = (j > qp[u] || j < ql[u]) ? -__builtin_huge_valf() : v;
-                        }
-                        s[u][t][r] = v;
-                    }
+                    for (int r = 0; r < 4; ++r) sx[u][t][r] = st[r];
                 }
             }
+        };
+        auto wrap = [&](int64_t sl) { return sl >= a.slots ? sl - a.slots : sl; };
+
+        // Software pipeline: the scores of step j + 1 run on the matrix cores
+        // while step j's softmax runs on the VALU. At the top of step j, K(j+1)
+        // is in lk[cur ^ 1], V(j) in lv[cur], and S(j) in registers; lk[cur]
+        // (K(j), read during step j - 1) is free for K(j+2).
+        int64_t sb = klo % a.slots; // ring slot of key jb
+        stage(kc, klo, sb);
+        commit(lk[0], SK);
+        stage(vc, klo, sb);
+        commit(lv[0], SV);
+        __syncthreads();
+        float s[RT][KT][4];
+        scores(lk[0], s);
+        if (klo + KS <= khi) {
+            stage(kc, klo + KS, wrap(sb + KS));
+            commit(lk[1], SK);
+        }
+        __syncthreads(); // K(1) is in lk[1]; every wave is done with lk[0]
+        int cur = 0;
+        for (int64_t jb = klo; jb <= khi; jb += KS) {
+            const int64_t s1 = wrap(sb + KS), s2 = wrap(s1 + KS);
+            const bool more = jb + KS <= khi, more2 = jb + 2 * KS <= khi;
+            if (more2) stage(kc, jb + 2 * KS, s2); // K(j+2), in flight through this step
+            // every row of the wave attends the whole step unless it reaches
+            // past the wave's first row or before its last row's window
+            const bool full = jb + KS - 1 <= wp0 && (a.window <= 0 || jb >= wp1 - a.window + 1);
+            if (!full) {
+#pragma unroll
+                for (int u = 0; u < RT; ++u)
+#pragma unroll
+                    for (int t = 0; t < KT; ++t)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int64_t j = jb + 16 * t + 4 * c + r;
+                            s[u][t][r] = (j > qp[u] || j < ql[u]) ? -__builtin_huge_valf() : s[u][t][r];
+                        }
+            }
+            // S(j+1) (from whatever lk[cur ^ 1] holds after the last step: in
+            // bounds, unused), issued ahead of step j's softmax
+            float sx[RT][KT][4];
+            scores(lk[cur ^ 1], sx);
             // online softmax per row; P for the p.v product, element 4(t%2) + r
             // of pair t/2 is key 16 t + 4c + r
             bf16x8 pb[RT][KT / 2];
@@ -226,12 +246,8 @@ namespace mg
                 l[u] = (mn != m[u] ? l[u] * corr[u] : l[u]) + ps;
                 m[u] = mn;
             }
-            if (more) {
-                // K(j+1) goes to the other buffer (its last readers passed the
-                // previous barrier); then the next V tile is requested
-                commit(lk[buf ^ 1], SK);
-                stage(vc, jb + KS, sn);
-            }
+            if (more2) commit(lk[cur], SK); // K(j+2) over K(j)
+            if (more) stage(vc, jb + KS, s1);
             if (__builtin_amdgcn_ballot_w64(moved) != 0) {
                 // O rows are query rows 4c + r: their factors come from lanes 4c + r
 #pragma unroll
@@ -248,7 +264,7 @@ namespace mg
             // V as B of P V: lane (dim n, c) gets keys 32 i + 4c + r and
             // 32 i + 16 + 4c + r of dim 16 s + n from the transposing read (lanes
             // 4j + q address key 32 i + 4c + j (+16), dims 16 s + 4q..)
-            const uint16_t *vr = sv + (4 * c + (n >> 2)) * SV + 4 * (n & 3);
+            const uint16_t *vr = lv[cur] + (4 * c + (n >> 2)) * SV + 4 * (n & 3);
 #pragma unroll
             for (int i = 0; i < KT / 2; ++i)
 #pragma unroll
@@ -259,10 +275,16 @@ namespace mg
 #pragma unroll
                     for (int u = 0; u < RT; ++u) o[u][t] = mfma_bf16(pb[u][i], vb, o[u][t]);
                 }
-            if (more) commit(lv[buf ^ 1], SV);
-            __syncthreads(); // the next buffer is written; this one is free again
-            buf ^= 1;
-            sb = sn;
+            if (more) commit(lv[cur ^ 1], SV); // V(j+1) over V(j-1)
+            __syncthreads(); // the next buffers are written; these are free again
+#pragma unroll
+            for (int u = 0; u < RT; ++u)
+#pragma unroll
+                for (int t = 0; t < KT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[u][t][r] = sx[u][t][r];
+            cur ^= 1;
+            sb = s1;
         }
 
         // out = acc / sumexp, rows 4c + r of each tile from lanes 4c + r
