@@ -1048,7 +1048,7 @@ namespace mg
     // The output tail alone: out[r, j] = vtail(in[r, j]) at storage, one
     // 16-byte vector per thread (grid: vectors of a row x rows). The vector's
     // values go through the steps side by side with no branch on the common
-    // path (|z / cap| < 1: the series or the table of tanh_fast_abs, selected,
+    // path (|z / cap| < 1: the table polynomial of tanh_fast_abs,
     // and the rounding test of tanh_stored), so their f64 chains overlap; a
     // wave with a value outside (|z / cap| >= 1, inf, NaN, an uncertain
     // rounding) runs vtail's own path for those values. Run ahead of the vocab
@@ -1084,7 +1084,7 @@ namespace mg
                 const float q = SI::dec(SI::enc32(mgm::softcap_quotient(z[e], t.cap, t.rcap)));
                 const double a = __builtin_fabs(double(q));
                 const double ac = __builtin_fmin(a, 0x1.fffffffffffffp-1);
-                const double th = a < 0x1p-5 ? mgm::tanh_series_abs(a) : mgm::tanh_table_abs(ac, tab);
+                const double th = mgm::tanh_table_abs(ac, tab);
                 const auto lo = SI::enc64(th - th * mgm::kTanhFastMargin), hi = SI::enc64(th + th * mgm::kTanhFastMargin);
                 ok[e] = t.rcap != 0.0f && az > 0x1p-100f && az < 0x1p100f && a < 1.0 && lo == hi;
                 r[e] = SI::dec(SI::enc32(__builtin_copysignf(SI::dec(lo), q) * t.cap));

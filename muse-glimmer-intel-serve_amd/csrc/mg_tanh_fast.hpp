@@ -8,14 +8,15 @@
 // it evaluates FDLIBM (rare: about 2m / 2^-24 of the inputs for f32).
 //
 // Method (Taylor series, ln 2 split into two doubles, all steps fma):
-//   a < 2^-5:  tanh a = a + a^3 P(a^2), P the series to a^11 (truncation
-//              below 1e-18 relative);
-//   a < 1:     the degree-5 Taylor polynomial about the nearest point
-//              a0 = (k + 0.5) / 128 of a table of tanh(a0) (correctly
-//              rounded, gen_tanh_table.py), |d| = |a - a0| <= 2^-8, its
-//              coefficients from t0 = tanh(a0) (every derivative of tanh is
-//              a polynomial in tanh): the remainder stays below 2^-51.8,
-//              2^-46.8 relative at a = 2^-5;
+//   a < 1:     the degree-5 Taylor polynomial about a point a0 of a table of
+//              tanh(a0) (correctly rounded, gen_tanh_table.py): a0 = 0 for
+//              a < 1/128, where the polynomial is tanh's own series
+//              a - a^3/3 + 2a^5/15 (truncation below 0.054 a^7, 2^-46.2
+//              relative at most), else the interval's midpoint
+//              a0 = (k + 0.5) / 128, |d| = |a - a0| <= 2^-8; its coefficients
+//              come from t0 = tanh(a0) (every derivative of tanh is a
+//              polynomial in tanh), and the remainder stays below 2^-51.8,
+//              2^-44.8 relative at a = 2^-7;
 //   a < 22:    tanh a = 1 - 2 / (e + 1), e = e^(2a) = 2^n e^r with
 //              2a = n ln2 + r, |r| <= ln2 / 2, e^r by its Taylor polynomial
 //              to r^12 (truncation below 2e-16). The cancellation in 1 - q is
@@ -40,22 +41,9 @@ namespace mgm
 {
     constexpr double kTanhFastMargin = 0x1p-40;
 
-    // the branch of tanh_fast_abs for 0 <= a < 2^-5
-    MG_TF double tanh_series_abs(double a)
-    {
-        const double u = a * a;
-        // tanh x / x - 1 = u (-1/3 + u (2/15 + u (-17/315 + u (62/2835 + u (-1382/155925)))))
-        double p = -1382.0 / 155925.0;
-        p = __builtin_fma(p, u, 62.0 / 2835.0);
-        p = __builtin_fma(p, u, -17.0 / 315.0);
-        p = __builtin_fma(p, u, 2.0 / 15.0);
-        p = __builtin_fma(p, u, -1.0 / 3.0);
-        return __builtin_fma(a * u, p, a);
-    }
-
-    // tanh((k + 0.5) / 128), correctly rounded (gen_tanh_table.py)
+    // tanh((k + 0.5) / 128), correctly rounded, and tanh(0) at k = 0 (gen_tanh_table.py)
     alignas(16) inline constexpr double kTanhTab[128] = {
-        0x1.ffff555599998p-9, 0x1.7ffb801032f83p-7, 0x1.3ff595bd7be22p-6, 0x1.bfe36cdabb028p-6,
+        0x0.0p+0, 0x1.7ffb801032f83p-7, 0x1.3ff595bd7be22p-6, 0x1.bfe36cdabb028p-6,
         0x1.1fe1a3d7a86c8p-5, 0x1.5fc89524d876dp-5, 0x1.9fa48d7b18ff3p-5, 0x1.df73915eafd29p-5,
         0x1.0f99d37864afap-4, 0x1.2f716b16ebeacp-4, 0x1.4f3f9495ba795p-4, 0x1.6f03562adb372p-4,
         0x1.8ebbb755f29f5p-4, 0x1.ae67c0fe4418bp-4, 0x1.ce067d9059519p-4, 0x1.ed96f91b44398p-4,
@@ -89,7 +77,7 @@ namespace mgm
         0x1.7feedc40e9a52p-1, 0x1.81ac7117793c5p-1, 0x1.8364cf3dc77a5p-1, 0x1.8518007873dd0p-1,
     };
 
-    // the branch of tanh_fast_abs for 2^-5 <= a < 1 (d = a - a0 is exact):
+    // the branch of tanh_fast_abs for 0 <= a < 1 (d = a - a0 is exact):
     //   tanh(a0 + d) = t0 + (1 - t0^2) d [1 - t0 d + (t0^2 - 1/3) d^2
     //                  + t0 (2/3 - t0^2) d^3 + (2/15 - t0^2 + t0^4) d^4] + R
     // (tab: kTanhTab or a copy of it, e.g. in a work-group's shared memory)
@@ -97,7 +85,7 @@ namespace mgm
     {
         const int k = int(a * 128.0);
         const double t = tab[k], u = t * t;
-        const double d = a - (double(k) + 0.5) * 0x1p-7;
+        const double d = a - (k == 0 ? 0.0 : (double(k) + 0.5) * 0x1p-7); // interval 0: about 0
         double e = __builtin_fma(u, u - 1.0, 2.0 / 15.0);
         e = __builtin_fma(d, e, t * (2.0 / 3.0 - u));
         e = __builtin_fma(d, e, u - 1.0 / 3.0);
@@ -108,12 +96,7 @@ namespace mgm
 
     MG_TF double tanh_fast_abs(double a)
     {
-        if (a < 1.0) {
-            // both evaluated and one selected: no divergent branch on the GPU
-            // (the table index stays in range for every a < 1)
-            const double s = tanh_series_abs(a), t = tanh_table_abs(a);
-            return a < 0x1p-5 ? s : t;
-        }
+        if (a < 1.0) return tanh_table_abs(a); // the table index stays in range for every a < 1
         if (a >= 22.0) return 1.0;
         const double y = a + a;
         constexpr double kLog2e = 1.4426950408889634;     // 1 / ln 2
