@@ -1085,7 +1085,9 @@ namespace mg
                 const double a = __builtin_fabs(double(q));
                 const double ac = __builtin_fmin(a, 0x1.fffffffffffffp-1);
                 const double th = mgm::tanh_table_abs(ac, tab);
-                const auto lo = SI::enc64(th - th * mgm::kTanhFastMargin), hi = SI::enc64(th + th * mgm::kTanhFastMargin);
+                double tl, tu;
+                mgm::tanh_interval(th, tl, tu);
+                const auto lo = SI::enc64(tl), hi = SI::enc64(tu);
                 ok[e] = t.rcap != 0.0f && az > 0x1p-100f && az < 0x1p100f && a < 1.0 && lo == hi;
                 r[e] = SI::dec(SI::enc32(__builtin_copysignf(SI::dec(lo), q) * t.cap));
                 slow |= ok[e] ? 0u : 1u << e;

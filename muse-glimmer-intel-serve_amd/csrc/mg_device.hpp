@@ -135,7 +135,9 @@ namespace mg
         const double a = __builtin_fabs(double(v));
         if (a == a) {
             const double t = mgm::tanh_fast_abs(a);
-            const auto lo = S::enc64(t - t * mgm::kTanhFastMargin), hi = S::enc64(t + t * mgm::kTanhFastMargin);
+            double tl, th;
+            mgm::tanh_interval(t, tl, th);
+            const auto lo = S::enc64(tl), hi = S::enc64(th);
             if (lo == hi) return __builtin_copysignf(S::dec(lo), v);
         }
         return S::dec(S::enc64(tanh_fdlibm(double(v))));

@@ -94,6 +94,13 @@ namespace mgm
         return __builtin_fma((1.0 - u) * d, e, t);
     }
 
+    // the interval t (1 -+ m) that a caller rounds at both ends, one rounding each
+    MG_TF void tanh_interval(double t, double &lo, double &hi, double m = kTanhFastMargin)
+    {
+        lo = __builtin_fma(-t, m, t);
+        hi = __builtin_fma(t, m, t);
+    }
+
     MG_TF double tanh_fast_abs(double a)
     {
         if (a < 1.0) return tanh_table_abs(a); // the table index stays in range for every a < 1

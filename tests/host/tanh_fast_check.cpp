@@ -32,7 +32,8 @@ int main(int argc, char **argv)
         const double t = mgm::tanh_fast_abs(a) * (1.0 + perturb), r = orc::tanh(a);
         const double rel = r == 0.0 ? std::fabs(t - r) : std::fabs(t - r) / r;
         if (rel > maxrel) maxrel = rel;
-        const double lo = t - t * m, hi = t + t * m;
+        double lo, hi;
+        mgm::tanh_interval(t, lo, hi, m);
         if (float(lo) == float(hi)) {
             if (float(lo) != float(r)) ++bad;
         } else {
