@@ -185,15 +185,17 @@ namespace mg
         stage(vc, klo, sb);
         commit(lv[0], SV);
         __syncthreads();
-        float s[RT][KT][4];
-        scores(lk[0], s);
+        float sA[RT][KT][4], sB[RT][KT][4];
+        scores(lk[0], sA);
         if (klo + KS <= khi) {
             stage(kc, klo + KS, wrap(sb + KS));
             commit(lk[1], SK);
         }
         __syncthreads(); // K(1) is in lk[1]; every wave is done with lk[0]
         int cur = 0;
-        for (int64_t jb = klo; jb <= khi; jb += KS) {
+        // one step: S(j) in s, S(j+1) computed into sx; the loop below takes two
+        // steps a pass with the arrays swapped, so no copy carries S(j+1) over
+        auto step = [&](int64_t jb, float (&s)[RT][KT][4], float (&sx)[RT][KT][4]) {
             const int64_t s1 = wrap(sb + KS), s2 = wrap(s1 + KS);
             const bool more = jb + KS <= khi, more2 = jb + 2 * KS <= khi;
             if (more2) stage(kc, jb + 2 * KS, s2); // K(j+2), in flight through this step
@@ -213,7 +215,6 @@ namespace mg
             }
             // S(j+1) (from whatever lk[cur ^ 1] holds after the last step: in
             // bounds, unused), issued ahead of step j's softmax
-            float sx[RT][KT][4];
             scores(lk[cur ^ 1], sx);
             // online softmax per row; P for the p.v product, element 4(t%2) + r
             // of pair t/2 is key 16 t + 4c + r
@@ -232,15 +233,23 @@ namespace mg
                 // a row with nothing attended yet keeps a zero reference: its
                 // weights are 2^-inf = 0 and nothing is rescaled into NaN
                 const float mref = mn == -__builtin_huge_valf() ? 0.0f : mn;
-                float ps = 0.0f;
+                float ev[KT][4];
 #pragma unroll
                 for (int t = 0; t < KT; ++t)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][r], a.scale2, -mref));
-                        ps += e;
-                        pb[u][t / 2][4 * (t % 2) + r] = __bf16(e);
+                        ev[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][r], a.scale2, -mref));
+                        pb[u][t / 2][4 * (t % 2) + r] = __bf16(ev[t][r]);
                     }
+                // four partial sums: a short chain ahead of the barrier
+                float ps4[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    ps4[r] = ev[0][r];
+#pragma unroll
+                    for (int t = 1; t < KT; ++t) ps4[r] += ev[t][r];
+                }
+                const float ps = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
                 corr[u] = __builtin_amdgcn_exp2f(m[u] - mref);
                 moved |= mn != m[u];
                 l[u] = (mn != m[u] ? l[u] * corr[u] : l[u]) + ps;
@@ -277,14 +286,13 @@ namespace mg
                 }
             if (more) commit(lv[cur ^ 1], SV); // V(j+1) over V(j-1)
             __syncthreads(); // the next buffers are written; these are free again
-#pragma unroll
-            for (int u = 0; u < RT; ++u)
-#pragma unroll
-                for (int t = 0; t < KT; ++t)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) s[u][t][r] = sx[u][t][r];
             cur ^= 1;
             sb = s1;
+        };
+        for (int64_t jb = klo; jb <= khi; jb += 2 * KS) {
+            step(jb, sA, sB);
+            if (jb + KS > khi) break;
+            step(jb + KS, sB, sA);
         }
 
         // out = acc / sumexp, rows 4c + r of each tile from lanes 4c + r
