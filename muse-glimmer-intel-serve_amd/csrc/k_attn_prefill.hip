@@ -229,7 +229,13 @@ namespace mg
 #pragma unroll
                     for (int r = 0; r < 4; ++r) mx = __builtin_fmaxf(mx, s[u][t][r]);
                 mx = rows4_max(mx) * a.scale2;
-                const float mn = __builtin_fmaxf(m[u], mx);
+                // lazy reference: a row's reference moves only when its new
+                // maximum passes the old by more than 8 (log2 units), so its
+                // weights stay at most 2^8 (exact to scale in f32 and bf16)
+                // and most steps rescale nothing; a row with nothing attended
+                // yet (m = -inf) takes the first finite maximum
+                const bool mv = mx > m[u] + 8.0f;
+                const float mn = mv ? mx : m[u];
                 // a row with nothing attended yet keeps a zero reference: its
                 // weights are 2^-inf = 0 and nothing is rescaled into NaN
                 const float mref = mn == -__builtin_huge_valf() ? 0.0f : mn;
@@ -251,8 +257,8 @@ namespace mg
                 }
                 const float ps = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
                 corr[u] = __builtin_amdgcn_exp2f(m[u] - mref);
-                moved |= mn != m[u];
-                l[u] = (mn != m[u] ? l[u] * corr[u] : l[u]) + ps;
+                moved |= mv;
+                l[u] = (mv ? l[u] * corr[u] : l[u]) + ps;
                 m[u] = mn;
             }
             if (more2) commit(lk[cur], SK); // K(j+2) over K(j)

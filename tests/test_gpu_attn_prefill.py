@@ -101,6 +101,15 @@ def test_peaked_scores(prims):
     prefill_case(prims, 300, 8, 2, 128, 512, 0, scaling=1.0, seed=140)
 
 
+@pytest.mark.parametrize("scaling", (0.35, 0.6))
+def test_reference_kept_below_threshold(prims, scaling):
+    """a row's reference maximum moves only when a new maximum passes it by more
+    than 8 in log2 units; at these scalings the maxima of later steps often pass
+    the first one by a few units without moving it, so weights between 1 and 2^8
+    reach the sums and the p.v product"""
+    prefill_case(prims, 257, 8, 2, 128, 512, 0, scaling=scaling, seed=141)
+
+
 @pytest.mark.parametrize("scaling", (-1.0 / math.sqrt(128), -1.0, 0.0, 1e-30))
 def test_scaling_signs(prims, scaling):
     """the kernel multiplies by |scaling| inside the exponent: a negative
