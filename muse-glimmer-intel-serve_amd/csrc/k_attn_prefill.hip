@@ -17,16 +17,19 @@
 // Layout of the work: a work-group serves one KV head, 32 query rows and up to
 // 8 query heads of its GQA group (two waves per head, one per 16-row tile), so
 // every K/V tile staged in LDS is used by all of them; larger groups (16 for
-// 32 q / 2 kv heads) take several work-groups. Per 64-key step:
-//   staging   coalesced 16-byte loads of the next step's K and V (whole 256-
-//             byte key rows per instruction), held in registers while this
-//             step computes, then written to the other LDS buffer (padded
-//             rows, conflict-free reads); one barrier per step;
-//   S^T       A = 16 keys x 32 dims of K from LDS, B = the wave's 16 query
-//             rows (registers): C lane (query n, c) holds keys 4c..4c+3 of the
+// 32 q / 2 kv heads) take several work-groups. Per 64-key step j:
+//   staging   coalesced 16-byte loads (whole 256-byte key rows per
+//             instruction) of K(j+2) and V(j+1), held in registers while the
+//             step computes, then written to free LDS buffers (padded rows,
+//             conflict-free reads); one barrier per step;
+//   S^T       of step j + 1, computed ahead of step j's softmax: A = 16 keys
+//             x 32 dims of K from LDS, B = the wave's 16 query rows
+//             (registers): C lane (query n, c) holds keys 4c..4c+3 of the
 //             tile, four key tiles per step;
-//   softmax   per query row in f32 (hardware exp2 on log2-scaled scores), the
-//             row max and sum across the four lane groups by permlane swaps;
+//   softmax   per query row in f32 (hardware exp2 of fma(score, scale, -ref)),
+//             the row max and sum across the four lane groups by permlane
+//             swaps; a row's reference maximum moves only when passed by more
+//             than 8 (log2 units), so most steps rescale nothing;
 //   P V       A = P of two key tiles, straight from the S^T layout, B = V from
 //             LDS through the transposing ds_read_b64_tr_b16.
 // Work-groups of the last query tiles (the most keys) start first.
