@@ -90,6 +90,14 @@ def test_window_and_ring(prims):
     prefill_case(prims, 96, 16, 2, 64, 200, 0, window=33, seed=122)
 
 
+def test_window_ring_many_steps(prims):
+    """a 256-key window over a 600-slot ring, positions 1000..1299: nine 64-key
+    steps per tile, the ring wrapping (slot 0 again at key 1200) inside the
+    chunk, so steps staged two ahead straddle the wrap"""
+    prefill_case(prims, 300, 8, 2, 128, 600, 1000, window=256, seed=123)
+    prefill_case(prims, 300, 10, 2, 64, 600, 1000, window=200, seed=124)
+
+
 def test_short_and_ragged(prims):
     """one row, rows that end inside a 16-row tile, a 32-row tile boundary"""
     for T in (1, 15, 17, 31, 32, 33):
