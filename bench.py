@@ -77,6 +77,10 @@ BYTES = {
     "probe_read_256MiB": 256 << 20,
     "probe_write_256MiB": 256 << 20,
     "probe_2r2w_norm_shape": 4 * 2 * T * D,
+    # other forms of the same copy, to compare the primitives' pattern against
+    "probe_copy_cached_256MiB": 2 * (256 << 20),
+    "probe_copy_4vec_256MiB": 2 * (256 << 20),
+    "probe_copy_persistent_256MiB": 2 * (256 << 20),
 }
 BYTES["softmax_causal_softcap30"] = BYTES["softmax_causal"]
 # size-matched probes: an op's own byte count moved by the probe's pattern (a copy moves half
@@ -112,6 +116,9 @@ KERNEL_OF = {
     "probe_read_256MiB": "k_probe<1> (read)",
     "probe_write_256MiB": "k_probe<2> (write)",
     "probe_2r2w_norm_shape": "k_probe<3> (2 reads + 2 writes, the residual_rmsnorm traffic)",
+    "probe_copy_cached_256MiB": "k_probe<4> (copy, ordinary cached accesses)",
+    "probe_copy_4vec_256MiB": "k_probe_4vec (copy, four 16-byte words a thread)",
+    "probe_copy_persistent_256MiB": "k_probe_persist (copy, persistent grid of 2048 work-groups)",
 }
 for _p, (_op, _kind) in SIZED_PROBES.items():
     KERNEL_OF[_p] = f"k_probe<{0 if _kind == 'copy' else 1}> ({_kind}, {_op}'s bytes)"
@@ -221,6 +228,9 @@ def make_inputs(torch, P):
         "probe_read_256MiB": lambda: P.probe_stream(P.PROBE_READ, I["copy_src"], I["one"]),
         "probe_write_256MiB": lambda: P.probe_stream(P.PROBE_WRITE, None, I["copy_dst"]),
         "probe_2r2w_norm_shape": lambda: P.probe_stream(P.PROBE_2R2W, I["pa"], None, I["pc"], I["pd"]),
+        "probe_copy_cached_256MiB": lambda: P.probe_stream(P.PROBE_COPY_CACHED, I["copy_src"], I["copy_dst"]),
+        "probe_copy_4vec_256MiB": lambda: P.probe_stream(P.PROBE_COPY_4VEC, I["copy_src"], I["copy_dst"]),
+        "probe_copy_persistent_256MiB": lambda: P.probe_stream(P.PROBE_COPY_PERSISTENT, I["copy_src"], I["copy_dst"]),
     }
     for name, (_op, kind) in SIZED_PROBES.items():
         if kind == "copy":

@@ -245,7 +245,9 @@ int mg_gemv_q8_0(mg_ctx *ctx, const int8_t *qs, const uint16_t *d, const uint16_
  * (16-byte non-temporal loads and stores, one-shot grid) with no arithmetic:
  * kind 0 copies a to b; 1 reads a (b receives at most one word); 2 writes b;
  * 3 reads a and c and writes a = a + c and d = (a + c) ^ c, 32-bit words (the
- * residual-add + RMSNorm traffic shape). Buffers 16-byte aligned. */
+ * residual-add + RMSNorm traffic shape); 4, 5 and 6 copy a to b in other forms
+ * (ordinary cached accesses; four words a thread; a persistent grid-stride
+ * loop) to compare the pattern against. Buffers 16-byte aligned. */
 int mg_probe_stream(mg_ctx *ctx, int kind, void *a, void *b, const void *c, void *d, int64_t bytes);
 
 /* Per row of logits [rows, V] (dtype_in f32 or bf16; row r at logits + r * ld,

@@ -459,12 +459,14 @@ class Prims:
         self._check(rc)
 
     PROBE_COPY, PROBE_READ, PROBE_WRITE, PROBE_2R2W = 0, 1, 2, 3
+    PROBE_COPY_CACHED, PROBE_COPY_4VEC, PROBE_COPY_PERSISTENT = 4, 5, 6
 
     def probe_stream(self, kind, a=None, b=None, c=None, d=None):
         """HBM stream probe (a measurement aid, no reference counterpart): kind
         PROBE_COPY b = a, PROBE_READ reads a (b: a sink of >= 4 bytes),
         PROBE_WRITE fills b, PROBE_2R2W a = a + c and d = (a + c) ^ c over
-        32-bit words. The moved size is the first operand's byte count; the
+        32-bit words; PROBE_COPY_CACHED, PROBE_COPY_4VEC and
+        PROBE_COPY_PERSISTENT copy a to b in other forms. The moved size is the first operand's byte count; the
         others must hold as many bytes (contiguous, 16-byte aligned)."""
         ts = [t for t in (a, b, c, d) if t is not None]
         self._dev(*ts)

@@ -37,6 +37,22 @@ def test_copy_write_2r2w(prims):
     assert int(sink.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("kind", (M.Prims.PROBE_COPY_CACHED, M.Prims.PROBE_COPY_4VEC, M.Prims.PROBE_COPY_PERSISTENT))
+@pytest.mark.parametrize("n", (64, (1 << 20) + 256, (9 << 20) + 4))
+def test_other_copy_forms(prims, kind, n):
+    """the cached, four-words-a-thread and persistent copies move every word:
+    sizes below one work-group's span, past a whole number of spans, and above
+    the persistent grid's 2048 groups x 256 words (so its loop runs twice)"""
+    import torch
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(6)
+    a = torch.randint(0, 2 ** 31 - 1, (n,), generator=g, device="cuda:0", dtype=torch.int32)
+    b = torch.zeros(n + 8, dtype=torch.int32, device="cuda:0")
+    prims.probe_stream(kind, a, b)
+    assert torch.equal(b[:n], a)
+    assert int(b[n:].abs().sum()) == 0  # nothing past the moved size
+
+
 def test_errors(prims):
     import torch
     a = torch.zeros(64, dtype=torch.int32, device="cuda:0")
