@@ -107,7 +107,7 @@ KERNEL_OF = {
     "quantize_q8_0": "k_quantize_q8_0",
     "attn_decode_131072": "k_attn_split<5,4> + k_attn_combine",
     "gemv_q8_0_decode": "k_gemv_q8_0<1>",
-    "vocab_tail_top64_dist": "k_vocab_tail_map + k_vocab_chunk + k_vocab_merge + k_sample_dist",
+    "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
     "attn_prefill_4096": "k_attn_prefill<5,4,1,4>",
     "softmax_causal_softcap30": "k_softmax_fast<cap>",
     "copy_256MiB": "torch copy (memory-only probe)",

@@ -342,11 +342,49 @@ namespace mg
 
     // ------------------------------------------------------------------ pass 1
 
+    // The tail on VW stored values side by side: the common path (|z / cap| < 1
+    // with a certain rounding) branch-free, a wave with any value outside it
+    // through vtail for those values. z: decoded inputs in, stored results out.
+    template <class SI, int VW>
+    MG_DEV void tail_vec(float (&z)[VW], const VTail &t, const double *tab)
+    {
+        if (t.cap == 0.0f) {
+#pragma unroll
+            for (int e = 0; e < VW; ++e) z[e] = vtail<SI>(z[e], t);
+            return;
+        }
+        float r[VW];
+        uint32_t slow = 0;
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+            float w = z[e];
+            if (t.mult != 1.0f) w = SI::dec(SI::enc32(w * t.mult));
+            const float az = __builtin_fabsf(w);
+            const float q = SI::dec(SI::enc32(mgm::softcap_quotient(w, t.cap, t.rcap)));
+            const double a = __builtin_fabs(double(q));
+            const double ac = __builtin_fmin(a, 0x1.fffffffffffffp-1);
+            const double th = mgm::tanh_table_abs(ac, tab);
+            double tl, tu;
+            mgm::tanh_interval(th, tl, tu);
+            const auto lo = SI::enc64(tl), hi = SI::enc64(tu);
+            const bool ok = t.rcap != 0.0f && az > 0x1p-100f && az < 0x1p100f && a < 1.0 && lo == hi;
+            r[e] = SI::dec(SI::enc32(__builtin_copysignf(SI::dec(lo), q) * t.cap));
+            slow |= ok ? 0u : 1u << e;
+        }
+        if (__builtin_amdgcn_ballot_w64(slow != 0) != 0) {
+#pragma unroll
+            for (int e = 0; e < VW; ++e)
+                if ((slow >> e) & 1u) r[e] = vtail<SI>(z[e], t);
+        }
+#pragma unroll
+        for (int e = 0; e < VW; ++e) z[e] = r[e];
+    }
+
     // A chunk's logits as f32 bit patterns (past V: -inf, which no sum, max or
     // candidate takes), tail-transformed and optionally written back
     template <class SI, int VW, bool TAIL>
     MG_DEV void chunk_load(const typename SI::raw *__restrict__ xr, int nvalid, const VTail &tail,
-                           typename SI::raw *orow, uint32_t (&xb)[kVLane])
+                           typename SI::raw *orow, uint32_t (&xb)[kVLane], const double *tab)
     {
         using raw = typename SI::raw;
         const int lane = threadIdx.x & 63;
@@ -357,8 +395,12 @@ namespace mg
 #pragma unroll
                 for (int i = 0; i < kVLane / VW; ++i) {
                     const Vec<raw, VW> v = ld16_stream<raw, VW>(xr + VW * lane + 64 * VW * i);
+                    float z[VW];
 #pragma unroll
-                    for (int e = 0; e < VW; ++e) xb[VW * i + e] = __builtin_bit_cast(uint32_t, float(SI::dec(v.v[e])));
+                    for (int e = 0; e < VW; ++e) z[e] = float(SI::dec(v.v[e]));
+                    if constexpr (TAIL && (SI::dt == F32 || SI::dt == BF16)) tail_vec<SI, VW>(z, tail, tab);
+#pragma unroll
+                    for (int e = 0; e < VW; ++e) xb[VW * i + e] = __builtin_bit_cast(uint32_t, z[e]);
                 }
                 loaded = true;
             }
@@ -371,10 +413,11 @@ namespace mg
             }
         }
         if constexpr (TAIL) {
+            if (!loaded || !(SI::dt == F32 || SI::dt == BF16)) // (else the vectors took it as they arrived)
 #pragma unroll
-            for (int s = 0; s < kVLane; ++s)
-                if (full || voff<VW>(lane, s) < nvalid)
-                    xb[s] = __builtin_bit_cast(uint32_t, vtail<SI>(__builtin_bit_cast(float, xb[s]), tail));
+                for (int s = 0; s < kVLane; ++s)
+                    if (full || voff<VW>(lane, s) < nvalid)
+                        xb[s] = __builtin_bit_cast(uint32_t, vtail<SI>(__builtin_bit_cast(float, xb[s]), tail));
             if (orow) {
                 bool stored = false;
                 if constexpr (VW > 1) {
@@ -446,7 +489,7 @@ namespace mg
     template <class SI, int VW, bool TAIL>
     MG_DEV void chunk_pass(const typename SI::raw *__restrict__ L, int64_t ld, int64_t V, int K, int nch,
                            VPart *__restrict__ part, uint64_t *__restrict__ blk, const VTail &tail, int ch,
-                           int64_t row, uint32_t *sb, uint32_t *so, uint64_t *sel)
+                           int64_t row, uint32_t *sb, uint32_t *so, uint64_t *sel, const double *tab)
     {
         using raw = typename SI::raw;
         const int lane = threadIdx.x & 63;
@@ -455,7 +498,7 @@ namespace mg
         uint32_t xb[kVLane];
         auto x = [&](int s) { return __builtin_bit_cast(float, xb[s]); };
         chunk_load<SI, VW, TAIL>(L + row * ld + cb, nvalid, tail,
-                                 tail.out ? static_cast<raw *>(tail.out) + row * V + cb : nullptr, xb);
+                                 tail.out ? static_cast<raw *>(tail.out) + row * V + cb : nullptr, xb, tab);
 
         // lane maximum over the non-NaN entries (fmax passes NaN's partner on)
         float m1 = -__builtin_huge_valf();
@@ -566,7 +609,13 @@ namespace mg
     {
         __shared__ uint32_t sb[kCand], so[kCand];
         __shared__ uint64_t sel[kCand];
-        chunk_pass<SI, VW, TAIL>(L, ld, V, K, nch, part, blk, tail, int(blockIdx.x), blockIdx.y, sb, so, sel);
+        __shared__ __align__(16) double tab[TAIL ? 128 : 2]; // the tanh table, read at random: LDS, not the cache
+        if constexpr (TAIL) {
+            *reinterpret_cast<Vec<double, 2> *>(tab + 2 * (threadIdx.x & 63)) =
+                *reinterpret_cast<const Vec<double, 2> *>(mgm::kTanhTab + 2 * (threadIdx.x & 63));
+            wave_lds_sync();
+        }
+        chunk_pass<SI, VW, TAIL>(L, ld, V, K, nch, part, blk, tail, int(blockIdx.x), blockIdx.y, sb, so, sel, tab);
     }
 
     // ------------------------------------------------------------------ pass 2
@@ -693,7 +742,7 @@ namespace mg
         const int lane = threadIdx.x & 63;
         uint32_t xb[kVLane];
         auto x = [&](int s) { return __builtin_bit_cast(float, xb[s]); };
-        chunk_load<SI, VW, TAIL>(xr, nvalid, tail, nullptr, xb);
+        chunk_load<SI, VW, TAIL>(xr, nvalid, tail, nullptr, xb, mgm::kTanhTab); // (rare: the table from memory)
         float m1 = -__builtin_huge_valf();
 #pragma unroll
         for (int s = 0; s < kVLane; ++s) m1 = __builtin_fmaxf(m1, x(s));
@@ -1045,64 +1094,6 @@ namespace mg
     }
 
 
-    // The output tail alone: out[r, j] = vtail(in[r, j]) at storage, one
-    // 16-byte vector per thread (grid: vectors of a row x rows). The vector's
-    // values go through the steps side by side with no branch on the common
-    // path (|z / cap| < 1: the table polynomial of tanh_fast_abs,
-    // and the rounding test of tanh_stored), so their f64 chains overlap; a
-    // wave with a value outside (|z / cap| >= 1, inf, NaN, an uncertain
-    // rounding) runs vtail's own path for those values. Run ahead of the vocab
-    // pass when the transformed logits have somewhere to go, so the pass's
-    // chunk kernel does not carry the tail's registers.
-    template <class SI, int VW>
-    __global__ __launch_bounds__(256) void k_vocab_tail_map(const typename SI::raw *__restrict__ in, int64_t ld,
-                                                            typename SI::raw *__restrict__ out, int64_t V, VTail t)
-    {
-        using raw = typename SI::raw;
-        __shared__ __align__(16) double tab[128]; // the tanh table, read at random: LDS, not the cache
-        if (threadIdx.x < 64)
-            *reinterpret_cast<Vec<double, 2> *>(tab + 2 * threadIdx.x) =
-                *reinterpret_cast<const Vec<double, 2> *>(mgm::kTanhTab + 2 * threadIdx.x);
-        __syncthreads();
-        const int64_t row = blockIdx.y;
-        const int64_t j = (int64_t(blockIdx.x) * 256 + threadIdx.x) * VW;
-        if (j >= V) return;
-        Vec<raw, VW> v = ld16_stream<raw, VW>(in + row * ld + j);
-        if (t.cap == 0.0f) {
-#pragma unroll
-            for (int e = 0; e < VW; ++e) v.v[e] = SI::enc32(vtail<SI>(float(SI::dec(v.v[e])), t));
-        } else {
-            float z[VW], r[VW];
-            bool ok[VW];
-            uint32_t slow = 0;
-#pragma unroll
-            for (int e = 0; e < VW; ++e) {
-                z[e] = float(SI::dec(v.v[e]));
-                if (t.mult != 1.0f) z[e] = SI::dec(SI::enc32(z[e] * t.mult));
-                const float az = __builtin_fabsf(z[e]);
-                // Markstein's quotient where it is certain (see vtail)
-                const float q = SI::dec(SI::enc32(mgm::softcap_quotient(z[e], t.cap, t.rcap)));
-                const double a = __builtin_fabs(double(q));
-                const double ac = __builtin_fmin(a, 0x1.fffffffffffffp-1);
-                const double th = mgm::tanh_table_abs(ac, tab);
-                double tl, tu;
-                mgm::tanh_interval(th, tl, tu);
-                const auto lo = SI::enc64(tl), hi = SI::enc64(tu);
-                ok[e] = t.rcap != 0.0f && az > 0x1p-100f && az < 0x1p100f && a < 1.0 && lo == hi;
-                r[e] = SI::dec(SI::enc32(__builtin_copysignf(SI::dec(lo), q) * t.cap));
-                slow |= ok[e] ? 0u : 1u << e;
-            }
-            if (__builtin_amdgcn_ballot_w64(slow != 0) != 0) {
-#pragma unroll
-                for (int e = 0; e < VW; ++e)
-                    if ((slow >> e) & 1u) r[e] = vtail<SI>(float(SI::dec(v.v[e])), t);
-            }
-#pragma unroll
-            for (int e = 0; e < VW; ++e) v.v[e] = SI::enc32(r[e]);
-        }
-        st16_stream<raw, VW>(out + row * V + j, v);
-    }
-
     // RN(1 / cap) where the tail takes Markstein's quotient (1 <= |cap| <= 2^20:
     // with 2^-100 < |v| < 2^100 the quotient and the remainder stay normal)
     static float tail_rcap(double cap)
@@ -1136,32 +1127,6 @@ namespace mg
         need(need_bytes <= work_bytes, "vocab_reduce: the partials of " + std::to_string(rows) + " rows x " +
                                            std::to_string(nch) + " chunks need " + std::to_string(need_bytes) +
                                            " bytes, more than " + room + " (" + std::to_string(work_bytes) + ")");
-        // The tail as its own elementwise pass (k_vocab_tail_map) wherever its
-        // output has somewhere to go — logits_out, else room in the workspace
-        // past the partials — then the plain pass over the transformed logits:
-        // the same values (vtail in both), without the tail's registers in the
-        // chunk kernel. Otherwise the chunk kernel applies the tail itself.
-        if (tail_on && (dt_in == F32 || dt_in == BF16)) {
-            const int64_t esz = dt_in == F32 ? 4 : 2, vw = 16 / esz;
-            const int64_t tmp_off = (need_bytes + 255) / 256 * 256;
-            void *dst = logits_out ? logits_out
-                                   : (tmp_off + rows * V * esz <= work_bytes ? static_cast<char *>(work) + tmp_off
-                                                                              : nullptr);
-            if (dst && V % vw == 0 && ld % vw == 0 && aligned16(logits) && aligned16(dst)) {
-                const VTail t{float(mult), float(cap), nullptr, tail_rcap(cap)};
-                const dim3 gm{unsigned((V / vw + 255) / 256), unsigned(rows), 1u};
-                if (dt_in == F32)
-                    hipLaunchKernelGGL((k_vocab_tail_map<SF32, 4>), gm, dim3(256), 0, stream,
-                                       static_cast<const float *>(logits), ld, static_cast<float *>(dst), V, t);
-                else
-                    hipLaunchKernelGGL((k_vocab_tail_map<SBf16, 8>), gm, dim3(256), 0, stream,
-                                       static_cast<const uint16_t *>(logits), ld, static_cast<uint16_t *>(dst), V, t);
-                check_launch("k_vocab_tail_map");
-                vocab_pass(stream, work, tmp_off, room, dst, V, rows, V, dt_in, K, lse, amax, top_idx, top_val, false,
-                           1.0, 0.0, nullptr);
-                return;
-            }
-        }
         VPart *part = static_cast<VPart *>(work);
         uint64_t *blk = reinterpret_cast<uint64_t *>(static_cast<char *>(work) + part_bytes);
         uint64_t *lst = blk + nc * kBlk;

@@ -280,11 +280,12 @@ def test_vocab_tail_fused_in_the_pass(prims, rows, V, out):
 
 @pytest.mark.parametrize("dt", (F32, BF16))
 @pytest.mark.parametrize("mult,cap", ((1.0, 30.0), (1.0, 0.75), (1.0, 3.0e6), (0.5, 1.0), (3.0, 7.5)))
-def test_vocab_tail_map_special_values(prims, dt, mult, cap):
-    """the tail's own pass on values off its common path: inf, NaN, signed
-    zeros, subnormals, magnitudes at the quotient's 2^-100 / 2^100 guards,
-    |z / cap| at the 2^-5 and 1 branch points, and caps outside [1, 2^20]
-    (the IEEE quotient), bitwise against the oracle's output tail"""
+def test_vocab_tail_special_values(prims, dt, mult, cap):
+    """the tail's side-by-side chain (applied as the chunk pass loads its
+    vectors) on values off its common path: inf, NaN, signed zeros,
+    subnormals, magnitudes at the quotient's 2^-100 / 2^100 guards, |z / cap|
+    at the table's segment 0 and at 1, and caps outside [1, 2^20] (the IEEE
+    quotient), bitwise against the oracle's output tail"""
     import torch
     V = 4096
     rng = np.random.default_rng(91)
