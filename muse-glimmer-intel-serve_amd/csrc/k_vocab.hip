@@ -393,14 +393,19 @@ namespace mg
         if constexpr (VW > 1) {
             if (full) {
 #pragma unroll
-                for (int i = 0; i < kVLane / VW; ++i) {
-                    const Vec<raw, VW> v = ld16_stream<raw, VW>(xr + VW * lane + 64 * VW * i);
-                    float z[VW];
+                for (int i = 0; i < kVLane / VW; i += 2) {
+                    float z[2 * VW];
 #pragma unroll
-                    for (int e = 0; e < VW; ++e) z[e] = float(SI::dec(v.v[e]));
-                    if constexpr (TAIL && (SI::dt == F32 || SI::dt == BF16)) tail_vec<SI, VW>(z, tail, tab);
+                    for (int g = 0; g < 2; ++g) {
+                        const Vec<raw, VW> v = ld16_stream<raw, VW>(xr + VW * lane + 64 * VW * (i + g));
 #pragma unroll
-                    for (int e = 0; e < VW; ++e) xb[VW * i + e] = __builtin_bit_cast(uint32_t, z[e]);
+                        for (int e = 0; e < VW; ++e) z[VW * g + e] = float(SI::dec(v.v[e]));
+                    }
+                    // two vectors at a time through the tail: eight or sixteen
+                    // independent f64 chains hide each other's latency
+                    if constexpr (TAIL && (SI::dt == F32 || SI::dt == BF16)) tail_vec<SI, 2 * VW>(z, tail, tab);
+#pragma unroll
+                    for (int e = 0; e < 2 * VW; ++e) xb[VW * i + e] = __builtin_bit_cast(uint32_t, z[e]);
                 }
                 loaded = true;
             }
