@@ -73,6 +73,29 @@ def test_tree_bf16_within_ulp(prims, kind, dim):
     check_lp(y, y_ref, BF16)
 
 
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("rows", (257, 4096))
+def test_tree_bf16_bitwise_on_exact_sums(prims, kind, rows):
+    """Rows of multiples of 1/16 up to 4 in magnitude: h + x and every sum of
+    squares is exact in any order, so rs is the twin's to the bit and each
+    bf16 output must equal the twin's chain (f64 product, f64 -> f32 -> bf16).
+    The kernel forms y in f32 first and keeps it only away from bf16 rounding
+    midpoints; with random rs and w the f32 results' low halves cover the
+    midpoint neighbourhood (rejected or accepted) some hundreds of times."""
+    rng = np.random.default_rng(90 + kind)
+    dim = 5120
+    h = rng.integers(-32, 33, (rows, dim)) / 16.0
+    x = rng.integers(-32, 33, (rows, dim)) / 16.0
+    ws, w = storage(93 + kind, (dim,), BF16, 1.0, 0.05)
+    dh, dx, dw = to_dev(O.from_f64(h, BF16), BF16), to_dev(O.from_f64(x, BF16), BF16), to_dev(ws, BF16)
+    dy = to_dev(np.zeros((rows, dim), np.uint16), BF16)
+    eps = 1e-6
+    prims.residual_rmsnorm(kind, dh, dx, None if kind == O.WEIGHTLESS else dw, eps, dy)
+    y_ref, h_ref = O.residual_rmsnorm(kind, h, x, w, eps, BF16)
+    assert same_bits(from_dev(dh, BF16), O.from_f64(h_ref, BF16))
+    assert same_bits(from_dev(dy, BF16), O.from_f64(y_ref, BF16))
+
+
 @pytest.mark.parametrize("T", (1, 2, 3, 4, 8, 16, 32, 64))
 def test_decode_shapes(prims, T):
     y, hn, y_ref, h_ref = run_residual_norm(prims, O.PLAIN, T, 5120, BF16, seed=31)
