@@ -96,7 +96,7 @@ PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 STEP_OPS = ("residual_rmsnorm", "swiglu", "softmax_causal")
 KERNEL_OF = {
     # the step ops name their kernel as the traffic summary does (template arguments included)
-    "residual_rmsnorm": "k_norm_tree<mg::SBf16,8,2,false>",
+    "residual_rmsnorm": "k_norm_row<mg::SBf16,2,true,true,false>",
     "swiglu": "k_gate_lut<mg::SBf16>",
     "softmax_causal": "k_softmax_fast<mg::SBf16,4,false,true>",
     "rope": "k_rope",
@@ -243,7 +243,7 @@ def make_inputs(torch, P):
         ops[f"residual_rmsnorm_T{t}"] = (lambda t=t: P.residual_rmsnorm(
             M.PLAIN, I["hdec"][:t], I["xdec"][:t], I["w"], 1e-6, I["ydec"][:t]))
         BYTES[f"residual_rmsnorm_T{t}"] = 4 * 2 * t * D + 2 * D
-        KERNEL_OF[f"residual_rmsnorm_T{t}"] = "k_norm_tree"
+        KERNEL_OF[f"residual_rmsnorm_T{t}"] = "k_norm_row"
     return ops
 
 

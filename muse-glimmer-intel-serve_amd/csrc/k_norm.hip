@@ -16,11 +16,12 @@
 //               mean_sq's eight interleaved f64 accumulators in its exact order
 //               and combine them with its tree (src/muse_glimmer.hpp:509-527),
 //               so the result is bit-identical to the twin in every dtype.
-//   dim  > 128  k_norm_tree: one work-group per row, the row held in registers
-//               (16-byte loads), f64 sum of squares reduced in a fixed
-//               lane/wave order (deterministic, within 1e-16 relative of the
-//               twin's order; the bf16 output equals the twin's except where
-//               x*rs*w lies within that distance of a rounding boundary).
+//   dim  > 128  k_norm_row (rows of 16-byte multiples, 16-byte aligned) or
+//               k_norm_tree (others): one work-group per row, the row held in
+//               registers, f64 sum of squares reduced in a fixed lane/wave
+//               order (deterministic, within 1e-16 relative of the twin's
+//               order; the bf16 output equals the twin's except where x*rs*w
+//               lies within that distance of a rounding boundary).
 // f64 storage with the f32-compat flag takes k_norm_f32compat, the
 // reference's --hf-f32-compat branch bit for bit (see the kernel).
 #include "mg_device.hpp"
@@ -136,12 +137,16 @@ namespace mg
         const int nchunk = dim / VEC;
 
         comp v[CPT][VEC];
-        Vec<raw, VEC> wpre[CPT];
-        if constexpr (WPRE) {
+        Vec<raw, VEC> wv[CPT], hv[CPT], xv[CPT];
+        // every load of the row is issued before the first store: a store
+        // between two loads would make each chunk its own round trip
 #pragma unroll
-            for (int c = 0; c < CPT; ++c) {
-                const int ch = threadIdx.x + c * blockDim.x;
-                if (ch < nchunk && kind != 2) wpre[c] = *reinterpret_cast<const Vec<raw, VEC> *>(w + ch * VEC);
+        for (int c = 0; c < CPT; ++c) {
+            const int ch = threadIdx.x + c * blockDim.x;
+            if (ch < nchunk) {
+                hv[c] = ldv<raw, VEC>(hr + ch * VEC);
+                if (xr) xv[c] = ldv<raw, VEC>(xr + ch * VEC);
+                if (WPRE && kind != 2) wv[c] = *reinterpret_cast<const Vec<raw, VEC> *>(w + ch * VEC);
             }
         }
         double ss = 0.0;
@@ -149,11 +154,10 @@ namespace mg
         for (int c = 0; c < CPT; ++c) {
             const int ch = threadIdx.x + c * blockDim.x;
             if (ch < nchunk) {
-                Vec<raw, VEC> a = ldv<raw, VEC>(hr + ch * VEC);
+                Vec<raw, VEC> a = hv[c];
                 if (xr) {
-                    const Vec<raw, VEC> b = ldv<raw, VEC>(xr + ch * VEC);
 #pragma unroll
-                    for (int e = 0; e < VEC; ++e) a.v[e] = S::enc(S::dec(a.v[e]) + S::dec(b.v[e]));
+                    for (int e = 0; e < VEC; ++e) a.v[e] = S::enc(S::dec(a.v[e]) + S::dec(xv[c].v[e]));
                     stv<raw, VEC>(hr + ch * VEC, a);
                 }
 #pragma unroll
@@ -167,18 +171,89 @@ namespace mg
         const double tot = block_sum(ss, part);
         const double rs = 1.0 / __builtin_sqrt(tot / double(dim) + eps);
 
+        if constexpr (!WPRE) {
+#pragma unroll
+            for (int c = 0; c < CPT; ++c) {
+                const int ch = threadIdx.x + c * blockDim.x;
+                if (ch < nchunk && kind != 2) wv[c] = *reinterpret_cast<const Vec<raw, VEC> *>(w + ch * VEC);
+            }
+        }
 #pragma unroll
         for (int c = 0; c < CPT; ++c) {
             const int ch = threadIdx.x + c * blockDim.x;
             if (ch < nchunk) {
-                Vec<raw, VEC> wv;
-                if (kind != 2) wv = WPRE ? wpre[c] : *reinterpret_cast<const Vec<raw, VEC> *>(w + ch * VEC);
                 Vec<raw, VEC> o;
 #pragma unroll
                 for (int e = 0; e < VEC; ++e)
-                    o.v[e] = S::enc64(norm_out(kind, double(v[c][e]), rs, kind != 2 ? double(S::dec(wv.v[e])) : 0.0));
+                    o.v[e] = S::enc64(norm_out(kind, double(v[c][e]), rs, kind != 2 ? double(S::dec(wv[c].v[e])) : 0.0));
                 stv<raw, VEC>(yr + ch * VEC, o);
             }
+        }
+    }
+
+    // The 16-byte path of k_norm_tree (rows of a multiple of 16 bytes, 16-byte
+    // aligned): the same arithmetic, every access a raw buffer access over the
+    // row, so threads past the row read zeros (adding nothing to the sum) and
+    // store nothing, and no memory access sits behind a branch. All of a row's
+    // loads (h, x and, with WPRE, w) are issued before its first store; w is
+    // otherwise requested right after the sum, all chunks at once. RES: x
+    // given (the fused residual add); WGT: a weighted kind.
+    template <class S, int CPT, bool RES, bool WGT, bool WPRE>
+    __global__ __launch_bounds__(1024) void k_norm_row(int kind, typename S::raw *h,
+                                                       const typename S::raw *__restrict__ x, int64_t ldh,
+                                                       int64_t ldx, const typename S::raw *__restrict__ w,
+                                                       double eps, typename S::raw *y, int64_t ldy, int dim)
+    {
+        using raw = typename S::raw;
+        using comp = typename S::comp;
+        constexpr int VEC = 16 / sizeof(raw);
+        __shared__ double part[16];
+        const int64_t row = blockIdx.x;
+        const int bytes = dim * int(sizeof(raw));
+        const auto rh = buf_rsrc(h + row * ldh, bytes);
+        const auto rx = buf_rsrc(RES ? x + row * ldx : h, bytes);
+        const auto rw = buf_rsrc(WGT ? w : h, bytes);
+        const auto ry = buf_rsrc(y + row * ldy, bytes);
+
+        Vec<raw, VEC> hv[CPT], xv[CPT], wv[CPT];
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int off = (int(threadIdx.x) + c * int(blockDim.x)) * 16;
+            hv[c] = buf_ld16<raw, VEC, kAuxNT>(rh, off);
+            if constexpr (RES) xv[c] = buf_ld16<raw, VEC, kAuxNT>(rx, off);
+            if constexpr (WGT && WPRE) wv[c] = buf_ld16<raw, VEC, 0>(rw, off);
+        }
+        comp v[CPT][VEC];
+        double ss = 0.0;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int off = (int(threadIdx.x) + c * int(blockDim.x)) * 16;
+            if constexpr (RES) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) hv[c].v[e] = S::enc(S::dec(hv[c].v[e]) + S::dec(xv[c].v[e]));
+                buf_st16<raw, VEC, kAuxNT>(rh, off, hv[c]);
+            }
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                v[c][e] = S::dec(hv[c].v[e]);
+                const double d = double(v[c][e]);
+                ss += d * d;
+            }
+        }
+        const double tot = block_sum(ss, part);
+        const double rs = 1.0 / __builtin_sqrt(tot / double(dim) + eps);
+        if constexpr (WGT && !WPRE) {
+#pragma unroll
+            for (int c = 0; c < CPT; ++c)
+                wv[c] = buf_ld16<raw, VEC, 0>(rw, (int(threadIdx.x) + c * int(blockDim.x)) * 16);
+        }
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            Vec<raw, VEC> o;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e)
+                o.v[e] = S::enc64(norm_out(kind, double(v[c][e]), rs, WGT ? double(S::dec(wv[c].v[e])) : 0.0));
+            buf_st16<raw, VEC, kAuxNT>(ry, (int(threadIdx.x) + c * int(blockDim.x)) * 16, o);
         }
     }
 
@@ -276,6 +351,36 @@ namespace mg
                                static_cast<raw *>(h), static_cast<const raw *>(x), ldh, ldx,
                                static_cast<const raw *>(w), eps, static_cast<raw *>(y), ldy, dim);
         };
+        if constexpr (VEC * sizeof(raw) == 16) {
+            // the branch-free buffer form; <= 2^31 bytes a row (dim <= 2^20 is checked)
+            auto row = [&](auto res, auto wgt, auto wpre) {
+                constexpr bool R = decltype(res)::value, G = decltype(wgt)::value, P = decltype(wpre)::value;
+                switch (cpt) {
+                case 1: args(k_norm_row<S, 1, R, G, P>); break;
+                case 2: args(k_norm_row<S, 2, R, G, P>); break;
+                case 4: args(k_norm_row<S, 4, R, G, P>); break;
+                case 8: args(k_norm_row<S, 8, R, G, P>); break;
+                default: args(k_norm_row<S, 16, R, G, P>); break;
+                }
+            };
+            auto pre = [&](auto res, auto wgt) {
+                if (rows <= kPrefetchRows)
+                    row(res, wgt, std::true_type{});
+                else
+                    row(res, wgt, std::false_type{});
+            };
+            auto wgt = [&](auto res) {
+                if (kind != 2)
+                    pre(res, std::true_type{});
+                else
+                    pre(res, std::false_type{});
+            };
+            if (x)
+                wgt(std::true_type{});
+            else
+                wgt(std::false_type{});
+            check_launch("k_norm_row");
+        } else {
         auto pick = [&](auto wpre) {
             constexpr bool P = decltype(wpre)::value;
             switch (cpt) {
@@ -291,6 +396,7 @@ namespace mg
         else
             pick(std::false_type{});
         check_launch("k_norm_tree");
+        }
     }
 
     template <class S>

@@ -247,6 +247,10 @@ namespace mg
     //
     // One row of the fast path in a wave's registers: lane `lane` holds keys
     // 512 c + 8 lane + e, raw scores until fast_finish transforms them.
+    // key of element e of chunk c in lane `lane`: two runs of 4 keys, 256 apart,
+    // so each 16-byte load instruction of the wave covers 1 KiB contiguously
+    MG_DEV int fast_key(int c, int e, int lane) { return c * 512 + (e >> 2) * 256 + lane * 4 + (e & 3); }
+
     template <int CH>
     struct FastRow
     {
@@ -281,10 +285,11 @@ namespace mg
                 __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(xr), short(0), (hi + 1) * 4, 0x00020000);
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
-                const int j0 = c * 512 + lane * 8;
-                const int off = j0 + 7 >= lo ? j0 * 4 : 0x40000000;
-                const u32x4 p = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2); // 2: non-temporal
-                const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, 2);
+                const int ja = c * 512 + lane * 4, jb = ja + 256;
+                const int offa = ja + 3 >= lo ? ja * 4 : 0x40000000;
+                const int offb = jb + 3 >= lo ? jb * 4 : 0x40000000;
+                const u32x4 p = __builtin_amdgcn_raw_buffer_load_b128(rs, offa, 0, 2); // 2: non-temporal
+                const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, offb, 0, 2);
                 // (element to a prvalue first: this clang lowers bit_cast of an
                 // ext_vector element lvalue to a read of element 0)
 #pragma unroll
@@ -296,9 +301,11 @@ namespace mg
         } else {
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
-                const int j0 = c * 512 + lane * 8;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) r.v[c][e] = (j0 + e >= lo && j0 + e <= hi) ? xr[j0 + e] : 0.0f;
+                for (int e = 0; e < 8; ++e) {
+                    const int j = fast_key(c, e, lane);
+                    r.v[c][e] = (j >= lo && j <= hi) ? xr[j] : 0.0f;
+                }
             }
         }
     }
@@ -316,7 +323,7 @@ namespace mg
         float m = kNegInf;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            const int cb = c * 512, j0 = cb + lane * 8;
+            const int cb = c * 512;
             if (cb > hi || cb + 511 < lo) continue;
             if (cb >= lo && cb + 511 <= hi) {
                 if constexpr (CAP) cap8(a, r.v[c], 0xffu);
@@ -325,7 +332,7 @@ namespace mg
                 // skipped every chunk above, so here 0 <= hi - lo < kc
                 uint32_t vis = 0;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vis |= uint32_t(unsigned(j0 + e - lo) <= unsigned(hi - lo)) << e;
+                for (int e = 0; e < 8; ++e) vis |= uint32_t(unsigned(fast_key(c, e, lane) - lo) <= unsigned(hi - lo)) << e;
                 if constexpr (CAP) {
                     cap8(a, r.v[c], vis);
                 } else {
@@ -357,18 +364,25 @@ namespace mg
         const float inv = m == kNegInf ? 0.0f : __builtin_amdgcn_rcpf(sum);
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            const int cb = c * 512, j0 = cb + lane * 8;
-            if (j0 >= kc) continue;
+            const int cb = c * 512;
             const bool none = m == kNegInf || cb > hi || cb + 511 < lo;
-            Vec<ro, 8> o;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o.v[e] = none ? ro(0) : SO::enc_finite(r.v[c][e] * inv);
-            if (vec && j0 + 8 <= kc) {
-                st16_stream<ro, 8>(yr + j0, o);
-            } else {
+            for (int hh = 0; hh < 2; ++hh) {
+                const int j0 = cb + hh * 256 + lane * 4;
+                if (j0 >= kc) continue;
+                Vec<ro, 4> o;
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (j0 + e < kc) yr[j0 + e] = o.v[e];
+                for (int e = 0; e < 4; ++e) o.v[e] = none ? ro(0) : SO::enc_finite(r.v[c][4 * hh + e] * inv);
+                if (vec && j0 + 4 <= kc) {
+                    const Vec<uint32_t, 2> u = __builtin_bit_cast(Vec<uint32_t, 2>, o);
+                    uint32_t *q = reinterpret_cast<uint32_t *>(yr + j0);
+                    __builtin_nontemporal_store(u.v[0], q);
+                    __builtin_nontemporal_store(u.v[1], q + 1);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (j0 + e < kc) yr[j0 + e] = o.v[e];
+                }
             }
         }
         return false;

@@ -180,6 +180,38 @@ namespace mg
         for (int i = 0; i < 4; ++i) __builtin_nontemporal_store(u.v[i], q + i);
     }
 
+    // Raw buffer accesses. A resource over [p, p + bytes): a 16-byte access
+    // at a byte offset past the range reads zeros and writes nothing, without
+    // touching memory, so a kernel can issue a fixed set of accesses with no
+    // branch around them (and the compiler's wait counts stay exact). Word 3
+    // is the gfx9 layout: 32-bit data format, no swizzle. AUX 2: non-temporal.
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int kAuxNT = 2;
+    MG_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, int bytes)
+    {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), short(0), bytes, 0x00020000);
+    }
+    template <class T, int N, int AUX>
+    MG_DEV Vec<T, N> buf_ld16(__amdgpu_buffer_rsrc_t rs, int off)
+    {
+        const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, AUX);
+        Vec<uint32_t, 4> w;
+        // (each element to a prvalue first: bit_cast of an ext_vector element
+        // lvalue lowers to a read of element 0 in this compiler)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w.v[i] = uint32_t(u[i]);
+        return __builtin_bit_cast(Vec<T, N>, w);
+    }
+    template <class T, int N, int AUX>
+    MG_DEV void buf_st16(__amdgpu_buffer_rsrc_t rs, int off, const Vec<T, N> &v)
+    {
+        const Vec<uint32_t, 4> w = __builtin_bit_cast(Vec<uint32_t, 4>, v);
+        u32x4 u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) u[i] = w.v[i];
+        __builtin_amdgcn_raw_buffer_store_b128(u, rs, off, 0, AUX);
+    }
+
     // N elements: one non-temporal 16-byte access when they fill 16 bytes,
     // plain element accesses otherwise (unaligned fallbacks)
     template <typename T, int N>
