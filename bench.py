@@ -96,7 +96,7 @@ PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 STEP_OPS = ("residual_rmsnorm", "swiglu", "softmax_causal")
 KERNEL_OF = {
     # the step ops name their kernel as the traffic summary does (template arguments included)
-    "residual_rmsnorm": "k_norm_row<mg::SBf16,2,true,true,false>",
+    "residual_rmsnorm": "k_norm_row<mg::SBf16,2,true,true,true>",
     "swiglu": "k_gate_lut<mg::SBf16>",
     "softmax_causal": "k_softmax_fast<mg::SBf16,4,false,true>",
     "rope": "k_rope",

@@ -363,12 +363,9 @@ namespace mg
                 default: args(k_norm_row<S, 16, R, G, P>); break;
                 }
             };
-            auto pre = [&](auto res, auto wgt) {
-                if (rows <= kPrefetchRows)
-                    row(res, wgt, std::true_type{});
-                else
-                    row(res, wgt, std::false_type{});
-            };
+            // w requested with h and x at every row count (30.0 against 30.5 us
+            // at [4096, 5120] with w after the sum)
+            auto pre = [&](auto res, auto wgt) { row(res, wgt, std::true_type{}); };
             auto wgt = [&](auto res) {
                 if (kind != 2)
                     pre(res, std::true_type{});

@@ -30,7 +30,7 @@ namespace mg
 {
     constexpr int kSplitChunk = 4096; // keys per work-group in the split path (256 x 16)
     constexpr unsigned kLdsPerCu = 160u * 1024u; // gfx950
-    constexpr unsigned kFastWavesNoCap = 4;      // waves per SIMD of the fast path without a cap
+    constexpr unsigned kFastWavesNoCap = 5;      // waves per SIMD of the fast path without a cap
     constexpr float kNegInf = -__builtin_huge_valf();
 
     struct SmArgs
@@ -615,6 +615,105 @@ namespace mg
         }
     }
 
+    // The same two passes for rows of 16-byte-aligned, multiple-of-8 keys,
+    // without a branch around any access: thread t holds keys base + 1024 c +
+    // 4 t + e (each wave load covers 1 KiB contiguously), loaded through a
+    // buffer resource over the row's keys [0, hi] (keys past hi read as zero
+    // and are masked, keys below lo masked after the load), so all of a
+    // thread's loads are in flight at once; the finishing pass stores through
+    // one over the row's kc keys.
+    __global__ __launch_bounds__(256) void k_softmax_partial_buf(const float *__restrict__ x, SmArgs a, float c2,
+                                                                 float2 *__restrict__ part)
+    {
+        __shared__ float red[4];
+        const int64_t row = blockIdx.y;
+        int64_t lo64, hi64;
+        row_range(a, row, lo64, hi64);
+        const int lo = int(lo64), hi = int(hi64); // kc < 2^29: checked by the launcher
+        const auto rs = buf_rsrc(x + row * a.ldx, (hi + 1) * 4);
+        const int base = int(blockIdx.x) * kSplitChunk + 4 * int(threadIdx.x);
+        Vec<float, 4> u[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) u[c] = buf_ld16<float, 4, kAuxNT>(rs, (base + 1024 * c) * 4);
+        float t[4][4];
+        float m = kNegInf;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = base + 1024 * c + e;
+                t[c][e] = (j >= lo && j <= hi) ? u[c].v[e] * c2 : kNegInf;
+                m = __builtin_fmaxf(m, t[c][e]);
+            }
+        m = block_max_dpp(m, red);
+        float sum = 0.0f;
+        if (m != kNegInf)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sum += __builtin_amdgcn_exp2f(t[c][e] - m); // exp2(-inf) = 0
+        sum = block_sum_dpp(sum, red);
+        if (threadIdx.x == 0) part[row * gridDim.x + blockIdx.x] = make_float2(m, sum);
+    }
+
+    template <class SO>
+    __global__ __launch_bounds__(256) void k_softmax_finish_buf(const float *__restrict__ x,
+                                                                typename SO::raw *__restrict__ y, SmArgs a,
+                                                                float c2, const float2 *__restrict__ part)
+    {
+        using ro = typename SO::raw;
+        static_assert(sizeof(ro) == 2, "16-bit probabilities");
+        __shared__ float red[4];
+        const int64_t row = blockIdx.y;
+        const int nch = int(gridDim.x);
+        const float2 *pr = part + row * nch;
+        int64_t lo64, hi64;
+        row_range(a, row, lo64, hi64);
+        const int lo = int(lo64), hi = int(hi64);
+        const auto rs = buf_rsrc(x + row * a.ldx, (hi + 1) * 4);
+        const auto ry = buf_rsrc(y + row * a.ldy, int(a.kc) * 2);
+        const int base = int(blockIdx.x) * kSplitChunk + 4 * int(threadIdx.x);
+        // the row's partials first (thread t takes partial t; rows of more
+        // than 256 chunks loop over the rest), then the chunk's scores: loads
+        // complete in order, so the merge waits only for the partials and runs
+        // while the scores are in flight
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 pv = __builtin_amdgcn_raw_buffer_load_b64(buf_rsrc(pr, nch * 8), int(threadIdx.x) * 8, 0, 0);
+        Vec<float, 4> u[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) u[c] = buf_ld16<float, 4, 0>(rs, (base + 1024 * c) * 4);
+        const bool own = int(threadIdx.x) < nch;
+        const float pm = own ? __builtin_bit_cast(float, uint32_t(pv[0])) : kNegInf;
+        const float pl = __builtin_bit_cast(float, uint32_t(pv[1]));
+        float M = pm;
+        for (int i = threadIdx.x + blockDim.x; i < nch; i += blockDim.x) M = pr[i].x > M ? pr[i].x : M;
+        M = block_max_dpp(M, red);
+        float L = 0.0f;
+        if (M != kNegInf) {
+            if (pm != kNegInf) L = pl * __builtin_amdgcn_exp2f(pm - M);
+            for (int i = threadIdx.x + blockDim.x; i < nch; i += blockDim.x)
+                if (pr[i].x != kNegInf) L += pr[i].y * __builtin_amdgcn_exp2f(pr[i].x - M);
+        }
+        L = block_sum_dpp(L, red);
+        const float inv = M == kNegInf ? 0.0f : 1.0f / L;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            Vec<ro, 8> o; // elements 0..3 stored (8 bytes), 4..7 unused
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = base + 1024 * c + e;
+                const float p = (j >= lo && j <= hi) ? __builtin_amdgcn_exp2f(u[c].v[e] * c2 - M) * inv : 0.0f;
+                o.v[e] = SO::enc32(p);
+            }
+            const Vec<uint32_t, 4> w = __builtin_bit_cast(Vec<uint32_t, 4>, o);
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            u32x2 w2;
+            w2[0] = w.v[0];
+            w2[1] = w.v[1];
+            __builtin_amdgcn_raw_buffer_store_b64(w2, ry, (base + 1024 * c) * 2, 0, kAuxNT);
+        }
+    }
+
     template <class SI, class SO, bool CAP>
     void launch_softmax_t(mg_ctx *c, const void *x, void *y, const SmArgs &a)
     {
@@ -636,8 +735,9 @@ namespace mg
                 const unsigned wgs = unsigned(a.nrows); // < 2^31: checked above
                 // Without the cap the kernel needs few registers (8 waves per SIMD
                 // would fit) but streams fastest at 4: the LDS each work-group
-                // reserves (and never touches) holds a CU at 16 of them (measured:
-                // 124.8 us at 8 waves, 121.8 at 4-5, config 4). With the cap its
+                // reserves (and never touches) holds a CU at 20 of them (measured
+                // with four keys per lane and load: 110.5 us at 8 waves, 109.9 at
+                // 4, 109.0 at 5, 126.4 at 3, config 4). With the cap its
                 // registers allow 5, which the extra arithmetic uses.
                 const unsigned lds = CAP ? 0u : kLdsPerCu / (4u * kFastWavesNoCap);
                 auto go = [&](auto kern) {
@@ -669,6 +769,13 @@ namespace mg
         const dim3 grid{unsigned(nch), unsigned(a.nrows), 1u};
         if constexpr (SI::dt == F32 && sizeof(ro) == 2 && !CAP) {
             const float c2 = float(double(a.scale) * 1.4426950408889634);
+            if (vec && a.kc < (int64_t(1) << 28)) {
+                hipLaunchKernelGGL(k_softmax_partial_buf, grid, dim3(256), 0, c->stream, xi, a, c2, part);
+                check_launch("k_softmax_partial_buf");
+                hipLaunchKernelGGL(k_softmax_finish_buf<SO>, grid, dim3(256), 0, c->stream, xi, yo, a, c2, part);
+                check_launch("k_softmax_finish_buf");
+                return;
+            }
             hipLaunchKernelGGL(k_softmax_partial_fast, grid, dim3(256), 0, c->stream, xi, a, c2, vec, part);
             check_launch("k_softmax_partial_fast");
             hipLaunchKernelGGL(k_softmax_finish_fast<SO>, grid, dim3(256), 0, c->stream, xi, yo, a, c2, vec, part);
