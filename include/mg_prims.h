@@ -293,17 +293,39 @@ int mg_vocab_reduce_tail(mg_ctx *ctx, const void *logits, int64_t ld, int64_t ro
 
 /* The sampler's final candidate distribution from a vocab pass's output
  * (serve/sampler.py:43-112, Sampler._transformed / dist after the logit edits):
- * top_idx/top_val [rows, K] sorted as mg_vocab_reduce writes them (K = the
- * sampler's top_k, 1..256), argmax [rows]. Per row: -inf candidates dropped;
- * none left, or temperature <= 0, gives the point mass on argmax; otherwise
- * probs = softmax(values), top_p < 1 keeps the first searchsorted(cumsum, top_p)+1,
- * min_p > 0 keeps probs >= min_p*max(probs), and the kept candidates get
- * softmax(values / temperature). Writes cand_count[r] candidates, in order, to
+ * top_idx/top_val [rows, K] sorted as mg_vocab_reduce writes them over the
+ * edited logits (K = the sampler's top_k, 1..256; other top_k:
+ * mg_sample_rows), argmax [rows] of the edited logits, raw_argmax [rows] of
+ * the logits before the edits (NULL: argmax; serve/sampler.py:70-74 falls
+ * back to np.argmax of the raw logits). Per row: no finite candidate (the
+ * edited row has no finite value) gives the point mass on raw_argmax (the
+ * reference's "masked" fallback); temperature <= 0 the point mass on argmax
+ * (greedy); otherwise -inf candidates are dropped, probs = softmax(values),
+ * top_p < 1 keeps the first searchsorted(cumsum, top_p)+1, min_p > 0 keeps
+ * probs >= min_p*max(probs), and the kept candidates get softmax(values /
+ * temperature). Writes cand_count[r] candidates, in order, to
  * cand_ids/cand_probs [rows, K]. Probabilities match the reference's numpy
- * float32 arithmetic to a few ulp (f32 exp, f64 sums). */
-int mg_sample_dist(mg_ctx *ctx, const int64_t *top_idx, const float *top_val, const int64_t *argmax, int64_t rows,
-                   int64_t K, double temperature, double top_p, double min_p, int64_t *cand_ids, float *cand_probs,
-                   int64_t *cand_count);
+ * float32 arithmetic to a few ulp (f32 exp, f64 sums); a cut whose cumulative
+ * sum lies within that distance of top_p may fall one candidate apart. */
+int mg_sample_dist(mg_ctx *ctx, const int64_t *top_idx, const float *top_val, const int64_t *argmax,
+                   const int64_t *raw_argmax, int64_t rows, int64_t K, double temperature, double top_p, double min_p,
+                   int64_t *cand_ids, float *cand_probs, int64_t *cand_count);
+
+/* The same filter chain on full rows of edited logits, for any top_k
+ * (serve/sampler.py:43-112 with top_k <= 0 keeping every token, 80-95):
+ * logits f32 [rows, V] (row stride ld, 0 = V), raw_argmax [rows] as in
+ * mg_sample_dist (NULL: the row's own argmax). Greedy takes np.argmax of the
+ * edited row (first maximum, NaN counting as the largest). top_k in (0, V)
+ * keeps the top_k largest finite-or-+inf values (ties by lower index), top_k
+ * <= 0 every value > -inf. Candidates come out in value order (ties by
+ * index) when top_k > 0 or top_p < 1, as the reference sorts them, else in
+ * index order. cand_ids/cand_probs are [rows, V]; cand_count[r] is the
+ * number written, or -1 for a row left to the host: one whose sorted
+ * candidates exceed 4096, or one holding +inf (the reference's probabilities
+ * are NaN there and its draw raises). */
+int mg_sample_rows(mg_ctx *ctx, const float *logits, int64_t ld, int64_t rows, int64_t V, const int64_t *raw_argmax,
+                   int64_t top_k, double temperature, double top_p, double min_p, int64_t *cand_ids,
+                   float *cand_probs, int64_t *cand_count);
 
 #ifdef __cplusplus
 }

@@ -29,7 +29,8 @@ namespace mg
 
     __global__ __launch_bounds__(256) void k_sample_dist(const int64_t *__restrict__ top_idx,
                                                          const float *__restrict__ top_val,
-                                                         const int64_t *__restrict__ amax, int64_t rows, int K,
+                                                         const int64_t *__restrict__ amax,
+                                                         const int64_t *__restrict__ raw_amax, int64_t rows, int K,
                                                          float temperature, float top_p, float min_p,
                                                          int64_t *__restrict__ out_ids, float *__restrict__ out_p,
                                                          int64_t *__restrict__ out_n)
@@ -43,18 +44,23 @@ namespace mg
         float *op = out_p + row * K;
         float cl[4];
         int64_t id[4];
-        int nvalid = 0;
+        int nvalid = 0, nfinite = 0;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int i = 4 * lane + q;
             cl[q] = i < K ? vr[i] : -__builtin_huge_valf();
             id[q] = i < K ? ir[i] : -1;
             nvalid += wave_count(cl[q] > -__builtin_huge_valf());
+            nfinite += wave_count(__builtin_isfinite(cl[q]));
         }
-        // candidates are sorted, so the valid ones are the first nvalid
-        if (nvalid == 0 || !(temperature > 0.0f)) {
+        // candidates are sorted, so the valid ones are the first nvalid. No
+        // finite value among them: the row has none (sorted keys put every
+        // finite value ahead of -inf and NaN), the reference's "masked"
+        // fallback, a point mass on the argmax of the raw logits (70-74);
+        // otherwise temperature <= 0 is greedy on the edited logits (76-78)
+        if (nfinite == 0 || !(temperature > 0.0f)) {
             if (lane == 0) {
-                oi[0] = amax[row];
+                oi[0] = nfinite == 0 && raw_amax ? raw_amax[row] : amax[row];
                 op[0] = 1.0f;
                 out_n[row] = 1;
             }
@@ -127,15 +133,431 @@ namespace mg
     }
 
     void launch_sample_dist(mg_ctx *c, const int64_t *top_idx, const float *top_val, const int64_t *amax,
-                            int64_t rows, int64_t K, double temperature, double top_p, double min_p,
-                            int64_t *out_ids, float *out_p, int64_t *out_n)
+                            const int64_t *raw_amax, int64_t rows, int64_t K, double temperature, double top_p,
+                            double min_p, int64_t *out_ids, float *out_p, int64_t *out_n)
     {
-        need(rows >= 0 && K >= 1 && K <= 256, "sample_dist: K must be in [1, 256]");
+        need(rows >= 0 && K >= 1 && K <= 256, "sample_dist: K must be in [1, 256] (other top_k: mg_sample_rows)");
         need(top_idx && top_val && amax && out_ids && out_p && out_n, "sample_dist: NULL tensor");
         need(rows <= int64_t(0x7fffffff) * 4, "sample_dist: too many rows");
         if (rows == 0) return;
         hipLaunchKernelGGL(k_sample_dist, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, c->stream, top_idx, top_val,
-                           amax, rows, int(K), float(temperature), float(top_p), float(min_p), out_ids, out_p, out_n);
+                           amax, raw_amax, rows, int(K), float(temperature), float(top_p), float(min_p), out_ids,
+                           out_p, out_n);
         check_launch("k_sample_dist");
+    }
+
+    // ------------------------------------------------------------------
+    // The whole filter chain on full logit rows, for any top_k
+    // (serve/sampler.py:43-112, Sampler._transformed after the logit edits):
+    // one 1024-thread work-group per row of lg (f32, the edited logits).
+    //   no finite lg            point mass on raw_amax[row] (the raw logits'
+    //                           argmax, 70-74; the row's own argmax if NULL)
+    //   temperature <= 0        point mass on np.argmax(lg): the first
+    //                           maximum, NaN counting as the largest (76-78)
+    //   candidates C            entries > -inf (NaN and -inf dropped, 97-98);
+    //                           0 < top_k < |C|: the top_k largest, ties by
+    //                           lower index (80-89: argpartition's tie order is
+    //                           unspecified, this one is total)
+    //   p = softmax(C)          e = exp(x - max) (exp_diff), S = sum e in f64
+    //   top_p < 1               the shortest prefix of C in (value desc, index
+    //                           asc) order whose e sum reaches top_p * S
+    //                           (searchsorted(cumsum, top_p) + 1, 104-106)
+    //   min_p > 0               keeps p >= min_p * max(p) (f32 compare, 107-109)
+    //   final                   softmax(x / T) over the kept entries (111-112)
+    // Output order: value order when top_k > 0 or top_p < 1 (the reference
+    // sorts then), else index order. Sorted outputs hold at most kSortMax
+    // candidates (sorted in LDS); a row needing more, or holding +inf (whose
+    // reference probabilities are NaN, so its draw raises), gets count -1 and
+    // is left to the host.
+    // Selections are MSD radix passes over the 32-bit order-preserving image
+    // of the values with LDS histograms of counts (u32) and of fixed-point
+    // weights (u64, e * 2^40): integer sums, so every result is independent
+    // of the order in which threads add; the f64 sums reduce in a fixed order.
+    constexpr int kSortMax = 4096;
+    constexpr int kSfThreads = 1024;
+    constexpr double kFix = 1099511627776.0; // 2^40
+
+    struct SfLds
+    {
+        uint32_t cnt[256];
+        uint64_t wgt[256];
+        uint64_t keys[kSortMax];
+        double redd[kSfThreads / 64];
+        uint64_t redu[kSfThreads / 64];
+        uint32_t bc[4]; // broadcast words
+    };
+
+    MG_DEV uint32_t sf_img(float x) { return f32_key(x + 0.0f); } // -0 ranks with +0
+    MG_DEV bool sf_cand(float x) { return x > -__builtin_huge_valf(); } // NaN and -inf fail
+
+    // work-group sums in a fixed order (every thread returns the total)
+    MG_DEV double sf_sum_f64(double v, SfLds &L)
+    {
+        v = dpp_sum(v);
+        if ((threadIdx.x & 63) == 0) L.redd[threadIdx.x >> 6] = v;
+        __syncthreads();
+        double t = 0.0;
+        for (int i = 0; i < kSfThreads / 64; ++i) t += L.redd[i];
+        __syncthreads();
+        return t;
+    }
+    template <class OP>
+    MG_DEV uint64_t sf_red_u64(uint64_t v, SfLds &L, OP op)
+    {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint64_t o = __shfl_xor(v, d, 64);
+            v = op(v, o);
+        }
+        if (lane == 0) L.redu[threadIdx.x >> 6] = v;
+        __syncthreads();
+        uint64_t t = L.redu[0];
+        for (int i = 1; i < kSfThreads / 64; ++i) t = op(t, L.redu[i]);
+        __syncthreads();
+        return t;
+    }
+    MG_DEV uint64_t sf_sum_u64(uint64_t v, SfLds &L)
+    {
+        return sf_red_u64(v, L, [](uint64_t a, uint64_t b) { return a + b; });
+    }
+    MG_DEV uint64_t sf_max_u64(uint64_t v, SfLds &L)
+    {
+        return sf_red_u64(v, L, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
+    }
+    // exclusive prefix over the work-group in thread order; total in *tot
+    MG_DEV int sf_scan(int v, SfLds &L, int *tot)
+    {
+        const int incl = wave_prefix_sum(v);
+        if ((threadIdx.x & 63) == 63) L.redu[threadIdx.x >> 6] = uint64_t(incl);
+        __syncthreads();
+        int base = 0, all = 0;
+        for (int i = 0; i < kSfThreads / 64; ++i) {
+            const int w = int(L.redu[i]);
+            base += i < int(threadIdx.x >> 6) ? w : 0;
+            all += w;
+        }
+        __syncthreads();
+        *tot = all;
+        return base + incl - v;
+    }
+
+    // The element of rank r (1-based) in (image desc, index asc) order among
+    // the entries for which in(i, x) holds (at least r of them): its image in
+    // *img and its index in *idx, so that the first r entries are those with
+    // a larger image and those with an equal one at index <= *idx. Radix
+    // passes over the image from the top byte, then over the index among
+    // the ties from the top byte.
+    template <class IN>
+    MG_DEV void sf_select(const float *lr, int64_t V, IN in, int64_t r, SfLds &L, uint32_t *img, uint32_t *idx)
+    {
+        uint32_t pre = 0;
+        int64_t rem = r;
+        for (int sh = 24; sh >= 0; sh -= 8) {
+            for (int b = threadIdx.x; b < 256; b += kSfThreads) L.cnt[b] = 0;
+            __syncthreads();
+            const uint32_t hm = sh == 24 ? 0u : (0xffffffffu << (sh + 8));
+            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
+                const float x = lr[i];
+                if (!in(i, x)) continue;
+                const uint32_t k = sf_img(x);
+                if ((k & hm) == pre) atomicAdd(&L.cnt[(k >> sh) & 255u], 1u);
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                int64_t acc = 0;
+                int b = 255;
+                for (; b > 0; --b) {
+                    if (acc + L.cnt[b] >= rem) break;
+                    acc += L.cnt[b];
+                }
+                L.bc[0] = uint32_t(b);
+                L.bc[1] = uint32_t(acc);
+            }
+            __syncthreads();
+            pre |= L.bc[0] << sh;
+            rem -= int64_t(L.bc[1]);
+            __syncthreads();
+        }
+        // rank rem among the ties at image pre, by index ascending
+        uint32_t ipre = 0;
+        for (int sh = 24; sh >= 0; sh -= 8) {
+            for (int b = threadIdx.x; b < 256; b += kSfThreads) L.cnt[b] = 0;
+            __syncthreads();
+            const uint32_t hm = sh == 24 ? 0u : (0xffffffffu << (sh + 8));
+            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
+                const float x = lr[i];
+                if (!in(i, x) || sf_img(x) != pre) continue;
+                const uint32_t k = uint32_t(i);
+                if ((k & hm) == ipre) atomicAdd(&L.cnt[(k >> sh) & 255u], 1u);
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                int64_t acc = 0;
+                int b = 0;
+                for (; b < 255; ++b) {
+                    if (acc + L.cnt[b] >= rem) break;
+                    acc += L.cnt[b];
+                }
+                L.bc[0] = uint32_t(b);
+                L.bc[1] = uint32_t(acc);
+            }
+            __syncthreads();
+            ipre |= L.bc[0] << sh;
+            rem -= int64_t(L.bc[1]);
+            __syncthreads();
+        }
+        *img = pre;
+        *idx = ipre;
+    }
+
+    // The shortest prefix, in (image desc, index asc) order, of the entries
+    // with in(i, x) whose fixed-point weights wt(x) reach `target`: its length,
+    // or `all` when the whole set falls short.
+    template <class IN, class WT>
+    MG_DEV int64_t sf_mass_prefix(const float *lr, int64_t V, IN in, WT wt, double target, int64_t all, SfLds &L)
+    {
+        uint32_t pre = 0;
+        double rem = target;
+        int64_t above = 0;
+        uint64_t wlast = 0, clast = 0;
+        for (int sh = 24; sh >= 0; sh -= 8) {
+            for (int b = threadIdx.x; b < 256; b += kSfThreads) {
+                L.cnt[b] = 0;
+                L.wgt[b] = 0;
+            }
+            __syncthreads();
+            const uint32_t hm = sh == 24 ? 0u : (0xffffffffu << (sh + 8));
+            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
+                const float x = lr[i];
+                if (!in(i, x)) continue;
+                const uint32_t k = sf_img(x);
+                if ((k & hm) == pre) {
+                    atomicAdd(&L.cnt[(k >> sh) & 255u], 1u);
+                    atomicAdd(reinterpret_cast<unsigned long long *>(&L.wgt[(k >> sh) & 255u]),
+                              static_cast<unsigned long long>(wt(x)));
+                }
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                double wacc = 0.0;
+                int64_t cacc = 0;
+                int b = 255;
+                for (; b >= 0; --b) {
+                    if (L.cnt[b] && wacc + double(L.wgt[b]) >= rem) break;
+                    wacc += double(L.wgt[b]);
+                    cacc += L.cnt[b];
+                }
+                L.bc[0] = uint32_t(b < 0 ? 0xffffffffu : uint32_t(b));
+                L.bc[1] = uint32_t(cacc);
+                L.bc[2] = b < 0 ? 0u : L.cnt[b];
+                L.redd[0] = wacc;
+                L.redu[0] = b < 0 ? 0 : L.wgt[b];
+            }
+            __syncthreads();
+            const uint32_t bsel = L.bc[0];
+            const int64_t cadd = L.bc[1];
+            const double wadd = L.redd[0];
+            clast = L.bc[2];
+            wlast = L.redu[0];
+            __syncthreads();
+            if (bsel == 0xffffffffu) return all; // the set's whole weight falls short
+            pre |= bsel << sh;
+            rem -= wadd;
+            above += cadd;
+        }
+        // every tie at image pre has the same weight: take as many as reach it
+        const double w1 = clast ? double(wlast) / double(clast) : 0.0;
+        int64_t t = 1;
+        if (rem > 0.0 && w1 > 0.0) t = int64_t(__builtin_ceil(rem / w1));
+        if (t < 1) t = 1;
+        if (t > int64_t(clast)) t = int64_t(clast);
+        return above + t;
+    }
+
+    __global__ __launch_bounds__(kSfThreads) void k_sample_rows(const float *__restrict__ lg, int64_t ld, int64_t V,
+                                                               const int64_t *__restrict__ raw_amax, int64_t top_k,
+                                                               float temperature, float top_p, float min_p,
+                                                               int64_t *__restrict__ out_ids,
+                                                               float *__restrict__ out_p, int64_t *__restrict__ out_n)
+    {
+        __shared__ SfLds L;
+        const int64_t row = blockIdx.x;
+        const float *lr = lg + row * ld;
+        int64_t *oi = out_ids + row * V;
+        float *op = out_p + row * V;
+        const float ninf = -__builtin_huge_valf();
+
+        // pass 1: finite count, candidate count, the candidates' largest
+        // image, np.argmax
+        int64_t nfin = 0, nc = 0;
+        uint64_t mk = 0;   // image of the candidates' maximum (0: none)
+        uint64_t best = 0; // (image with NaN on top) << 32 | ~index
+        for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
+            const float x = lr[i];
+            nfin += __builtin_isfinite(x) ? 1 : 0;
+            if (sf_cand(x)) {
+                ++nc;
+                mk = sf_img(x) > mk ? sf_img(x) : mk;
+            }
+            const uint32_t g = x != x ? 0xffffffffu : sf_img(x);
+            const uint64_t key = (uint64_t(g) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+            best = key > best ? key : best;
+        }
+        nfin = int64_t(sf_sum_u64(uint64_t(nfin), L));
+        nc = int64_t(sf_sum_u64(uint64_t(nc), L));
+        best = sf_max_u64(best, L);
+        mk = sf_max_u64(mk, L);
+        if (nfin == 0 || !(temperature > 0.0f)) {
+            if (threadIdx.x == 0) {
+                oi[0] = nfin == 0 && raw_amax ? raw_amax[row] : int64_t(0xffffffffu - uint32_t(best));
+                op[0] = 1.0f;
+                out_n[row] = 1;
+            }
+            return;
+        }
+        const float mx = key_f32(uint32_t(mk));
+        if (!(mx < __builtin_huge_valf())) { // +inf among the candidates
+            if (threadIdx.x == 0) out_n[row] = -1;
+            return;
+        }
+
+        // the candidate set: the top_k largest when top_k < |C|
+        const int64_t k = top_k > 0 ? (top_k < V ? top_k : V) : 0;
+        uint32_t kimg = 0, kidx = 0xffffffffu;
+        if (k > 0 && k < nc) sf_select(lr, V, [](int64_t, float x) { return sf_cand(x); }, k, L, &kimg, &kidx);
+        const int64_t ncand = k > 0 && k < nc ? k : nc;
+        auto inC = [=](int64_t i, float x) {
+            if (!sf_cand(x)) return false;
+            const uint32_t g = sf_img(x);
+            return g > kimg || (g == kimg && uint32_t(i) <= kidx);
+        };
+
+        // S = sum of e over C (f64, fixed order) and its fixed-point twin
+        double S = 0.0;
+        uint64_t W = 0;
+        for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
+            const float x = lr[i];
+            if (!inC(i, x)) continue;
+            const float e = exp_diff(x, mx);
+            S += double(e);
+            W += uint64_t(double(e) * kFix);
+        }
+        S = sf_sum_f64(S, L);
+        W = sf_sum_u64(W, L);
+
+        // top_p: the nucleus length
+        int64_t n = ncand;
+        if (top_p < 1.0f) {
+            auto wt = [=](float x) { return uint64_t(double(exp_diff(x, mx)) * kFix); };
+            n = sf_mass_prefix(lr, V, inC, wt, double(top_p) * double(W), ncand, L);
+        }
+        // min_p: p >= min_p * max(p), p = e / S rounded to f32
+        const float pmax = float(1.0 / S), thr = min_p * pmax;
+        if (min_p > 0.0f) {
+            int64_t nm = 0;
+            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
+                const float x = lr[i];
+                if (inC(i, x) && float(double(exp_diff(x, mx)) / S) >= thr) ++nm;
+            }
+            nm = int64_t(sf_sum_u64(uint64_t(nm), L));
+            n = nm < n ? nm : n;
+        }
+
+        const bool sorted = top_k > 0 || top_p < 1.0f;
+        const float y0 = mx / temperature;
+        if (!sorted) {
+            // every candidate (top_k <= 0) passing min_p, in index order
+            double F = 0.0;
+            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
+                const float x = lr[i];
+                if (sf_cand(x) && (!(min_p > 0.0f) || float(double(exp_diff(x, mx)) / S) >= thr))
+                    F += double(exp_diff(x / temperature, y0));
+            }
+            F = sf_sum_f64(F, L);
+            int64_t base = 0;
+            for (int64_t i0 = 0; i0 < V; i0 += kSfThreads) {
+                const int64_t i = i0 + threadIdx.x;
+                const float x = i < V ? lr[i] : ninf;
+                const bool keep = sf_cand(x) && (!(min_p > 0.0f) || float(double(exp_diff(x, mx)) / S) >= thr);
+                int tot;
+                const int pos = sf_scan(keep ? 1 : 0, L, &tot);
+                if (keep) {
+                    oi[base + pos] = i;
+                    op[base + pos] = float(double(exp_diff(x / temperature, y0)) / F);
+                }
+                base += tot;
+            }
+            if (threadIdx.x == 0) out_n[row] = base;
+            return;
+        }
+        if (n > kSortMax) {
+            if (threadIdx.x == 0) out_n[row] = -1;
+            return;
+        }
+        // the kept prefix: its last entry, then gather and sort it
+        uint32_t fimg = 0, fidx = 0xffffffffu;
+        if (n < nc) sf_select(lr, V, inC, n, L, &fimg, &fidx);
+        for (int i = threadIdx.x; i < kSortMax; i += kSfThreads) L.keys[i] = 0;
+        __syncthreads();
+        int64_t base = 0;
+        for (int64_t i0 = 0; i0 < V; i0 += kSfThreads) {
+            const int64_t i = i0 + threadIdx.x;
+            const float x = i < V ? lr[i] : ninf;
+            bool keep = inC(i, x);
+            if (keep) {
+                const uint32_t g = sf_img(x);
+                keep = g > fimg || (g == fimg && uint32_t(i) <= fidx);
+            }
+            int tot;
+            const int pos = sf_scan(keep ? 1 : 0, L, &tot);
+            if (keep && base + pos < kSortMax)
+                L.keys[base + pos] = (uint64_t(sf_img(x)) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+            base += tot;
+        }
+        __syncthreads();
+        int np2 = 1;
+        while (np2 < n) np2 <<= 1;
+        // bitonic sort, descending, of keys[0, np2)
+        for (int size = 2; size <= np2; size <<= 1)
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                for (int i = threadIdx.x; i < np2; i += kSfThreads) {
+                    const int j = i ^ stride;
+                    if (j > i) {
+                        const bool desc = (i & size) == 0;
+                        const uint64_t a = L.keys[i], b = L.keys[j];
+                        if (desc ? a < b : a > b) {
+                            L.keys[i] = b;
+                            L.keys[j] = a;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        double F = 0.0;
+        for (int i = threadIdx.x; i < n; i += kSfThreads)
+            F += double(exp_diff(key_f32(uint32_t(L.keys[i] >> 32)) / temperature, y0));
+        F = sf_sum_f64(F, L);
+        for (int i = threadIdx.x; i < n; i += kSfThreads) {
+            const uint64_t key = L.keys[i];
+            oi[i] = int64_t(0xffffffffu - uint32_t(key));
+            op[i] = float(double(exp_diff(key_f32(uint32_t(key >> 32)) / temperature, y0)) / F);
+        }
+        if (threadIdx.x == 0) out_n[row] = n;
+    }
+
+    void launch_sample_rows(mg_ctx *c, const float *lg, int64_t ld, int64_t rows, int64_t V,
+                            const int64_t *raw_amax, int64_t top_k, double temperature, double top_p, double min_p,
+                            int64_t *out_ids, float *out_p, int64_t *out_n)
+    {
+        need(rows >= 0 && V >= 1 && V < (int64_t(1) << 31), "sample_rows: V must be in [1, 2^31)");
+        need(rows <= int64_t(0x7fffffff), "sample_rows: too many rows");
+        need(lg && out_ids && out_p && out_n, "sample_rows: NULL tensor");
+        if (ld == 0) ld = V;
+        need(ld >= V, "sample_rows: row stride < V");
+        if (rows == 0) return;
+        hipLaunchKernelGGL(k_sample_rows, dim3(unsigned(rows)), dim3(kSfThreads), 0, c->stream, lg, ld, V, raw_amax,
+                           top_k, float(temperature), float(top_p), float(min_p), out_ids, out_p, out_n);
+        check_launch("k_sample_rows");
     }
 } // namespace mg

@@ -300,13 +300,24 @@ int mg_vocab_reduce_noalloc(void *stream, const void *logits, int64_t ld, int64_
     });
 }
 
-int mg_sample_dist(mg_ctx *ctx, const int64_t *top_idx, const float *top_val, const int64_t *argmax, int64_t rows,
-                   int64_t K, double temperature, double top_p, double min_p, int64_t *cand_ids, float *cand_probs,
-                   int64_t *cand_count)
+int mg_sample_dist(mg_ctx *ctx, const int64_t *top_idx, const float *top_val, const int64_t *argmax,
+                   const int64_t *raw_argmax, int64_t rows, int64_t K, double temperature, double top_p, double min_p,
+                   int64_t *cand_ids, float *cand_probs, int64_t *cand_count)
 {
     MG_GUARD(-1, {
-        mg::launch_sample_dist(ctx_of(ctx), top_idx, top_val, argmax, rows, K, temperature, top_p, min_p, cand_ids,
-                               cand_probs, cand_count);
+        mg::launch_sample_dist(ctx_of(ctx), top_idx, top_val, argmax, raw_argmax, rows, K, temperature, top_p, min_p,
+                               cand_ids, cand_probs, cand_count);
+        return 0;
+    });
+}
+
+int mg_sample_rows(mg_ctx *ctx, const float *logits, int64_t ld, int64_t rows, int64_t V, const int64_t *raw_argmax,
+                   int64_t top_k, double temperature, double top_p, double min_p, int64_t *cand_ids,
+                   float *cand_probs, int64_t *cand_count)
+{
+    MG_GUARD(-1, {
+        mg::launch_sample_rows(ctx_of(ctx), logits, ld, rows, V, raw_argmax, top_k, temperature, top_p, min_p,
+                               cand_ids, cand_probs, cand_count);
         return 0;
     });
 }

@@ -100,8 +100,12 @@ namespace mg
     void launch_dequant_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, void *out,
                              int64_t rows, int64_t in, int dt_out);
     // k_vocab.hip
+    // k_sample.hip
     void launch_sample_dist(mg_ctx *c, const int64_t *top_idx, const float *top_val, const int64_t *amax,
-                            int64_t rows, int64_t K, double temperature, double top_p, double min_p,
+                            const int64_t *raw_amax, int64_t rows, int64_t K, double temperature, double top_p,
+                            double min_p, int64_t *out_ids, float *out_p, int64_t *out_n);
+    void launch_sample_rows(mg_ctx *c, const float *lg, int64_t ld, int64_t rows, int64_t V,
+                            const int64_t *raw_amax, int64_t top_k, double temperature, double top_p, double min_p,
                             int64_t *out_ids, float *out_p, int64_t *out_n);
     void launch_quantize_q8_0(mg_ctx *c, const uint16_t *w, int64_t rows, int64_t in, int8_t *qs, uint16_t *d);
     void launch_gemv_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, const uint16_t *x, int64_t batch,

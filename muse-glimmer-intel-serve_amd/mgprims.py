@@ -61,7 +61,8 @@ _SIGS = {
     "mg_gemv_q8_0": ([_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _INT], _INT),
     "mg_attn_decode": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _D, _P], _INT),
     "mg_attn_prefill": ([_P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _D, _P, _I], _INT),
-    "mg_sample_dist": ([_P, _P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P], _INT),
+    "mg_sample_dist": ([_P, _P, _P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P], _INT),
+    "mg_sample_rows": ([_P, _P, _I, _I, _I, _P, _I, _D, _D, _D, _P, _P, _P], _INT),
     "mg_vocab_reduce_tail": ([_P, _P, _I, _I, _I, _INT, _D, _D, _I, _P, _P, _P, _P, _P], _INT),
     "mg_vocab_reduce_noalloc": ([_P, _P, _I, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
     "mg_probe_stream": ([_P, _INT, _P, _P, _P, _P, _I], _INT),
@@ -481,12 +482,15 @@ class Prims:
                     raise MgError("probe_stream: operands smaller than the moved size")
         self._check(self.lib.mg_probe_stream(self.h, kind, _ptr(a), _ptr(b), _ptr(c), _ptr(d), nbytes))
 
-    def sample_dist(self, top_idx, top_val, argmax, temperature, top_p, min_p, ids=None, probs=None, n=None):
-        """serve/sampler.py's candidate distribution (ids, probs, count per row) from a vocab pass.
-        Row r's first n[r] slots hold its candidates; the slots after them are not written."""
+    def sample_dist(self, top_idx, top_val, argmax, temperature, top_p, min_p, ids=None, probs=None, n=None,
+                    raw_argmax=None):
+        """serve/sampler.py's candidate distribution (ids, probs, count per row) from a vocab pass
+        over the edited logits; raw_argmax (the raw logits' argmax, for the fully masked fallback)
+        defaults to argmax. Row r's first n[r] slots hold its candidates; the slots after them are
+        not written."""
         import torch
-        self._dev(top_idx, top_val, argmax)
-        self._contig("sample_dist", top_idx, top_val, argmax)
+        self._dev(top_idx, top_val, argmax, raw_argmax)
+        self._contig("sample_dist", top_idx, top_val, argmax, raw_argmax)
         rows, K = top_idx.shape
         dev = top_idx.device
         ids = torch.empty((rows, K), dtype=torch.int64, device=dev) if ids is None else ids
@@ -496,9 +500,32 @@ class Prims:
         self._contig("sample_dist", ids, probs, n)
         for t in (top_val, ids, probs):
             self._numel("sample_dist", t, rows * K)
-        for t in (argmax, n):
-            self._numel("sample_dist", t, rows)
-        self._check(self.lib.mg_sample_dist(self.h, _ptr(top_idx), _ptr(top_val), _ptr(argmax), rows, K, temperature,
+        for t in (argmax, n, raw_argmax):
+            if t is not None:
+                self._numel("sample_dist", t, rows)
+        self._check(self.lib.mg_sample_dist(self.h, _ptr(top_idx), _ptr(top_val), _ptr(argmax), _ptr(raw_argmax),
+                                            rows, K, temperature, top_p, min_p, _ptr(ids), _ptr(probs), _ptr(n)))
+        return ids, probs, n
+
+    def sample_rows(self, logits, top_k, temperature, top_p, min_p, raw_argmax=None):
+        """Sampler._transformed (serve/sampler.py:43-112) on full rows of edited f32 logits, any
+        top_k: (ids [rows, V], probs [rows, V], n [rows]); row r's first n[r] slots hold its
+        candidates (value order when top_k > 0 or top_p < 1, else index order); n[r] = -1 marks
+        a row left to the host (more than 4096 sorted candidates, or +inf logits)."""
+        import torch
+        self._dev(logits, raw_argmax)
+        ld = self._rows("sample_rows", logits)
+        if logits.dtype != torch.float32:
+            raise MgError("sample_rows: logits must be float32")
+        rows, V = logits.shape
+        self._contig("sample_rows", raw_argmax)
+        if raw_argmax is not None:
+            self._numel("sample_rows", raw_argmax, rows)
+        dev = logits.device
+        ids = torch.empty((rows, V), dtype=torch.int64, device=dev)
+        probs = torch.empty((rows, V), dtype=torch.float32, device=dev)
+        n = torch.empty(rows, dtype=torch.int64, device=dev)
+        self._check(self.lib.mg_sample_rows(self.h, _ptr(logits), ld, rows, V, _ptr(raw_argmax), top_k, temperature,
                                             top_p, min_p, _ptr(ids), _ptr(probs), _ptr(n)))
         return ids, probs, n
 

@@ -301,6 +301,55 @@ def sample_dist(top_idx, top_val, argmax, temperature, top_p, min_p):
     return ids, p, n
 
 
+def sample_rows(lg, raw_argmax, top_k, temperature, top_p, min_p):
+    """Sampler._transformed's final distribution (serve/sampler.py:43-112) on rows of
+    already-edited f32 logits, for any top_k, in numpy float32 as the reference computes
+    it (its steps in its order: finite check 70-74, greedy 76-78, candidates 80-95, the
+    -inf drop 97-98, softmax 104, top_p 104-106, min_p 107-109, final softmax 111-112).
+    The one choice the reference leaves open, which of several values tied at the
+    top_k-th place argpartition keeps and their order, is fixed here as lower index
+    first (numpy's stable lexsort). Returns one (ids int64, probs float32) pair per row;
+    the probabilities follow the reference's float32 operations, so cuts at top_p and
+    min_p fall exactly where the reference's fall."""
+    lg = np.asarray(lg, dtype=np.float32)
+    out = []
+    f32 = np.float32
+    for r in range(lg.shape[0]):
+        x = lg[r]
+        V = x.size
+        if not np.isfinite(x).any():          # fully masked: the raw logits' argmax
+            out.append((np.array([int(raw_argmax[r])], np.int64), np.ones(1, f32)))
+            continue
+        if not temperature > 0:               # greedy: first maximum (NaN counts as largest)
+            out.append((np.array([int(np.argmax(x))], np.int64), np.ones(1, f32)))
+            continue
+        # value-descending order, ties by index (NaN last, -inf before it)
+        order = np.lexsort((np.arange(V), -x))
+        kk = min(top_k, V) if top_k > 0 else 0
+        if kk:
+            ids = order[:kk]
+        elif top_p < 1.0:
+            ids = order
+        else:
+            ids = np.arange(V)
+        vals = x[ids]
+        live = vals > -np.inf
+        ids, vals = ids[live], vals[live]
+        ex = np.exp(vals - vals.max())
+        p = ex / ex.sum()
+        if top_p < 1.0:
+            cut = int(np.searchsorted(np.cumsum(p), top_p)) + 1
+            ids, vals, p = ids[:cut], vals[:cut], p[:cut]
+        if min_p > 0.0:
+            sel = p >= min_p * p.max()
+            ids, vals = ids[sel], vals[sel]
+        y = vals / f32(temperature)
+        ey = np.exp(y - y.max())
+        q = ey / ey.sum()
+        out.append((ids.astype(np.int64), (q / q.sum()).astype(f32)))
+    return out
+
+
 class NpyError(RuntimeError):
     pass
 

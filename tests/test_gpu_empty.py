@@ -46,7 +46,8 @@ def test_zero_sized_calls(prims, guard):
         "mg_gemv_q8_0": lambda: L.mg_gemv_q8_0(h, p, p, p, 1, 0, 64, 0, p, 0, 0),
         "mg_vocab_reduce": lambda: L.mg_vocab_reduce(h, p, 0, 0, 100, F32, 4, p, p, p, p),
         "mg_vocab_reduce_tail": lambda: L.mg_vocab_reduce_tail(h, p, 0, 0, 100, F32, 1.0, 30.0, 4, p, p, p, p, p),
-        "mg_sample_dist": lambda: L.mg_sample_dist(h, p, p, p, 0, 4, 1.0, 0.9, 0.0, p, p, p),
+        "mg_sample_dist": lambda: L.mg_sample_dist(h, p, p, p, p, 0, 4, 1.0, 0.9, 0.0, p, p, p),
+        "mg_sample_rows": lambda: L.mg_sample_rows(h, p, 0, 0, 100, p, 0, 1.0, 0.9, 0.0, p, p, p),
         "mg_attn_prefill": lambda: L.mg_attn_prefill(h, p, 0, p, p, 0, 8, 2, 128, 16, 0, 0, 0.1, p, 0),
     }
     failed = {}

@@ -18,6 +18,8 @@ import oracle as O
 from util import F32, to_dev
 
 pytestmark = pytest.mark.gpu
+GOLD_SAMPLER = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden",
+                                                  "sampler.npz"))
 
 MARGIN = 1e-5
 
@@ -70,3 +72,126 @@ def test_tail_then_dist(prims):
     lse, am, ti, tv = prims.vocab_reduce_tail(dL, 1.0, 30.0, 64)
     ids, probs, n = prims.sample_dist(ti, tv, am, 0.7, 0.95, 0.0)
     check_rows(ids.cpu().numpy(), probs.cpu().numpy(), n.cpu().numpy(), Z, 64, 0.7, 0.95, 0.0)
+
+
+# ------------------------------------------------------- the masked fallback
+def test_masked_fallback_takes_the_raw_argmax(prims):
+    """serve/sampler.py:70-74: with no finite edited logit the point mass goes to
+    np.argmax of the RAW logits, not of the edited ones. Golden rows from the
+    reference (a full mask, and a full mask over a bias that moved the argmax),
+    run through the vocab pass on the edited rows and mg_sample_dist with the
+    raw rows' argmax; a row whose mask leaves tokens keeps its distribution."""
+    import torch
+    g = GOLD_SAMPLER
+    rows = [r for r in range(g["raw"].shape[0]) if g["kind"][r] == 2]
+    rows.append(int(np.nonzero((g["params"][:, 1] == 64) & (g["kind"] == 0))[0][0]))
+    raw = torch.from_numpy(g["raw"][rows]).cuda()
+    ed = torch.from_numpy(g["edited"][rows]).cuda()
+    _, ram, _, _ = prims.vocab_reduce(raw, 64)
+    _, am, ti, tv = prims.vocab_reduce(ed, 64)
+    ids, probs, n = prims.sample_dist(ti, tv, am, 0.7, 0.95, 0.0, raw_argmax=ram)
+    ids, probs, n = ids.cpu().numpy(), probs.cpu().numpy(), n.cpu().numpy()
+    for i, r in enumerate(rows):
+        c = int(g["count"][r])
+        assert n[i] == c
+        assert np.array_equal(ids[i, :c], g["cand"][r, :c]), r
+        assert np.abs(probs[i, :c].astype(np.float64) - g["probs"][r, :c]).max() <= 2e-6
+    # the masked rows' raw argmax differs from what the edited rows give
+    assert any(int(am[i]) != int(g["raw_argmax"][r]) for i, r in enumerate(rows[:-1]))
+
+
+# ---------------------------------------------------------- any top_k, full rows
+
+
+def test_sample_rows_matches_reference_golden(prims):
+    """mg_sample_rows on the reference's own edited rows (top_k 64, 0, -1, 300,
+    1000, 5000 > V; index-order outputs; bias, penalties, masks; greedy; masked;
+    -inf entries): identical ids and counts, probabilities within 2e-6. Rows
+    marked `boundary` put top_p exactly on one of the row's float32 cumulative
+    sums (or the next float): the device sums exp in f64, the reference in
+    float32, so there the cut may fall one candidate apart; the ids the two
+    share must agree and the device's cut must lie within 1e-6 of top_p."""
+    import torch
+    g = GOLD_SAMPLER
+    rows = g["raw"].shape[0]
+    for r in range(rows):
+        T, k, tp, mp = g["params"][r]
+        ed = torch.from_numpy(g["edited"][r:r + 1]).cuda()
+        ram = torch.from_numpy(g["raw_argmax"][r:r + 1]).cuda()
+        ids, probs, n = prims.sample_rows(ed, int(k), T, tp, mp, raw_argmax=ram)
+        n = int(n.cpu()[0])
+        ids = ids.cpu().numpy()[0, :n]
+        probs = probs.cpu().numpy()[0, :n].astype(np.float64)
+        c = int(g["count"][r])
+        if g["boundary"][r] and n != c:
+            assert abs(n - c) == 1, (r, n, c)
+            m = min(n, c)
+            assert np.array_equal(ids[:m], g["cand"][r, :m]), r
+            x = g["edited"][r].astype(np.float64)
+            e = np.exp(np.sort(x)[::-1] - x.max())
+            cs = np.cumsum(e / e.sum())
+            assert abs(cs[m - 1] - np.float32(tp)) <= 1e-6, (r, cs[m - 1], tp)
+            continue
+        assert n == c, (r, n, c)
+        assert np.array_equal(ids, g["cand"][r, :c]), r
+        assert np.abs(probs - g["probs"][r, :c]).max() <= 2e-6, r
+        assert abs(probs.sum() - 1.0) <= 1e-5
+
+
+@pytest.mark.parametrize("top_k,top_p,min_p,temp", ((0, 0.95, 0.0, 1.0), (0, 0.95, 0.02, 0.7), (0, 1.0, 0.01, 1.0),
+                                                    (1000, 1.0, 0.0, 0.8), (3000, 0.95, 0.0, 1.0)))
+def test_sample_rows_vocab_scale(prims, top_k, top_p, min_p, temp):
+    """[8, 201088] rows at the vocab pass's shape against oracle.sample_rows (pinned
+    to the reference above): top_k = 0 with top_p = 0.95 (nuclei of a few hundred
+    to a few thousand tokens), index-order outputs, top_k far above 256. Rows built
+    with their cuts away from top_p / min_p (asserted), so both precisions agree."""
+    import torch
+    rows, V = 8, 201088
+    L = O.from_f64(O.to_f64(O.normal(51, (rows, V), 0.0, 1.0, F32), F32), F32).view(np.float32).copy()
+    # scales 3..7: 0.95-nuclei from about 18 000 tokens (beyond the device's sort) down to 6
+    L *= np.array([3.0, 3.5, 4.0, 4.5, 5.0, 5.5, 6.0, 7.0], np.float32)[:, None]
+    L[2, ::3] = -np.inf
+    for r in range(rows):
+        x = np.sort(L[r][np.isfinite(L[r])])[::-1]
+        kk = top_k if 0 < top_k < x.size else x.size
+        p64 = softmax(x[:kk].astype(np.float64))
+        e32 = np.exp(x[:kk] - x[0])
+        p32 = e32 / e32.sum()
+        if top_p < 1.0:
+            # the float32 and the exact cumulative sums cut at the same place, or
+            # both beyond what the device sorts (numpy's float32 cumsum drifts by
+            # up to ~1e-5 over tens of thousands of terms and moves long cuts)
+            c32 = np.searchsorted(np.cumsum(p32), np.float32(top_p)) + 1
+            c64 = np.searchsorted(np.cumsum(p64), np.float64(np.float32(top_p))) + 1
+            assert c32 == c64 or min(c32, c64) > 4096, (r, c32, c64)
+        if min_p > 0.0:
+            assert np.min(np.abs(p64 / p64[0] - np.float32(min_p))) > 1e-6, r
+    want = O.sample_rows(L, np.argmax(L, axis=1), top_k, temp, top_p, min_p)
+    ids, probs, n = prims.sample_rows(torch.from_numpy(L).cuda(), top_k, temp, top_p, min_p)
+    ids, probs, n = ids.cpu().numpy(), probs.cpu().numpy(), n.cpu().numpy()
+    for r in range(rows):
+        wi, wp = want[r]
+        if len(wi) > 4096 and (top_k > 0 or top_p < 1.0):
+            assert n[r] == -1, r                  # more sorted candidates than the device sorts
+            continue
+        assert n[r] == len(wi), (r, n[r], len(wi))
+        assert np.array_equal(ids[r, :n[r]], wi), r
+        assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, r
+
+
+def test_sample_rows_left_to_host(prims):
+    """count -1: a nucleus of more than 4096 sorted candidates (flat logits), and a
+    row holding +inf (the reference's probabilities are NaN there); other rows of
+    the same call are served"""
+    import torch
+    V = 20000
+    L = np.zeros((3, V), np.float32)
+    L[0] = np.linspace(0.0, 0.01, V, dtype=np.float32)   # almost flat: nucleus ~ 0.95 V
+    L[1, 5] = np.inf
+    L[2] = np.linspace(0.0, 40.0, V, dtype=np.float32)   # steep: a short nucleus
+    ids, probs, n = prims.sample_rows(torch.from_numpy(L).cuda(), 0, 1.0, 0.95, 0.0)
+    n = n.cpu().numpy()
+    assert n[0] == -1 and n[1] == -1
+    (wi, wp), = O.sample_rows(L[2:3], [0], 0, 1.0, 0.95, 0.0)
+    assert n[2] == len(wi)
+    assert np.array_equal(ids.cpu().numpy()[2, :n[2]], wi)

@@ -170,3 +170,65 @@ def test_plausible_mistakes_are_caught():
     # at T = 0.25 the final distribution sharpens, but the top_p cut uses the T = 1 shares
     _, _, n = run(row_from_weights([60, 30, 10], 4), 0.25, 0.8, 0.0)
     assert n[0] == 2
+
+
+# ---------------------------------------------------------------- full rows
+# oracle.sample_rows (any top_k, on full rows of edited logits) against the
+# reference's own Sampler._transformed: tests/golden/sampler.npz, written by
+# tests/golden/make_sampler_golden.py from serve/sampler.py. The golden rows
+# include the cuts no closed form fixes (top_p equal to one of the row's
+# float32 cumulative sums and the next float above it, min_p at a probability
+# ratio), the fully masked fallback under a bias, greedy after a bias, top_k
+# above 256 and above V, top_k <= 0 with and without top_p.
+GOLD_SAMPLER = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden",
+                                                  "sampler.npz"))
+
+
+def gold_rows():
+    return range(GOLD_SAMPLER["raw"].shape[0])
+
+
+@pytest.mark.parametrize("r", gold_rows())
+def test_sample_rows_matches_reference_golden(r):
+    g = GOLD_SAMPLER
+    T, k, tp, mp = g["params"][r]
+    (ids, probs), = O.sample_rows(g["edited"][r:r + 1], g["raw_argmax"][r:r + 1], int(k), T, tp, mp)
+    n = int(g["count"][r])
+    assert len(ids) == n
+    assert np.array_equal(ids, g["cand"][r, :n])
+    # the same float32 operations in the same order: the same bits
+    assert np.array_equal(probs, g["probs"][r, :n])
+
+
+def test_sample_rows_golden_covers_the_edges():
+    g = GOLD_SAMPLER
+    kinds = set(g["kind"].tolist())
+    assert kinds == {0, 1, 2}                       # dist, greedy, masked
+    masked = np.nonzero(g["kind"] == 2)[0]
+    assert all(g["cand"][r, 0] == g["raw_argmax"][r] for r in masked)
+    # an edited argmax that differs from the raw one (bias, mask, penalties)
+    moved = [r for r in gold_rows() if np.isfinite(g["edited"][r]).any()
+             and np.argmax(g["edited"][r]) != g["raw_argmax"][r]]
+    assert moved
+    assert (g["params"][:, 1] <= 0).any() and (g["params"][:, 1] > 256).any()
+    assert g["boundary"].sum() >= 6
+    # the nudged top_p rows cut one candidate later than the exact ones
+    b = np.nonzero(g["boundary"])[0]
+    assert any(g["count"][i + 1] == g["count"][i] + 1 for i in b[:-1])
+
+
+def test_sample_rows_planted_strict_cut_fails():
+    """a top_p cut taken with '>' instead of '>=' misses the boundary rows"""
+    g = GOLD_SAMPLER
+    hit = 0
+    for r in np.nonzero(g["boundary"])[0]:
+        T, k, tp, mp = g["params"][r]
+        if mp > 0:
+            continue
+        x = g["edited"][r].astype(np.float32)
+        srt = np.sort(x)[::-1]
+        e = np.exp(srt - srt.max())
+        cs = np.cumsum(e / e.sum())
+        wrong = int(np.searchsorted(cs, tp, side="right")) + 1
+        hit += wrong != g["count"][r]
+    assert hit >= 1
