@@ -10,6 +10,8 @@
  *     same thread (c_api.cpp:15-17, 170-188);
  *   - a context is not thread-safe; calls are asynchronous on the context's
  *     stream, and mg_sync() waits for them;
+ *   - a call runs on its context's device (mg_vocab_reduce_noalloc: on its
+ *     stream's) and leaves the calling thread's current HIP device as it was;
  *   - all tensor pointers are DEVICE pointers, row-major and contiguous unless
  *     a leading dimension argument says otherwise; counts are int64.
  *
@@ -33,6 +35,12 @@ extern "C" {
 typedef struct mg_ctx mg_ctx;
 
 enum mg_dtype { MG_F64 = 0, MG_BF16 = 1, MG_F16 = 2, MG_F32 = 3 };
+
+/* An output format of mg_norm_rows_mixed only: f32 words holding bf16 values
+ * (the value rounded f64 -> f32 -> bf16, then widened), the layout of
+ * bf16exec's norm_rows_f32 (src/bf16exec.hpp:422-442) and of the GPU engine's
+ * k_rmsnorm_f32 (src/gpu/gpu_engine.cpp:392-415), the embedding norm. */
+enum { MG_BF16_AS_F32 = 4 };
 
 /* Flag OR-ed into a dtype argument, together with MG_F64 only: the reference's
  * --hf-f32-compat mode (src/main.cpp:164-165; f64 runs only,
@@ -87,12 +95,15 @@ int mg_rmsnorm_rows(mg_ctx *ctx, int kind, const void *x, int64_t ldx, const voi
                     double eps, void *y, int64_t ldy, int64_t rows, int64_t dim, int dtype);
 
 /* The same norm with each operand at its own storage format — the bf16exec
- * candidate's norm_rows (src/bf16exec.hpp:398-421: x f32 rows, w bf16, y bf16;
- * its norm_rows_f32, 423-442, is the same y widened back to f32): f64
- * internals, one rounding to y_dtype. The sum of squares runs in a fixed
- * parallel order, not bf16exec's sequential one (within 1e-16 relative).
- * ldx/ldy: row strides in elements (0 = dim); in place only with one format
- * and one stride. */
+ * candidate's norm_rows (src/bf16exec.hpp:398-421: x f32 rows, w bf16, y bf16):
+ * f64 internals, one rounding to y_dtype. y_dtype MG_BF16_AS_F32 is its
+ * norm_rows_f32 (422-442; the embedding norm, 469, and the GPU engine's
+ * k_rmsnorm_f32, src/gpu/gpu_engine.cpp:392-415, 4283): y f32 holding the
+ * bf16-rounded values, in place on f32 rows allowed, and, as there, the
+ * weight applied for MG_NORM_PLAIN only (a Centered call is weight-less,
+ * 437-438). The sum of squares runs in a fixed parallel order, not bf16exec's
+ * sequential one (within 1e-16 relative). ldx/ldy: row strides in elements
+ * (0 = dim); in place only with one element size and one stride. */
 int mg_norm_rows_mixed(mg_ctx *ctx, int kind, const void *x, int64_t ldx, int x_dtype, const void *w, int w_dtype,
                        double eps, void *y, int64_t ldy, int y_dtype, int64_t rows, int64_t dim);
 
@@ -268,8 +279,9 @@ int mg_vocab_reduce(mg_ctx *ctx, const void *logits, int64_t ld, int64_t rows, i
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Same kernels and results as mg_vocab_reduce (dtype_in f32 or
  * bf16, 0 < K <= 256, ld the row stride (0 = V), any output pointer may be
- * NULL), launched on `stream` (hipStream_t; NULL = the default stream) of the
- * current HIP device. The reduction partials live in a fixed 16 MiB device
+ * NULL), launched on `stream` (hipStream_t; NULL = the default stream of the
+ * current HIP device) on that stream's device, whose own copy of the array it
+ * uses. The reduction partials live in a fixed 16 MiB device
  * array (one per GPU, held until the process ends; its address is looked up
  * once per device, which allocates nothing): a call needs
  * rows * ceil(V / 4096) * 2216 bytes of it, e.g. 64 rows x V = 201088 take

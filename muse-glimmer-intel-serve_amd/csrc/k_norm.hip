@@ -442,6 +442,7 @@ namespace mg
         case BF16: static_cast<uint16_t *>(p)[i] = SBf16::enc64(v); break;
         case F16: static_cast<uint16_t *>(p)[i] = SF16::enc64(v); break;
         case F32: static_cast<float *>(p)[i] = float(v); break;
+        case kBf16AsF32: static_cast<float *>(p)[i] = bf16_f32(SBf16::enc64(v)); break;
         default: static_cast<double *>(p)[i] = v; break;
         }
     }
@@ -465,15 +466,21 @@ namespace mg
                            double eps, void *y, int64_t ldy, int dty, int64_t rows, int64_t dim)
     {
         need(kind >= 0 && kind <= 2, "norm_rows_mixed: unknown norm kind " + std::to_string(kind));
-        for (const int dt : {dtx, dtw, dty})
+        for (const int dt : {dtx, dtw})
             need(dt >= F64 && dt <= F32, "norm_rows_mixed: unknown dtype " + std::to_string(dt));
+        need((dty >= F64 && dty <= F32) || dty == kBf16AsF32, "norm_rows_mixed: unknown dtype " + std::to_string(dty));
+        // bf16 values kept in f32: bf16exec's norm_rows_f32 (src/bf16exec.hpp:422-442),
+        // which applies the weight for Plain only (437-438): a Centered call there
+        // is weight-less
+        if (dty == kBf16AsF32 && kind == 0) kind = 2;
         need(rows >= 0 && dim > 0 && dim <= (int64_t(1) << 24), "norm_rows_mixed: bad shape");
         need(rows < (int64_t(1) << 31), "norm_rows_mixed: too many rows");
         need(x != nullptr && y != nullptr && (kind == 2 || w != nullptr), "norm_rows_mixed: NULL tensor");
         if (ldx == 0) ldx = dim;
         if (ldy == 0) ldy = dim;
         need(ldx >= dim && ldy >= dim, "norm_rows_mixed: leading dimension < dim");
-        need(x != y || (dtx == dty && ldx == ldy), "norm_rows_mixed: in place needs one format and stride");
+        const int sx = dtx == F64 ? 8 : dtx == F32 ? 4 : 2, sy = dty == F64 ? 8 : (dty == F32 || dty == kBf16AsF32) ? 4 : 2;
+        need(x != y || (sx == sy && ldx == ldy), "norm_rows_mixed: in place needs one element size and stride");
         if (rows == 0) return;
         hipLaunchKernelGGL(k_norm_mixed, dim3(unsigned(rows)), dim3(256), 0, c->stream, kind, x, ldx, dtx, w, dtw, eps,
                            y, ldy, dty, int(dim));

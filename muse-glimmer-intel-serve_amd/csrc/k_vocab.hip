@@ -1201,8 +1201,9 @@ namespace mg
     static __device__ __align__(256) unsigned char scratch[kVocabScratchBytes];
 
     // scratch's device address on the current device, looked up once per device
-    // (hipGetSymbolAddress allocates nothing); host code passes this address,
-    // never the array's name, which on the host is a stand-in.
+    // (hipGetSymbolAddress allocates nothing; each GPU holds its own copy at its
+    // own address); host code passes this address, never the array's name,
+    // which on the host is a stand-in.
     static void *scratch_address()
     {
         constexpr int kMaxDevices = 64;
@@ -1224,6 +1225,15 @@ namespace mg
     void launch_vocab_noalloc(hipStream_t stream, const void *logits, int64_t ld, int64_t rows, int64_t V,
                               int dt_in, int64_t K, double *lse, int64_t *amax, int64_t *top_idx, float *top_val)
     {
+        // the kernels run on the stream's device: make it current so the
+        // scratch address is that device's copy (the C ABI restores the
+        // caller's device on return); NULL is the current device's stream
+        if (stream) {
+            int sd = -1, cur = -1;
+            check(hipStreamGetDevice(stream, &sd), "vocab_reduce_noalloc: hipStreamGetDevice");
+            check(hipGetDevice(&cur), "vocab_reduce_noalloc: hipGetDevice");
+            if (sd != cur) check(hipSetDevice(sd), "vocab_reduce_noalloc: hipSetDevice");
+        }
         vocab_pass(stream, scratch_address(), kVocabScratchBytes, "the fixed scratch array", logits, ld, rows, V,
                    dt_in, K, lse, amax, top_idx, top_val, false, 1.0, 0.0, nullptr);
     }

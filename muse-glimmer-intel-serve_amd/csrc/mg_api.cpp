@@ -22,9 +22,30 @@ namespace
     constexpr int64_t kDefaultWorkspace = int64_t(64) << 20;
 }
 
+namespace
+{
+    // The caller's current HIP device, put back when an entry point returns:
+    // a call switches to its context's device (or its stream's) for its own
+    // work and leaves the caller's choice as it found it.
+    struct DeviceRestore
+    {
+        int dev = -1;
+        DeviceRestore()
+        {
+            if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+        }
+        ~DeviceRestore()
+        {
+            int now = -1;
+            if (dev >= 0 && hipGetDevice(&now) == hipSuccess && now != dev) (void)hipSetDevice(dev);
+        }
+    };
+}
+
 // one shape for every entry point: BODY may return; a throw becomes FAIL
 #define MG_GUARD(FAIL, BODY)                         \
     do {                                             \
+        DeviceRestore restore_device_;               \
         g_err.clear();                               \
         try {                                        \
             BODY                                     \
@@ -42,7 +63,9 @@ namespace
     mg_ctx *ctx_of(mg_ctx *c)
     {
         if (!c) mg::fail("NULL context");
-        mg::check(hipSetDevice(c->device), "hipSetDevice");
+        int cur = -1;
+        mg::check(hipGetDevice(&cur), "hipGetDevice");
+        if (cur != c->device) mg::check(hipSetDevice(c->device), "hipSetDevice");
         return c;
     }
 

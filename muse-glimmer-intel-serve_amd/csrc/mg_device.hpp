@@ -15,6 +15,7 @@ namespace mg
     enum Dt : int { F64 = 0, BF16 = 1, F16 = 2, F32 = 3 };
     // OR-ed into an f64 dtype: the reference's --hf-f32-compat chains
     constexpr int kF32Compat = 0x100;
+    constexpr int kBf16AsF32 = 4; // f32 words holding bf16 values (an output format of the mixed norm)
 
     // Visible keys [lo, hi] of a score row at position qpos over kc keys.
     // mask 1 causal: j <= qpos; 2 sliding window: qpos - window < j <= qpos

@@ -26,6 +26,7 @@ LIB_PATH = os.path.join(HERE, "libmgprims.so")
 HEADER = os.path.join(ROOT, "include", "mg_prims.h")
 
 F64, BF16, F16, F32 = 0, 1, 2, 3
+BF16_AS_F32 = 4  # f32 words holding bf16 values (an output format of norm_rows_mixed)
 F32_COMPAT = 0x100  # with F64: the reference's --hf-f32-compat chains
 CENTERED, PLAIN, WEIGHTLESS = 0, 1, 2
 MASK_NONE, MASK_CAUSAL, MASK_WINDOW, MASK_BIWINDOW = 0, 1, 2, 3
@@ -201,18 +202,25 @@ class Prims:
         self._check(self.lib.mg_rmsnorm_rows(self.h, kind, _ptr(X), ldx, _ptr(w), eps, _ptr(Y), ldy, rows, dim,
                                              _code(X, f32_compat)))
 
-    def norm_rows_mixed(self, kind, X, w, eps, Y):
+    def norm_rows_mixed(self, kind, X, w, eps, Y, bf16_as_f32=False):
         """bf16exec's norm_rows (src/bf16exec.hpp:398-421) generalised: X, w and Y each
-        at its own dtype (f32 rows, bf16 weights, bf16 output there); X, Y: [rows, dim]."""
+        at its own dtype (f32 rows, bf16 weights, bf16 output there); X, Y: [rows, dim].
+        bf16_as_f32 (Y float32): its norm_rows_f32 (422-442), Y holding the bf16-rounded
+        values, the weight applied for PLAIN only; Y may be X (the embedding norm in place)."""
         self._dev(X, w, Y)
         ldx, ldy = self._rows("norm_rows_mixed", X), self._rows("norm_rows_mixed", Y)
         self._same("norm_rows_mixed", X, Y, "shape")
         self._contig("norm_rows_mixed", w)
         rows, dim = X.shape
         self._numel("norm_rows_mixed weight", w, dim)
+        ycode = _dtype_code(Y)
+        if bf16_as_f32:
+            if ycode != F32:
+                raise MgError("norm_rows_mixed: bf16_as_f32 needs a float32 output")
+            ycode = BF16_AS_F32
         self._check(self.lib.mg_norm_rows_mixed(self.h, kind, _ptr(X), ldx, _dtype_code(X), _ptr(w),
                                                 _dtype_code(w) if w is not None else 0, eps, _ptr(Y), ldy,
-                                                _dtype_code(Y), rows, dim))
+                                                ycode, rows, dim))
 
     def residual_rmsnorm(self, kind, h, x, w, eps, y, f32_compat=False):
         """h = rnd(h + x) in place, then y = norm(h); h, x, y: [rows, dim] with unit

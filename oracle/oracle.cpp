@@ -338,6 +338,29 @@ extern "C"
         }
     }
 
+    // bf16exec's norm_rows_f32 (bf16exec.hpp:422-442), the embedding norm of
+    // its layer loop (469) and of the GPU engine (k_rmsnorm_f32,
+    // gpu_engine.cpp:392-415, weight-less): the sum of squares in index
+    // order, the output rounded to bf16 (f64 -> f32 -> bf16) and kept as an
+    // f32 value; the weight enters for Plain only, so a Centered call is
+    // weight-less there (437-438). X and Y hold f32 values; in place allowed.
+    void or_norm_rows_f32(int kind, const double *X, const double *w, double eps, double *Y, int64_t rows,
+                          int64_t dim)
+    {
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            const double *x = X + r * dim;
+            double ss = 0;
+            for (int64_t i = 0; i < dim; ++i) ss += x[i] * x[i];
+            const double rs = 1.0 / std::sqrt(ss / double(dim) + eps);
+            for (int64_t i = 0; i < dim; ++i) {
+                double v = x[i] * rs;
+                if (kind == PLAIN) v = v * w[i];
+                Y[r * dim + i] = rnd(BF16, v);
+            }
+        }
+    }
+
     // Residual add (muse_glimmer.hpp:1023-1024, 1048-1049: h = rnd(h + m)) followed
     // by the next norm on the updated stream (muse_glimmer.hpp:1028-1031). The
     // reference runs them as two loops; the fused op has the same arithmetic.

@@ -58,6 +58,7 @@ _SIGS = {
     "or_quantize_q8_0": [_P, _P, _P, _I, _I],
     "or_vocab_reduce": [_P, _I, _I, _I, _P, _P, _P, _P],
     "or_sample_dist": [_P, _P, _P, _I, _I, _D, _D, _D, _P, _P, _P],
+    "or_norm_rows_f32": [_INT, _P, _P, _D, _P, _I, _I],
     "or_save_npy_f64": [ctypes.c_char_p, _P, _P, _INT],
     "or_save_npy_i64": [ctypes.c_char_p, _P, _I],
     "or_npy_info": [ctypes.c_char_p, ctypes.c_char_p, _P, ctypes.POINTER(_INT)],
@@ -185,6 +186,17 @@ def norm_rows_mixed(kind, X, w, eps, dt):
     Y = np.empty_like(X)
     w = _c(w) if w is not None else None
     lib().or_norm_rows_mixed(kind, _p(X), _p(w), eps, _p(Y), rows, dim, dt)
+    return Y
+
+
+def norm_rows_f32(kind, X, w, eps):
+    """bf16exec's norm_rows_f32 (src/bf16exec.hpp:422-442): X f32-valued f64, w bf16-valued
+    (read for Plain only); the output bf16-rounded values as f64."""
+    X = _c(X)
+    rows, dim = X.shape
+    Y = np.empty_like(X)
+    w = _c(w) if w is not None else None
+    lib().or_norm_rows_f32(kind, _p(X), _p(w), eps, _p(Y), rows, dim)
     return Y
 
 
@@ -404,6 +416,10 @@ class Ref:
         self.s.rs_round.argtypes = [_INT, _P, _P, _I]
         self.s.rs_f16_to_f64.argtypes = [_P, _P, _I]
         self.s.rs_rmsnorm_rows.argtypes = [_INT, _P, _P, _D, _P, _I, _I, _INT, _INT]
+        self.s.rs_bf16exec_norm_rows.argtypes = [_INT, _P, _P, _D, _P, _I, _I]
+        self.s.rs_bf16exec_norm_rows_f32.argtypes = [_INT, _P, _P, _D, _P, _I, _I]
+        self.s.rs_bf16exec_norm_rows.restype = None
+        self.s.rs_bf16exec_norm_rows_f32.restype = None
         self.s.rs_rope_table.argtypes = [_D, _I, _I, _INT, _INT, _P, _P]
         self.s.rs_apply_rope.argtypes = [_P, _I, _P, _P, _I, _I, _INT]
         self.s.rs_output_tail.argtypes = [_D, _D, _P, _I, _INT]
@@ -458,6 +474,22 @@ class Ref:
         w = _c(w) if w is not None else None
         self.s.rs_rmsnorm_rows(kind, _p(X), _p(w), eps, _p(Y), X.shape[0], X.shape[1], int(f32_compat), dt)
         return Y
+
+    def bf16exec_norm_rows(self, kind, X, wt, eps):
+        """Engine::norm_rows (bf16exec.hpp:398-420): X f32 [rows, dim], wt bf16 bits -> bf16 bits"""
+        X = np.ascontiguousarray(X, np.float32)
+        wt = None if wt is None else np.ascontiguousarray(wt, np.uint16)
+        out = np.empty(X.shape, np.uint16)
+        self.s.rs_bf16exec_norm_rows(kind, _p(X), _p(wt), eps, _p(out), X.shape[0], X.shape[1])
+        return out
+
+    def bf16exec_norm_rows_f32(self, kind, X, wt, eps):
+        """Engine::norm_rows_f32 (bf16exec.hpp:422-442): X f32 [rows, dim] -> f32 holding bf16 values"""
+        X = np.ascontiguousarray(X, np.float32)
+        wt = None if wt is None else np.ascontiguousarray(wt, np.uint16)
+        out = np.empty(X.shape, np.float32)
+        self.s.rs_bf16exec_norm_rows_f32(kind, _p(X), _p(wt), eps, _p(out), X.shape[0], X.shape[1])
+        return out
 
     def rope_table(self, theta, dim, T, dt, f32_compat=False):
         c = np.empty((T, dim // 2))

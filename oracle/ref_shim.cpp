@@ -10,6 +10,7 @@
 #include <exception>
 #include <vector>
 
+#include "bf16exec.hpp"
 #include "muse_glimmer.hpp"
 #include "rounding.hpp"
 #include "safetensors.hpp"
@@ -29,6 +30,23 @@ extern "C"
     {
         for (int64_t i = 0; i < n; ++i)
             y[i] = st::f16_to_f64(h[i]);
+    }
+
+    // bf16exec Engine::norm_rows (bf16exec.hpp:398-420): f32 rows, bf16 weights,
+    // bf16 out; and Engine::norm_rows_f32 (422-442): the same rounding stored
+    // back in f32, weight applied for Plain only. Neither reads engine state,
+    // so a default-constructed engine serves.
+    void rs_bf16exec_norm_rows(int kind, const float *X, const uint16_t *wt, double eps, uint16_t *out,
+                               int64_t rows, int64_t dim)
+    {
+        const muse::bf16::Engine e{};
+        e.norm_rows(muse::NormKind(kind), X, wt, eps, out, rows, dim);
+    }
+    void rs_bf16exec_norm_rows_f32(int kind, const float *X, const uint16_t *wt, double eps, float *out,
+                                   int64_t rows, int64_t dim)
+    {
+        const muse::bf16::Engine e{};
+        e.norm_rows_f32(muse::NormKind(kind), X, wt, eps, out, rows, dim);
     }
 
     // muse::rmsnorm_rows (muse_glimmer.hpp:572-608)

@@ -6,10 +6,11 @@ Every expected output below is computed by the reference's C++ sources,
 compiled from /root/reference by oracle/Makefile into oracle/_ref:
 tools/oracle_kernels.cpp (the reference's referee library: fmath exp/tanh/
 sin/cos/pow, silu, sigmoid, the blocked-8 mean of squares) and
-oracle/ref_shim.cpp over src/rounding.hpp, src/safetensors.hpp and
+oracle/ref_shim.cpp over src/rounding.hpp, src/safetensors.hpp,
 src/muse_glimmer.hpp (round_act, f16_to_f64, rmsnorm_rows, build_rope_table,
 apply_rope, apply_output_tail; rmsnorm_rows and build_rope_table also in
-their --hf-f32-compat branches) and src/tensor.cpp (save_npy, save_npy_i64,
+their --hf-f32-compat branches) and src/bf16exec.hpp (norm_rows,
+norm_rows_f32) and src/tensor.cpp (save_npy, save_npy_i64,
 load_npy: the .npy files under npy/ and what the reference reads from numpy's). Inputs come from the oracle's portable seeded
 generator (splitmix64 + Box-Muller), stored in the fixtures as well, so the
 tests never regenerate them. Loops the reference writes inline (the residual
@@ -103,6 +104,20 @@ def norms():
     save("norms.npz", **out)
 
 
+def bf16exec():
+    """The bf16exec candidate's norm_rows (bf16 out) and norm_rows_f32 (bf16 values kept in
+    f32, the embedding norm; weight for Plain only) over f32 rows and bf16 weights, every kind."""
+    out = {}
+    for dim in (13, 640, 6656):
+        x = O.from_f64(O.to_f64(O.normal(60 + dim, (6, dim), 0, 1, F32), F32), F32).view(np.float32)
+        wb = O.normal(61 + dim, (dim,), 1, 0.05, BF16)
+        out[f"x{dim}"], out[f"w{dim}"] = x, wb
+        for kind in (0, 1, 2):
+            out[f"y{dim}_k{kind}"] = R.bf16exec_norm_rows(kind, x, None if kind == 2 else wb, 1e-6)
+            out[f"f{dim}_k{kind}"] = R.bf16exec_norm_rows_f32(kind, x, None if kind == 2 else wb, 1e-6)
+    save("bf16exec.npz", **out)
+
+
 def rope():
     out = {}
     for theta, dim, T in ((1e6, 128, 64), (5e5, 128, 48), (1e4, 64, 40)):
@@ -159,6 +174,6 @@ if __name__ == "__main__":
     if not O.Ref.available():
         sys.exit("oracle/_ref is not built (make -C oracle ref)")
     parts = {"rounding": rounding, "fmath": fmath, "config1": config1, "norms": norms, "rope": rope,
-             "tail": tail, "npy": npy}
+             "tail": tail, "npy": npy, "bf16exec": bf16exec}
     for name in sys.argv[1:] or parts:
         parts[name]()

@@ -217,3 +217,51 @@ def test_norm_rows_mixed_strided_inplace(prims):
     rel = np.abs(out[:, :dim].astype(np.float64) - ref) / np.maximum(np.abs(ref), 1e-30)
     assert rel.max() <= 1e-6
     assert same_bits(out[:, dim:], xs[:, dim:])
+
+
+# --------------------------------------- norm_rows_f32: the embedding norm
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dim", (5120, 6656))
+def test_norm_rows_f32_in_place(prims, kind, dim):
+    """bf16exec's norm_rows_f32 (src/bf16exec.hpp:422-442; the GPU engine's k_rmsnorm_f32,
+    src/gpu/gpu_engine.cpp:392-415) as mg_norm_rows_mixed with y = MG_BF16_AS_F32, in place
+    on f32 rows of N(0,1): every stored word is a bf16 value, within 1 bf16 ulp of the
+    oracle's restatement (pinned bitwise to the compiled reference), and a Centered call
+    is weight-less as in the reference"""
+    xs, x = storage(101 + dim, (65, dim), F32)
+    ws, w = storage(102 + dim, (dim,), BF16, 1.0, 0.05)
+    dx = to_dev(xs, F32)
+    prims.norm_rows_mixed(kind, dx, None if kind == O.WEIGHTLESS else to_dev(ws, BF16), 1e-6, dx, bf16_as_f32=True)
+    got = from_dev(dx, F32).view(np.uint32)
+    assert ((got & 0xffff) == 0).all()
+    ref = O.norm_rows_f32(kind, x, w, 1e-6)
+    check_lp((got >> 16).astype(np.uint16), ref, BF16, max_frac=1e-3)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_norm_rows_f32_bitwise_on_exact_sums(prims, kind):
+    """f32 rows of multiples of 1/16: every sum of squares is exact in any order, so the
+    device's bf16-in-f32 outputs equal the reference's sequential-sum chain bit for bit"""
+    rng = np.random.default_rng(110 + kind)
+    rows, dim = 257, 6656
+    x = rng.integers(-32, 33, (rows, dim)) / 16.0
+    ws, w = storage(111 + kind, (dim,), BF16, 1.0, 0.05)
+    dx = to_dev(x.astype(np.float32), F32)
+    dy = to_dev(np.zeros((rows, dim), np.float32), F32)
+    prims.norm_rows_mixed(kind, dx, None if kind == O.WEIGHTLESS else to_dev(ws, BF16), 1e-6, dy, bf16_as_f32=True)
+    ref = O.norm_rows_f32(kind, x, w, 1e-6)
+    assert same_bits(from_dev(dy, F32), ref.astype(np.float32))
+
+
+def test_norm_rows_f32_reference_golden(prims):
+    """the reference's own norm_rows_f32 outputs (tests/golden/bf16exec.npz): within 1 bf16 ulp"""
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "bf16exec.npz"))
+    for dim in (13, 640, 6656):
+        for kind in KINDS:
+            dx = to_dev(g[f"x{dim}"], F32)
+            dw = None if kind == O.WEIGHTLESS else to_dev(g[f"w{dim}"], BF16)
+            prims.norm_rows_mixed(kind, dx, dw, 1e-6, dx, bf16_as_f32=True)
+            got = (from_dev(dx, F32).view(np.uint32) >> 16).astype(np.uint16)
+            want = (g[f"f{dim}_k{kind}"].view(np.uint32) >> 16).astype(np.uint16)
+            assert ulp_diff16(got, want).max() <= 1, (dim, kind)

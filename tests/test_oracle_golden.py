@@ -88,3 +88,20 @@ def test_output_tail():
         z = g[f"z_d{dt}"]
         for mult, cap in ((1.0, 30.0), (0.5, 30.0), (2.0, 0.0)):
             assert eq(O.softcap(z, mult, cap, dt), g[f"tail_d{dt}_m{mult}_c{cap}"])
+
+
+def test_bf16exec_norms():
+    """bf16exec's norm_rows (bf16 out) and norm_rows_f32 (bf16 values kept in f32, weight
+    for Plain only), both compiled from src/bf16exec.hpp, against the oracle's
+    or_norm_rows_mixed and or_norm_rows_f32: bitwise at every kind and dim 13 / 640 / 6656"""
+    g = load("bf16exec.npz")
+    for dim in (13, 640, 6656):
+        x = g[f"x{dim}"].astype(np.float64)
+        w = O.to_f64(g[f"w{dim}"], BF16)
+        for kind in (0, 1, 2):
+            wk = None if kind == 2 else w
+            assert eq(O.norm_rows_f32(kind, x, wk, 1e-6), g[f"f{dim}_k{kind}"])
+            assert np.array_equal(O.from_f64(O.norm_rows_mixed(kind, x, wk, 1e-6, BF16), BF16), g[f"y{dim}_k{kind}"])
+    # the reference's rule: norm_rows_f32 applies the weight for Plain only, so its
+    # Centered output is the weight-less one (src/bf16exec.hpp:437-438)
+    assert eq(g["f640_k0"], g["f640_k2"]) and not eq(g["f640_k1"], g["f640_k2"])

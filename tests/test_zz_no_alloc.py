@@ -74,3 +74,23 @@ def test_noalloc_rejects_partials_beyond_the_scratch(prims):
     rlse, ram, rti, rtv = prims.vocab_reduce(dL, 8)
     torch.cuda.synchronize()
     assert same(lse, rlse) and same(am, ram) and same(ti, rti) and same(tv, rtv)
+
+
+def test_noalloc_on_a_side_stream_keeps_the_current_device(prims):
+    """the call runs on its stream's device (here the one GPU, through a stream other
+    than torch's current one) and leaves the thread's current device as it was"""
+    import torch
+    lib = prims.lib
+    L = O.normal(63, (4, 30000), 0.0, 4.0, F32)
+    dL = to_dev(L, F32)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    before = torch.cuda.current_device()
+    with torch.cuda.stream(side):
+        rc, lse, am, ti, tv = noalloc(lib, side.cuda_stream, dL, 16)
+    assert rc == 0, lib.mg_last_error().decode()
+    side.synchronize()
+    assert torch.cuda.current_device() == before
+    rlse, ram, rti, rtv = prims.vocab_reduce(dL, 16)
+    torch.cuda.synchronize()
+    assert same(lse, rlse) and same(am, ram) and same(ti, rti) and same(tv, rtv)
