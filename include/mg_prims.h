@@ -339,6 +339,30 @@ int mg_sample_rows(mg_ctx *ctx, const float *logits, int64_t ld, int64_t rows, i
                    int64_t top_k, double temperature, double top_p, double min_p, int64_t *cand_ids,
                    float *cand_probs, int64_t *cand_count);
 
+/* .npy files to and from device tensors — oracle::Tensor's I/O
+ * (src/tensor.h:11-48, src/tensor.cpp:13-224), the format of the reference's
+ * fixtures and of its --dump-hidden / --trace-dir dumps (src/main.cpp:55-76).
+ * Synchronous: file I/O on the host, one copy on the context's stream, waited
+ * for. mg_npy_info needs no context or GPU: the stored descr ('<f8', '<f4',
+ * '<i8', '<i4', '|u1', ...) into descr (at least 16 bytes, NULL to skip) and
+ * the shape into shape[0..*ndim) (at most max_ndim dimensions). */
+int mg_npy_info(const char *path, char *descr, int64_t *shape, int max_ndim, int *ndim);
+
+/* load_npy (tensor.cpp:91-224): version 1-3 headers, C order, '<f8', '<f4',
+ * '<i8', '<i4' or '|u1' data, every value widened to f64 as there (u1 stays
+ * 0..255), then stored to the device buffer dst at `dtype` (MG_F64, MG_F32,
+ * MG_BF16, MG_F16) with the twin's rounding (prec::round_act,
+ * src/rounding.hpp:64-166). n must equal the file's element count. */
+int mg_npy_load(mg_ctx *ctx, const char *path, void *dst, int64_t n, int dtype);
+
+/* save_npy (tensor.cpp:62-76): the device tensor src at `dtype`, widened to f64
+ * (exact), written as '<f8' with shape[0..ndim), header padded to 64 bytes as
+ * write_npy_header does (13-38). */
+int mg_npy_save(mg_ctx *ctx, const char *path, const void *src, int dtype, const int64_t *shape, int ndim);
+
+/* save_npy_i64 (tensor.cpp:78-89): n int64 device values as a 1-d '<i8' file. */
+int mg_npy_save_i64(mg_ctx *ctx, const char *path, const int64_t *src, int64_t n);
+
 #ifdef __cplusplus
 }
 #endif

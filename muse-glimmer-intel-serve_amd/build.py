@@ -22,7 +22,7 @@ LIB = os.path.join(HERE, "libmgprims.so")
 OBJ = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
-SOURCES = ["mg_api.cpp", "k_norm.hip", "k_elementwise.hip", "k_rope.hip", "k_qk.hip", "k_softmax.hip", "k_softmax64.hip",
+SOURCES = ["mg_api.cpp", "mg_npy.cpp", "k_norm.hip", "k_elementwise.hip", "k_rope.hip", "k_qk.hip", "k_softmax.hip", "k_softmax64.hip",
            "k_q8.hip", "k_vocab.hip", "k_sample.hip", "k_attn.hip", "k_attn_prefill.hip", "k_probe.hip"]
 
 FLAGS = [

@@ -345,6 +345,38 @@ int mg_sample_rows(mg_ctx *ctx, const float *logits, int64_t ld, int64_t rows, i
     });
 }
 
+int mg_npy_info(const char *path, char *descr, int64_t *shape, int max_ndim, int *ndim)
+{
+    MG_GUARD(-1, {
+        mg::npy_info(path, descr, shape, max_ndim, ndim);
+        return 0;
+    });
+}
+
+int mg_npy_load(mg_ctx *ctx, const char *path, void *dst, int64_t n, int dtype)
+{
+    MG_GUARD(-1, {
+        mg::npy_load(ctx_of(ctx), path, dst, n, dtype);
+        return 0;
+    });
+}
+
+int mg_npy_save(mg_ctx *ctx, const char *path, const void *src, int dtype, const int64_t *shape, int ndim)
+{
+    MG_GUARD(-1, {
+        mg::npy_save(ctx_of(ctx), path, src, dtype, shape, ndim);
+        return 0;
+    });
+}
+
+int mg_npy_save_i64(mg_ctx *ctx, const char *path, const int64_t *src, int64_t n)
+{
+    MG_GUARD(-1, {
+        mg::npy_save_i64(ctx_of(ctx), path, src, n);
+        return 0;
+    });
+}
+
 int mg_quantize_q8_0(mg_ctx *ctx, const uint16_t *w, int64_t rows, int64_t in, int8_t *qs, uint16_t *d)
 {
     MG_GUARD(-1, {

@@ -100,6 +100,11 @@ namespace mg
     void launch_dequant_q8_0(mg_ctx *c, const int8_t *qs, const uint16_t *d, void *out,
                              int64_t rows, int64_t in, int dt_out);
     // k_vocab.hip
+    // mg_npy.cpp (host: .npy files to and from device tensors)
+    void npy_info(const char *path, char *descr, int64_t *shape, int max_ndim, int *ndim);
+    void npy_load(mg_ctx *c, const char *path, void *dst, int64_t n, int dt);
+    void npy_save(mg_ctx *c, const char *path, const void *src, int dt, const int64_t *shape, int ndim);
+    void npy_save_i64(mg_ctx *c, const char *path, const int64_t *src, int64_t n);
     // k_sample.hip
     void launch_sample_dist(mg_ctx *c, const int64_t *top_idx, const float *top_val, const int64_t *amax,
                             const int64_t *raw_amax, int64_t rows, int64_t K, double temperature, double top_p,

@@ -67,6 +67,10 @@ _SIGS = {
     "mg_vocab_reduce_tail": ([_P, _P, _I, _I, _I, _INT, _D, _D, _I, _P, _P, _P, _P, _P], _INT),
     "mg_vocab_reduce_noalloc": ([_P, _P, _I, _I, _I, _INT, _I, _P, _P, _P, _P], _INT),
     "mg_probe_stream": ([_P, _INT, _P, _P, _P, _P, _I], _INT),
+    "mg_npy_info": ([ctypes.c_char_p, ctypes.c_char_p, _P, _INT, ctypes.POINTER(_INT)], _INT),
+    "mg_npy_load": ([_P, ctypes.c_char_p, _P, _I, _INT], _INT),
+    "mg_npy_save": ([_P, ctypes.c_char_p, _P, _INT, _P, _INT], _INT),
+    "mg_npy_save_i64": ([_P, ctypes.c_char_p, _P, _I], _INT),
 }
 
 _lib = None
@@ -96,6 +100,17 @@ def load_library(path: str = LIB_PATH):
 
 class MgError(RuntimeError):
     pass
+
+
+def npy_info(path):
+    """(descr, shape) of an .npy file, read by the library (mg_npy_info; no GPU needed)"""
+    L = load_library()
+    descr = ctypes.create_string_buffer(16)
+    shape = (ctypes.c_int64 * 32)()
+    nd = _INT(0)
+    if L.mg_npy_info(os.fsencode(path), descr, ctypes.cast(shape, _P), 32, ctypes.byref(nd)) != 0:
+        raise MgError(L.mg_last_error().decode())
+    return descr.value.decode(), tuple(shape[i] for i in range(nd.value))
 
 
 def _dtype_code(t):
@@ -514,6 +529,35 @@ class Prims:
         self._check(self.lib.mg_sample_dist(self.h, _ptr(top_idx), _ptr(top_val), _ptr(argmax), _ptr(raw_argmax),
                                             rows, K, temperature, top_p, min_p, _ptr(ids), _ptr(probs), _ptr(n)))
         return ids, probs, n
+
+    # ------------------------------------------------------------- .npy
+    def load_npy(self, path, dtype=None):
+        """load_npy (src/tensor.cpp:91-224) into a new device tensor of the file's shape:
+        values widened to f64 as there, stored at dtype (torch.float64 by default, or
+        float32 / bfloat16 / float16 with the twin's rounding)"""
+        import torch
+        dtype = torch.float64 if dtype is None else dtype
+        _, shape = npy_info(path)
+        t = torch.empty(shape, dtype=dtype, device=f"cuda:{self.device}")
+        self._check(self.lib.mg_npy_load(self.h, os.fsencode(path), _ptr(t), t.numel(), _dtype_code(t)))
+        return t
+
+    def save_npy(self, path, t):
+        """save_npy (src/tensor.cpp:62-76): a device tensor written as '<f8' of its shape"""
+        self._dev(t)
+        self._contig("save_npy", t)
+        shape = (ctypes.c_int64 * max(1, t.dim()))(*t.shape)
+        self._check(self.lib.mg_npy_save(self.h, os.fsencode(path), _ptr(t), _dtype_code(t),
+                                         ctypes.cast(shape, _P), t.dim()))
+
+    def save_npy_i64(self, path, t):
+        """save_npy_i64 (src/tensor.cpp:78-89): an int64 device vector as a 1-d '<i8' file"""
+        import torch
+        self._dev(t)
+        self._contig("save_npy_i64", t)
+        if t.dtype != torch.int64:
+            raise MgError("save_npy_i64: an int64 tensor is needed")
+        self._check(self.lib.mg_npy_save_i64(self.h, os.fsencode(path), _ptr(t), t.numel()))
 
     def sample_rows(self, logits, top_k, temperature, top_p, min_p, raw_argmax=None):
         """Sampler._transformed (serve/sampler.py:43-112) on full rows of edited f32 logits, any
