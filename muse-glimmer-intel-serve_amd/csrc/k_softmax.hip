@@ -725,10 +725,10 @@ namespace mg
         if (a.kc <= 2048) {
             const unsigned blocks = unsigned((a.nrows + 3) / 4);
             need(a.nrows < (int64_t(1) << 31), "softmax: too many rows");
-            // the fast capped score takes 1 <= |cap| <= 2^60 (mg_softcap_fast.hpp);
-            // other caps take the accurate kernel
+            // the fast capped score takes 1 <= |cap| <= 2^20 (mg_softcap_fast.hpp,
+            // the range its host checker sweeps); other caps take the accurate kernel
             const float acap = __builtin_fabsf(a.cap);
-            const bool cap_ok = !CAP || (acap >= 1.0f && acap <= 0x1p60f);
+            const bool cap_ok = !CAP || (acap >= 1.0f && acap <= 0x1p20f);
             if constexpr (SI::dt == F32 && sizeof(ro) == 2) if (cap_ok && (CAP || a.scale > 0.0)) {
                 // log2-domain factor: the scale folds in unless the cap comes after it
                 const float c2 = float((CAP ? 1.0 : double(a.scale)) * 1.4426950408889634);

@@ -10,6 +10,8 @@
 #include <cmath>
 #include <string>
 
+#include "mg_softcap_fast.hpp"
+
 struct mg_ctx
 {
     int device = 0;
@@ -32,23 +34,7 @@ namespace mg
     }
     inline void check_launch(const char *what) { check(hipGetLastError(), what); }
     inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-    // RN(1 / c) in f32 for a finite nonzero f32 c: the f64 quotient rounded to
-    // f32, then corrected to the neighbour whose residual 1 - r c (exact in
-    // f64: r c has at most 48 significant bits) is smallest
-    inline float recip_rn(float c)
-    {
-        const float r = float(1.0 / double(c));
-        float best = r;
-        double err = std::fabs(1.0 - double(r) * double(c));
-        for (const float n : {std::nextafter(r, 0.0f), std::nextafter(r, 2.0f * r)}) {
-            const double e = std::fabs(1.0 - double(n) * double(c));
-            if (e < err) {
-                err = e;
-                best = n;
-            }
-        }
-        return best;
-    }
+    using mgm::recip_rn; // RN(1 / c), mg_softcap_fast.hpp (shared with its host checker)
     inline int dt_size(int dt)
     {
         switch (dt) {

@@ -8,10 +8,10 @@
 //            the correctly rounded quotient when operands and quotient are
 //            normal (P. Markstein, IBM J. Res. Dev. 34(1), 1990); the host
 //            test checks it against the IEEE quotient for every f32 s with
-//            2^-100 < |s| < 2^100 at several caps. With 1 <= cap <= 2^60 (the
-//            caller's condition) a result with 2^-99 <= |q| < 2^-5 implies s
-//            in that range: |s| < 2^-100 gives |q| <= 2 |s| < 2^-99, and
-//            |s| >= 2^100 gives |q| >= 2^40.
+//            2^-100 < |s| < 2^100 at several caps, negative ones included.
+//            With 1 <= |cap| <= 2^20 (the caller's condition) a result with
+//            2^-99 <= |q| < 2^-5 implies s in that range: |s| < 2^-100 gives
+//            |q| <= 2 |s| < 2^-99, and |s| >= 2^100 gives |q| >= 2^80.
 //   tanh     tanh a = a + a^3 (-1/3 + 2/15 a^2 - 17/315 a^4) in f64 for
 //            a = |q| < 2^-5: the dropped terms are below 0.022 a^9, a
 //            relative error under 2^-45.5. Its f32 rounding equals that of
@@ -37,6 +37,27 @@
 
 namespace mgm
 {
+    // RN(1 / c) in f32 for a finite nonzero f32 c, the rcap the kernels take
+    // (computed on the host): the f64 quotient rounded to f32, then corrected
+    // to the neighbour whose residual 1 - r c (exact in f64: r c has at most
+    // 48 significant bits) is smallest. Host code; the exhaustive checker
+    // calls this same function.
+    inline float recip_rn(float c)
+    {
+        const float r = float(1.0 / double(c));
+        const float nb[2] = {__builtin_nextafterf(r, 0.0f), __builtin_nextafterf(r, 2.0f * r)};
+        float best = r;
+        double err = __builtin_fabs(1.0 - double(r) * double(c));
+        for (int i = 0; i < 2; ++i) {
+            const double e = __builtin_fabs(1.0 - double(nb[i]) * double(c));
+            if (e < err) {
+                err = e;
+                best = nb[i];
+            }
+        }
+        return best;
+    }
+
     MG_SF float softcap_quotient(float s, float cap, float rcap)
     {
         const float q0 = s * rcap;
@@ -60,7 +81,8 @@ namespace mgm
         return __builtin_fma(a * v, p, a);
     }
 
-    // the capped score; valid for 1 <= |cap| <= 2^60, rcap = RN(1 / cap)
+    // the capped score; valid for 1 <= |cap| <= 2^20 (the range the host checks
+    // exhaustively and the callers use it for), rcap = recip_rn(cap)
     MG_SF float softcap_score_fast(float x, float scale, float cap, float rcap, bool &ok)
     {
         const float q = softcap_quotient(x * scale, cap, rcap);

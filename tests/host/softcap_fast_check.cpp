@@ -39,7 +39,7 @@ int main(int argc, char **argv)
     long long bad = 0, fb = 0, count = 0;
     if (!std::strcmp(argv[1], "quot") && argc > 2) {
         const float cap = float(std::atof(argv[2]));
-        const float rcap = float(1.0 / double(cap));
+        const float rcap = mgm::recip_rn(cap); // what the kernels are given
         const int64_t lo = 0x0d800000; // 2^-100
         const int64_t hi = 0x71800000; // 2^100
 #pragma omp parallel for schedule(static, 1 << 16) reduction(+ : bad, count)
@@ -76,7 +76,7 @@ int main(int argc, char **argv)
     }
     if (!std::strcmp(argv[1], "score") && argc > 4) {
         const float scale = float(std::atof(argv[2])), cap = float(std::atof(argv[3]));
-        const float rcap = float(1.0 / double(cap));
+        const float rcap = mgm::recip_rn(cap);
         const int64_t stride = std::atoll(argv[4]);
 #pragma omp parallel for schedule(static, 1 << 12) reduction(+ : bad, fb, count)
         for (int64_t i = 0; i < (int64_t(1) << 32); i += stride) {

@@ -194,6 +194,15 @@ def test_softcap_fast_rows(prims, kc):
     check(y, ref, BF16, visible(4, 64, kc, O.MASK_CAUSAL, 0, kc - 64))
 
 
+@pytest.mark.parametrize("cap,std", ((1.0, 3.0), (-30.0, 60.0), (1048576.0, 60.0), (2.0 ** 21, 60.0), (0.5, 3.0)))
+def test_softcap_fast_rows_other_caps(prims, cap, std):
+    """the fast capped score at the ends of its range (|cap| = 1 and 2^20), at a
+    negative cap, and caps outside it (2^21, 0.5) that take the accurate kernel:
+    all within 1 bf16 ulp of the twin's chain with that cap"""
+    y, ref = run(prims, 4, 64, 2048, softcap=cap, std=std, q_pos0=2048 - 64)
+    check(y, ref, BF16, visible(4, 64, 2048, O.MASK_CAUSAL, 0, 2048 - 64))
+
+
 def test_softcap_split_rows(prims):
     """softcap 30 on the split path (rows longer than 2048 keys), bf16 and f32 out"""
     y, ref = run(prims, 3, 2, 9001, softcap=30.0, std=60.0, q_pos0=8990)

@@ -10,7 +10,8 @@ compiles) runs every input: every normal-range f32 quotient at several caps,
 every float in [2^-100, 2^-5) through the rounding test against the oracle's
 FDLIBM tanh, and the whole capped score against the twin's chain (each step
 exact in f64, rounded to f32) on a strided sweep of all f32 scores, for caps in
-the range the kernel uses it for (1 <= cap <= 2^60).
+the range the kernel uses it for (1 <= |cap| <= 2^20, negative caps included),
+with the reciprocal the kernels are given (recip_rn).
 """
 import pathlib
 import subprocess
@@ -35,7 +36,7 @@ def run(exe, *args):
 
 
 @pytest.mark.parametrize("cap", ("30", "50", "20", "1", "3", "7.5", "0.7", "0.001", "12345.678", "1048575.9",
-                                 "1048576"))
+                                 "1048576", "-30", "-1", "-1048576"))
 def test_markstein_quotient_is_correctly_rounded(checker, cap):
     bad, count = run(checker, "quot", cap)
     assert count == 0x71800000 - 0x0d800000 - 1
@@ -57,7 +58,8 @@ def test_rounding_test_sees_errors_beyond_its_margin(checker):
     assert bad > 0
 
 
-@pytest.mark.parametrize("scale,cap", (("0.08838834764831845", "30"), ("1.0", "50"), ("0.125", "20"), ("2.0", "1")))
+@pytest.mark.parametrize("scale,cap", (("0.08838834764831845", "30"), ("1.0", "50"), ("0.125", "20"), ("2.0", "1"),
+                                       ("0.08838834764831845", "-30"), ("1.0", "1048576")))
 def test_capped_score_equals_the_twin(checker, scale, cap):
     bad, fb, count = run(checker, "score", scale, cap, 7)
     assert bad == 0
