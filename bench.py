@@ -68,6 +68,11 @@ BYTES = {
                        + 2 * 2 * T * (HD // 2),
     # q and the K/V ring read, f32 out written (the op is bound by the matrix cores: FLOPS)
     "attn_prefill_4096": 2 * T * Q_H * HD + 2 * 2 * T * K_H * HD + 4 * T * Q_H * HD,
+    # the embedding norm in place: f32 rows [4096, 5120] read, bf16-valued f32 written back
+    "norm_rows_f32_embed": 2 * 4 * T * D,
+    # the sampler's whole chain on full rows (top_k <= 0, top_p 0.95): the logits read once
+    # (the selections re-read them from the caches) + the candidate lists (at most 4096 per row)
+    "sample_rows_topk0": V_ROWS * VOCAB * 4,
     # a plain device copy (torch's copy kernel): the access-pattern ceiling the others are read against
     "copy_256MiB": 2 * (256 << 20),
     # one 4-byte fill (torch's fill kernel): what the timing protocol itself costs for any single launch
@@ -110,6 +115,8 @@ KERNEL_OF = {
     "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
     "attn_prefill_4096": "k_attn_prefill<5,4,1,4>",
     "softmax_causal_softcap30": "k_softmax_fast<cap>",
+    "norm_rows_f32_embed": "k_norm_mixed",
+    "sample_rows_topk0": "k_sample_rows",
     "copy_256MiB": "torch copy (memory-only probe)",
     "launch_floor": "torch fill of one float (timing-protocol probe)",
     "probe_copy_256MiB": "k_probe<0> (copy)",
@@ -191,6 +198,7 @@ def make_inputs(torch, P):
     I["pk"] = randn((T, K_H, HD))
     I["pv"] = randn((T, K_H, HD))
     I["pout"] = torch.empty((T, Q_H, HD), dtype=torch.float32, device=dev)
+    I["hf32"] = randn((T, D), 0.0, 1.0, torch.float32)
     I["copy_src"] = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
     I["copy_dst"] = torch.empty_like(I["copy_src"])
     I["one"] = torch.empty(1, dtype=torch.float32, device=dev)
@@ -222,6 +230,9 @@ def make_inputs(torch, P):
         "attn_prefill_4096": lambda: P.attn_prefill(I["q"], I["pk"], I["pv"], 0, scale, 0, I["pout"]),
         "qk_norm_rope_kv": lambda: P.qk_norm_rope(I["q"], I["k"], 1e-6, 3.87, I["cos"], I["sin"], None, 0, I["v"],
                                                   I["kcache"], I["vcache"]),
+        "norm_rows_f32_embed": lambda: P.norm_rows_mixed(M.WEIGHTLESS, I["hf32"], None, 1e-6, I["hf32"],
+                                                         bf16_as_f32=True),
+        "sample_rows_topk0": lambda: P.sample_rows(I["logits"], 0, 1.0, 0.95, 0.0),
         "copy_256MiB": lambda: I["copy_dst"].copy_(I["copy_src"]),
         "launch_floor": lambda: I["one"].zero_(),
         "probe_copy_256MiB": lambda: P.probe_stream(P.PROBE_COPY, I["copy_src"], I["copy_dst"]),
@@ -264,18 +275,34 @@ def time_op(torch, fn, reps, flush):
     return statistics.median(times), min(times)
 
 
+def lib_digest():
+    """sha256 of the libmgprims.so this process loads"""
+    import hashlib
+    import mgprims
+    with open(mgprims.LIB_PATH, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
 def read_traffic(path, kernel):
     """Measured HBM bytes per launch for `kernel` from the rocprofv3 PMC summary:
     the line naming it exactly (template arguments included), else the one line
-    whose name starts with it; None when absent or ambiguous."""
+    whose name starts with it; None when absent or ambiguous, and None when the
+    summary was measured on another build of the library than the one loaded
+    (its '# library sha256:' line), so a kernel change never pairs new times
+    with old counters."""
     rows = {}
+    digest = None
     try:
         with open(path) as f:
             for line in f:
+                if line.startswith("# library sha256:"):
+                    digest = line.split(":", 1)[1].strip()
                 parts = line.split()
                 if len(parts) >= 3 and not line.startswith("#"):
                     rows[parts[0]] = int(float(parts[1]) + float(parts[2]))
     except OSError:
+        return None
+    if digest != lib_digest():
         return None
     if kernel in rows:
         return rows[kernel]

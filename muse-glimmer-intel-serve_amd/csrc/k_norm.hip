@@ -462,6 +462,65 @@ namespace mg
                    norm_out(kind, ld_any(x, row * ldx + i, dtx), rs, kind == 2 ? 0.0 : ld_any(w, i, dtw)), dty);
     }
 
+    // f32 rows, bf16 weights (or none), y as bf16, f32 or bf16 values in f32 —
+    // bf16exec's norm_rows and norm_rows_f32 (src/bf16exec.hpp:398-442) on
+    // 16-byte-aligned rows of a multiple of 4: k_norm_row's form (one
+    // work-group per row, every access a raw buffer access, every load before
+    // the first store, so y may be x), four values a 16-byte chunk.
+    template <int CPT, int DTY, bool WGT>
+    __global__ __launch_bounds__(1024) void k_norm_f32rows(int kind, const float *x, int64_t ldx,
+                                                           const uint16_t *__restrict__ w, double eps, void *y,
+                                                           int64_t ldy, int dim)
+    {
+        __shared__ double part[16];
+        const int64_t row = blockIdx.x;
+        const auto rx = buf_rsrc(x + row * ldx, dim * 4);
+        const auto rw = buf_rsrc(WGT ? static_cast<const void *>(w) : static_cast<const void *>(x), WGT ? dim * 2 : 0);
+        Vec<float, 4> xv[CPT];
+        uint32_t wv[CPT][2];
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int ch = int(threadIdx.x) + c * int(blockDim.x);
+            xv[c] = buf_ld16<float, 4, kAuxNT>(rx, ch * 16);
+            if constexpr (WGT) {
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rw, ch * 8, 0, 0);
+                wv[c][0] = u[0];
+                wv[c][1] = u[1];
+            }
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ss += double(xv[c].v[e]) * double(xv[c].v[e]);
+        const double rs = 1.0 / __builtin_sqrt(block_sum(ss, part) / double(dim) + eps);
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int ch = int(threadIdx.x) + c * int(blockDim.x);
+            double o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const double wt = WGT ? double(bf16_f32((e & 1) ? wv[c][e >> 1] >> 16 : wv[c][e >> 1] & 0xffffu)) : 0.0;
+                o[e] = norm_out(kind, double(xv[c].v[e]), rs, wt);
+            }
+            if constexpr (DTY == BF16) {
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                u32x2 u;
+                u[0] = uint32_t(SBf16::enc64(o[0])) | uint32_t(SBf16::enc64(o[1])) << 16;
+                u[1] = uint32_t(SBf16::enc64(o[2])) | uint32_t(SBf16::enc64(o[3])) << 16;
+                __builtin_amdgcn_raw_buffer_store_b64(u, buf_rsrc(static_cast<uint16_t *>(y) + row * ldy, dim * 2),
+                                                      ch * 8, 0, kAuxNT);
+            } else {
+                Vec<float, 4> v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    v.v[e] = DTY == F32 ? float(o[e]) : bf16_f32(SBf16::enc64(o[e]));
+                buf_st16<float, 4, kAuxNT>(buf_rsrc(static_cast<float *>(y) + row * ldy, dim * 4), ch * 16, v);
+            }
+        }
+    }
+
     void launch_norm_mixed(mg_ctx *c, int kind, const void *x, int64_t ldx, int dtx, const void *w, int dtw,
                            double eps, void *y, int64_t ldy, int dty, int64_t rows, int64_t dim)
     {
@@ -482,6 +541,47 @@ namespace mg
         const int sx = dtx == F64 ? 8 : dtx == F32 ? 4 : 2, sy = dty == F64 ? 8 : (dty == F32 || dty == kBf16AsF32) ? 4 : 2;
         need(x != y || (sx == sy && ldx == ldy), "norm_rows_mixed: in place needs one element size and stride");
         if (rows == 0) return;
+        const bool wgt = kind != 2;
+        if (dtx == F32 && (!wgt || dtw == BF16) && (dty == BF16 || dty == F32 || dty == kBf16AsF32) && dim % 4 == 0 &&
+            ldx % 4 == 0 && ldy % (dty == BF16 ? 8 : 4) == 0 && aligned16(x) && aligned16(y) &&
+            (!wgt || (reinterpret_cast<uintptr_t>(w) & 7u) == 0) && dim <= (int64_t(1) << 20)) {
+            const int nchunk = int(dim / 4);
+            int cpt = 1;
+            while ((nchunk + cpt - 1) / cpt > (rows <= 256 ? 1024 : 512) && cpt < 16) cpt *= 2;
+            const int nt = ((nchunk + cpt - 1) / cpt + 63) / 64 * 64;
+            if (nt <= 1024) {
+                auto go = [&](auto kern) {
+                    hipLaunchKernelGGL(kern, dim3(unsigned(rows)), dim3(unsigned(nt)), 0, c->stream, kind,
+                                       static_cast<const float *>(x), ldx, static_cast<const uint16_t *>(w), eps, y,
+                                       ldy, int(dim));
+                };
+                auto pick = [&](auto dtyc, auto wgtc) {
+                    constexpr int D = decltype(dtyc)::value;
+                    constexpr bool G = decltype(wgtc)::value;
+                    switch (cpt) {
+                    case 1: go(k_norm_f32rows<1, D, G>); break;
+                    case 2: go(k_norm_f32rows<2, D, G>); break;
+                    case 4: go(k_norm_f32rows<4, D, G>); break;
+                    case 8: go(k_norm_f32rows<8, D, G>); break;
+                    default: go(k_norm_f32rows<16, D, G>); break;
+                    }
+                };
+                auto bywgt = [&](auto dtyc) {
+                    if (wgt)
+                        pick(dtyc, std::true_type{});
+                    else
+                        pick(dtyc, std::false_type{});
+                };
+                if (dty == BF16)
+                    bywgt(std::integral_constant<int, BF16>{});
+                else if (dty == F32)
+                    bywgt(std::integral_constant<int, F32>{});
+                else
+                    bywgt(std::integral_constant<int, kBf16AsF32>{});
+                check_launch("k_norm_f32rows");
+                return;
+            }
+        }
         hipLaunchKernelGGL(k_norm_mixed, dim3(unsigned(rows)), dim3(256), 0, c->stream, kind, x, ldx, dtx, w, dtw, eps,
                            y, ldy, dty, int(dim));
         check_launch("k_norm_mixed");

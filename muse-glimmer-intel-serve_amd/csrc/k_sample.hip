@@ -165,23 +165,23 @@ namespace mg
     //   min_p > 0               keeps p >= min_p * max(p) (f32 compare, 107-109)
     //   final                   softmax(x / T) over the kept entries (111-112)
     // Output order: value order when top_k > 0 or top_p < 1 (the reference
-    // sorts then), else index order. Sorted outputs hold at most kSortMax
-    // candidates (sorted in LDS); a row needing more, or holding +inf (whose
-    // reference probabilities are NaN, so its draw raises), gets count -1 and
-    // is left to the host.
+    // sorts then), else index order. Sorted outputs: the largest (at most
+    // kSortMax) candidates are gathered into LDS and sorted, the top_p cut is
+    // found by an f64 prefix sum in that order; a row whose kept prefix does
+    // not fit, or that holds +inf (whose reference probabilities are NaN, so
+    // its draw raises), gets count -1 and is left to the host.
     // Selections are MSD radix passes over the 32-bit order-preserving image
-    // of the values with LDS histograms of counts (u32) and of fixed-point
-    // weights (u64, e * 2^40): integer sums, so every result is independent
-    // of the order in which threads add; the f64 sums reduce in a fixed order.
+    // of the values with an LDS count histogram; counts are integers, so every
+    // result is independent of the order in which threads add, and the f64
+    // sums reduce in a fixed order.
     constexpr int kSortMax = 4096;
     constexpr int kSfThreads = 1024;
-    constexpr double kFix = 1099511627776.0; // 2^40
 
     struct SfLds
     {
         uint32_t cnt[256];
-        uint64_t wgt[256];
         uint64_t keys[kSortMax];
+        double red[kSortMax / 4];
         double redd[kSfThreads / 64];
         uint64_t redu[kSfThreads / 64];
         uint32_t bc[4]; // broadcast words
@@ -225,6 +225,10 @@ namespace mg
     {
         return sf_red_u64(v, L, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
     }
+    MG_DEV uint64_t sf_min_u64(uint64_t v, SfLds &L)
+    {
+        return sf_red_u64(v, L, [](uint64_t a, uint64_t b) { return a < b ? a : b; });
+    }
     // exclusive prefix over the work-group in thread order; total in *tot
     MG_DEV int sf_scan(int v, SfLds &L, int *tot)
     {
@@ -241,28 +245,123 @@ namespace mg
         *tot = all;
         return base + incl - v;
     }
+    // the same for f64 values: each thread's exclusive prefix, summed in a
+    // fixed order (the lanes' values through LDS, then the waves')
+    MG_DEV double sf_scan_f64(double v, SfLds &L)
+    {
+        L.red[threadIdx.x] = v;
+        __syncthreads();
+        const int w0 = int(threadIdx.x) & ~63, lane = int(threadIdx.x) & 63;
+        double in_wave = 0.0;
+        for (int i = 0; i < lane; ++i) in_wave += L.red[w0 + i];
+        double wave_tot = in_wave;
+        for (int i = lane; i < 64; ++i) wave_tot += L.red[w0 + i];
+        if (lane == 63) L.redd[threadIdx.x >> 6] = wave_tot;
+        __syncthreads();
+        double base = 0.0;
+        for (int i = 0; i < int(threadIdx.x >> 6); ++i) base += L.redd[i];
+        __syncthreads();
+        return base + in_wave;
+    }
+
+    // f(i, x) for every entry of the row; 16-byte loads on 16-byte-aligned rows
+    // (thread t takes entries 4t..4t+3 of each 4096-entry block, four blocks in
+    // flight), entry by entry otherwise. Every lane of a wave calls f the same
+    // number of times except in the row's last block (lanes past the end idle).
+    template <class F>
+    MG_DEV void sf_each(const float *lr, int64_t V, bool al16, F f)
+    {
+        if (al16) {
+            const int64_t V4 = V >> 2;
+            const Vec<float, 4> *p = reinterpret_cast<const Vec<float, 4> *>(lr);
+            int64_t g = threadIdx.x;
+            for (; g + 3 * kSfThreads < V4; g += 4 * kSfThreads) {
+                Vec<float, 4> a[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) a[u] = p[g + u * kSfThreads];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) f(4 * (g + u * kSfThreads) + e, a[u].v[e]);
+            }
+            for (; g < V4; g += kSfThreads) {
+                const Vec<float, 4> a = p[g];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) f(4 * g + e, a.v[e]);
+            }
+            for (int64_t i = (V4 << 2) + threadIdx.x; i < V; i += kSfThreads) f(i, lr[i]);
+        } else {
+            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) f(i, lr[i]);
+        }
+    }
+
+    // The entries with keep(i, x), in index order: emit(position, i, x) for
+    // each, the positions counted from 0; returns how many. Blocks of 4 x 1024
+    // entries (aligned rows) or 1024, each thread's entries consecutive and the
+    // threads in order, so positions follow the index.
+    template <class KEEP, class EMIT>
+    MG_DEV int64_t sf_compact(const float *lr, int64_t V, bool al16, SfLds &L, KEEP keep, EMIT emit)
+    {
+        const int per = al16 ? 4 : 1;
+        int64_t base = 0;
+        for (int64_t i0 = 0; i0 < V; i0 += int64_t(kSfThreads) * per) {
+            const int64_t j = i0 + int64_t(threadIdx.x) * per;
+            float xs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (al16 && j + 3 < V) {
+                const Vec<float, 4> a = *reinterpret_cast<const Vec<float, 4> *>(lr + j);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xs[e] = a.v[e];
+            } else {
+                for (int e = 0; e < per; ++e)
+                    if (j + e < V) xs[e] = lr[j + e];
+            }
+            bool ks[4];
+            int cnt = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                ks[e] = e < per && j + e < V && keep(j + e, xs[e]);
+                cnt += ks[e] ? 1 : 0;
+            }
+            int tot;
+            int pos = sf_scan(cnt, L, &tot);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (ks[e]) emit(base + pos++, j + e, xs[e]);
+            base += tot;
+        }
+        return base;
+    }
+
+    // add one to cnt[bin] for every lane with `valid` (LDS atomics; a wave's
+    // lanes on one bin serialize in the LDS, which measured cheaper here than
+    // gathering equal bins by ballots first: a wave's 64 values spread over
+    // ~16 top-byte bins)
+    MG_DEV void sf_hist_add(uint32_t *cnt, uint32_t bin, bool valid)
+    {
+        if (valid) atomicAdd(&cnt[bin], 1u);
+    }
 
     // The element of rank r (1-based) in (image desc, index asc) order among
     // the entries for which in(i, x) holds (at least r of them): its image in
     // *img and its index in *idx, so that the first r entries are those with
     // a larger image and those with an equal one at index <= *idx. Radix
-    // passes over the image from the top byte, then over the index among
-    // the ties from the top byte.
+    // passes over the image from the top byte; when the rank falls inside a
+    // run of equal values, passes over the index among them from the top byte.
     template <class IN>
-    MG_DEV void sf_select(const float *lr, int64_t V, IN in, int64_t r, SfLds &L, uint32_t *img, uint32_t *idx)
+    MG_DEV void sf_select(const float *lr, int64_t V, bool al16, IN in, int64_t r, SfLds &L, uint32_t *img,
+                          uint32_t *idx)
     {
         uint32_t pre = 0;
         int64_t rem = r;
+        uint32_t ties = 0;
         for (int sh = 24; sh >= 0; sh -= 8) {
             for (int b = threadIdx.x; b < 256; b += kSfThreads) L.cnt[b] = 0;
             __syncthreads();
             const uint32_t hm = sh == 24 ? 0u : (0xffffffffu << (sh + 8));
-            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
-                const float x = lr[i];
-                if (!in(i, x)) continue;
+            sf_each(lr, V, al16, [&](int64_t i, float x) {
                 const uint32_t k = sf_img(x);
-                if ((k & hm) == pre) atomicAdd(&L.cnt[(k >> sh) & 255u], 1u);
-            }
+                sf_hist_add(L.cnt, (k >> sh) & 255u, in(i, x) && (k & hm) == pre);
+            });
             __syncthreads();
             if (threadIdx.x == 0) {
                 int64_t acc = 0;
@@ -273,24 +372,28 @@ namespace mg
                 }
                 L.bc[0] = uint32_t(b);
                 L.bc[1] = uint32_t(acc);
+                L.bc[2] = L.cnt[b];
             }
             __syncthreads();
             pre |= L.bc[0] << sh;
             rem -= int64_t(L.bc[1]);
+            ties = L.bc[2];
             __syncthreads();
         }
-        // rank rem among the ties at image pre, by index ascending
+        *img = pre;
+        if (int64_t(ties) == rem) { // every entry equal to the image is taken: no index cut
+            *idx = 0xffffffffu;
+            return;
+        }
         uint32_t ipre = 0;
         for (int sh = 24; sh >= 0; sh -= 8) {
             for (int b = threadIdx.x; b < 256; b += kSfThreads) L.cnt[b] = 0;
             __syncthreads();
             const uint32_t hm = sh == 24 ? 0u : (0xffffffffu << (sh + 8));
-            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
-                const float x = lr[i];
-                if (!in(i, x) || sf_img(x) != pre) continue;
+            sf_each(lr, V, al16, [&](int64_t i, float x) {
                 const uint32_t k = uint32_t(i);
-                if ((k & hm) == ipre) atomicAdd(&L.cnt[(k >> sh) & 255u], 1u);
-            }
+                sf_hist_add(L.cnt, (k >> sh) & 255u, in(i, x) && sf_img(x) == pre && (k & hm) == ipre);
+            });
             __syncthreads();
             if (threadIdx.x == 0) {
                 int64_t acc = 0;
@@ -307,72 +410,7 @@ namespace mg
             rem -= int64_t(L.bc[1]);
             __syncthreads();
         }
-        *img = pre;
         *idx = ipre;
-    }
-
-    // The shortest prefix, in (image desc, index asc) order, of the entries
-    // with in(i, x) whose fixed-point weights wt(x) reach `target`: its length,
-    // or `all` when the whole set falls short.
-    template <class IN, class WT>
-    MG_DEV int64_t sf_mass_prefix(const float *lr, int64_t V, IN in, WT wt, double target, int64_t all, SfLds &L)
-    {
-        uint32_t pre = 0;
-        double rem = target;
-        int64_t above = 0;
-        uint64_t wlast = 0, clast = 0;
-        for (int sh = 24; sh >= 0; sh -= 8) {
-            for (int b = threadIdx.x; b < 256; b += kSfThreads) {
-                L.cnt[b] = 0;
-                L.wgt[b] = 0;
-            }
-            __syncthreads();
-            const uint32_t hm = sh == 24 ? 0u : (0xffffffffu << (sh + 8));
-            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
-                const float x = lr[i];
-                if (!in(i, x)) continue;
-                const uint32_t k = sf_img(x);
-                if ((k & hm) == pre) {
-                    atomicAdd(&L.cnt[(k >> sh) & 255u], 1u);
-                    atomicAdd(reinterpret_cast<unsigned long long *>(&L.wgt[(k >> sh) & 255u]),
-                              static_cast<unsigned long long>(wt(x)));
-                }
-            }
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                double wacc = 0.0;
-                int64_t cacc = 0;
-                int b = 255;
-                for (; b >= 0; --b) {
-                    if (L.cnt[b] && wacc + double(L.wgt[b]) >= rem) break;
-                    wacc += double(L.wgt[b]);
-                    cacc += L.cnt[b];
-                }
-                L.bc[0] = uint32_t(b < 0 ? 0xffffffffu : uint32_t(b));
-                L.bc[1] = uint32_t(cacc);
-                L.bc[2] = b < 0 ? 0u : L.cnt[b];
-                L.redd[0] = wacc;
-                L.redu[0] = b < 0 ? 0 : L.wgt[b];
-            }
-            __syncthreads();
-            const uint32_t bsel = L.bc[0];
-            const int64_t cadd = L.bc[1];
-            const double wadd = L.redd[0];
-            clast = L.bc[2];
-            wlast = L.redu[0];
-            __syncthreads();
-            if (bsel == 0xffffffffu) return all; // the set's whole weight falls short
-            pre |= bsel << sh;
-            rem -= wadd;
-            above += cadd;
-        }
-        // every tie at image pre has the same weight: take as many as reach it
-        const double w1 = clast ? double(wlast) / double(clast) : 0.0;
-        int64_t t = 1;
-        if (rem > 0.0 && w1 > 0.0) t = int64_t(__builtin_ceil(rem / w1));
-        if (t < 1) t = 1;
-        if (t > int64_t(clast)) t = int64_t(clast);
-        return above + t;
     }
 
     __global__ __launch_bounds__(kSfThreads) void k_sample_rows(const float *__restrict__ lg, int64_t ld, int64_t V,
@@ -386,15 +424,14 @@ namespace mg
         const float *lr = lg + row * ld;
         int64_t *oi = out_ids + row * V;
         float *op = out_p + row * V;
-        const float ninf = -__builtin_huge_valf();
+        const bool al16 = (reinterpret_cast<uintptr_t>(lr) & 15u) == 0;
 
         // pass 1: finite count, candidate count, the candidates' largest
         // image, np.argmax
         int64_t nfin = 0, nc = 0;
         uint64_t mk = 0;   // image of the candidates' maximum (0: none)
         uint64_t best = 0; // (image with NaN on top) << 32 | ~index
-        for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
-            const float x = lr[i];
+        sf_each(lr, V, al16, [&](int64_t i, float x) {
             nfin += __builtin_isfinite(x) ? 1 : 0;
             if (sf_cand(x)) {
                 ++nc;
@@ -403,7 +440,7 @@ namespace mg
             const uint32_t g = x != x ? 0xffffffffu : sf_img(x);
             const uint64_t key = (uint64_t(g) << 32) | uint64_t(0xffffffffu - uint32_t(i));
             best = key > best ? key : best;
-        }
+        });
         nfin = int64_t(sf_sum_u64(uint64_t(nfin), L));
         nc = int64_t(sf_sum_u64(uint64_t(nc), L));
         best = sf_max_u64(best, L);
@@ -425,7 +462,8 @@ namespace mg
         // the candidate set: the top_k largest when top_k < |C|
         const int64_t k = top_k > 0 ? (top_k < V ? top_k : V) : 0;
         uint32_t kimg = 0, kidx = 0xffffffffu;
-        if (k > 0 && k < nc) sf_select(lr, V, [](int64_t, float x) { return sf_cand(x); }, k, L, &kimg, &kidx);
+        if (k > 0 && k < nc)
+            sf_select(lr, V, al16, [](int64_t, float x) { return sf_cand(x); }, k, L, &kimg, &kidx);
         const int64_t ncand = k > 0 && k < nc ? k : nc;
         auto inC = [=](int64_t i, float x) {
             if (!sf_cand(x)) return false;
@@ -433,92 +471,54 @@ namespace mg
             return g > kimg || (g == kimg && uint32_t(i) <= kidx);
         };
 
-        // S = sum of e over C (f64, fixed order) and its fixed-point twin
+        // S = sum of e over C (f64, fixed order)
         double S = 0.0;
-        uint64_t W = 0;
-        for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
-            const float x = lr[i];
-            if (!inC(i, x)) continue;
-            const float e = exp_diff(x, mx);
-            S += double(e);
-            W += uint64_t(double(e) * kFix);
-        }
+        sf_each(lr, V, al16, [&](int64_t i, float x) {
+            if (inC(i, x)) S += double(exp_diff(x, mx));
+        });
         S = sf_sum_f64(S, L);
-        W = sf_sum_u64(W, L);
-
-        // top_p: the nucleus length
-        int64_t n = ncand;
-        if (top_p < 1.0f) {
-            auto wt = [=](float x) { return uint64_t(double(exp_diff(x, mx)) * kFix); };
-            n = sf_mass_prefix(lr, V, inC, wt, double(top_p) * double(W), ncand, L);
-        }
         // min_p: p >= min_p * max(p), p = e / S rounded to f32
         const float pmax = float(1.0 / S), thr = min_p * pmax;
-        if (min_p > 0.0f) {
-            int64_t nm = 0;
-            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
-                const float x = lr[i];
-                if (inC(i, x) && float(double(exp_diff(x, mx)) / S) >= thr) ++nm;
-            }
-            nm = int64_t(sf_sum_u64(uint64_t(nm), L));
-            n = nm < n ? nm : n;
+        auto minp_ok = [=](float x) { return !(min_p > 0.0f) || float(double(exp_diff(x, mx)) / S) >= thr; };
+        const float y0 = mx / temperature;
+
+        if (!(top_k > 0 || top_p < 1.0f)) {
+            // every candidate (top_k <= 0) passing min_p, in index order
+            auto kept = [=](int64_t, float x) { return sf_cand(x) && minp_ok(x); };
+            double F = 0.0;
+            sf_each(lr, V, al16, [&](int64_t i, float x) {
+                if (kept(i, x)) F += double(exp_diff(x / temperature, y0));
+            });
+            F = sf_sum_f64(F, L);
+            const int64_t cnt = sf_compact(lr, V, al16, L, kept, [&](int64_t pos, int64_t i, float x) {
+                oi[pos] = i;
+                op[pos] = float(double(exp_diff(x / temperature, y0)) / F);
+            });
+            if (threadIdx.x == 0) out_n[row] = cnt;
+            return;
         }
 
-        const bool sorted = top_k > 0 || top_p < 1.0f;
-        const float y0 = mx / temperature;
-        if (!sorted) {
-            // every candidate (top_k <= 0) passing min_p, in index order
-            double F = 0.0;
-            for (int64_t i = threadIdx.x; i < V; i += kSfThreads) {
-                const float x = lr[i];
-                if (sf_cand(x) && (!(min_p > 0.0f) || float(double(exp_diff(x, mx)) / S) >= thr))
-                    F += double(exp_diff(x / temperature, y0));
-            }
-            F = sf_sum_f64(F, L);
-            int64_t base = 0;
-            for (int64_t i0 = 0; i0 < V; i0 += kSfThreads) {
-                const int64_t i = i0 + threadIdx.x;
-                const float x = i < V ? lr[i] : ninf;
-                const bool keep = sf_cand(x) && (!(min_p > 0.0f) || float(double(exp_diff(x, mx)) / S) >= thr);
-                int tot;
-                const int pos = sf_scan(keep ? 1 : 0, L, &tot);
-                if (keep) {
-                    oi[base + pos] = i;
-                    op[base + pos] = float(double(exp_diff(x / temperature, y0)) / F);
-                }
-                base += tot;
-            }
-            if (threadIdx.x == 0) out_n[row] = base;
-            return;
-        }
-        if (n > kSortMax) {
-            if (threadIdx.x == 0) out_n[row] = -1;
-            return;
-        }
-        // the kept prefix: its last entry, then gather and sort it
-        uint32_t fimg = 0, fidx = 0xffffffffu;
-        if (n < nc) sf_select(lr, V, inC, n, L, &fimg, &fidx);
+        // sorted outputs: the largest min(|C|, kSortMax) candidates, gathered and
+        // sorted in LDS
+        const int64_t ng = ncand < kSortMax ? ncand : kSortMax;
+        uint32_t gimg = 0, gidx = 0xffffffffu;
+        if (ng < ncand) sf_select(lr, V, al16, inC, ng, L, &gimg, &gidx);
         for (int i = threadIdx.x; i < kSortMax; i += kSfThreads) L.keys[i] = 0;
         __syncthreads();
-        int64_t base = 0;
-        for (int64_t i0 = 0; i0 < V; i0 += kSfThreads) {
-            const int64_t i = i0 + threadIdx.x;
-            const float x = i < V ? lr[i] : ninf;
-            bool keep = inC(i, x);
-            if (keep) {
+        sf_compact(
+            lr, V, al16, L,
+            [=](int64_t i, float x) {
+                if (!inC(i, x)) return false;
                 const uint32_t g = sf_img(x);
-                keep = g > fimg || (g == fimg && uint32_t(i) <= fidx);
-            }
-            int tot;
-            const int pos = sf_scan(keep ? 1 : 0, L, &tot);
-            if (keep && base + pos < kSortMax)
-                L.keys[base + pos] = (uint64_t(sf_img(x)) << 32) | uint64_t(0xffffffffu - uint32_t(i));
-            base += tot;
-        }
+                return g > gimg || (g == gimg && uint32_t(i) <= gidx);
+            },
+            [&](int64_t pos, int64_t i, float x) {
+                if (pos < kSortMax) L.keys[pos] = (uint64_t(sf_img(x)) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+            });
         __syncthreads();
         int np2 = 1;
-        while (np2 < n) np2 <<= 1;
-        // bitonic sort, descending, of keys[0, np2)
+        while (np2 < ng) np2 <<= 1;
+        // bitonic sort, descending, of keys[0, np2) (zeros sort last)
         for (int size = 2; size <= np2; size <<= 1)
             for (int stride = size >> 1; stride > 0; stride >>= 1) {
                 for (int i = threadIdx.x; i < np2; i += kSfThreads) {
@@ -534,15 +534,59 @@ namespace mg
                 }
                 __syncthreads();
             }
-        double F = 0.0;
-        for (int i = threadIdx.x; i < n; i += kSfThreads)
-            F += double(exp_diff(key_f32(uint32_t(L.keys[i] >> 32)) / temperature, y0));
-        F = sf_sum_f64(F, L);
-        for (int i = threadIdx.x; i < n; i += kSfThreads) {
-            const uint64_t key = L.keys[i];
-            oi[i] = int64_t(0xffffffffu - uint32_t(key));
-            op[i] = float(double(exp_diff(key_f32(uint32_t(key >> 32)) / temperature, y0)) / F);
+        // the cut: thread t holds sorted entries 4t..4t+3
+        const int t0 = 4 * int(threadIdx.x);
+        float xv[4];
+        double ev[4], own = 0.0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bool in = t0 + e < ng;
+            xv[e] = in ? key_f32(uint32_t(L.keys[t0 + e] >> 32)) : 0.0f;
+            ev[e] = in ? double(exp_diff(xv[e], mx)) : 0.0;
+            own += ev[e];
         }
+        int64_t n = ncand;
+        if (top_p < 1.0f) {
+            // searchsorted(cumsum(p), top_p) + 1: the first position whose
+            // cumulative e reaches top_p * S
+            const double target = double(top_p) * S;
+            double run = sf_scan_f64(own, L);
+            uint64_t first = ~uint64_t(0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                run += ev[e];
+                if (t0 + e < ng && run >= target && first == ~uint64_t(0)) first = uint64_t(t0 + e);
+            }
+            first = sf_min_u64(first, L);
+            if (first != ~uint64_t(0))
+                n = int64_t(first) + 1;
+            else if (ng < ncand)
+                n = kSortMax + 1; // the cut lies beyond the gathered candidates
+        }
+        if (min_p > 0.0f) {
+            // a prefix too: p falls along the sorted order
+            int nm = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) nm += t0 + e < ng && minp_ok(xv[e]) ? 1 : 0;
+            int64_t nmt = int64_t(sf_sum_u64(uint64_t(nm), L));
+            if (nmt == ng && ng < ncand) nmt = kSortMax + 1; // min_p keeps past the gathered ones
+            n = nmt < n ? nmt : n;
+        }
+        if (n > ng) {
+            if (threadIdx.x == 0) out_n[row] = -1;
+            return;
+        }
+        double F = 0.0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (t0 + e < n) F += double(exp_diff(xv[e] / temperature, y0));
+        F = sf_sum_f64(F, L);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (t0 + e < n) {
+                oi[t0 + e] = int64_t(0xffffffffu - uint32_t(L.keys[t0 + e]));
+                op[t0 + e] = float(double(exp_diff(xv[e] / temperature, y0)) / F);
+            }
         if (threadIdx.x == 0) out_n[row] = n;
     }
 
