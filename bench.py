@@ -105,7 +105,7 @@ KERNEL_OF = {
     "swiglu": "k_gate_lut<mg::SBf16>",
     "softmax_causal": "k_softmax_fast<mg::SBf16,4,false,true>",
     "rope": "k_rope",
-    "softmax_decode": "k_softmax_partial_fast + k_softmax_finish_fast",
+    "softmax_decode": "k_softmax_partial_buf + k_softmax_finish_buf",
     "dequant_q8_0": "k_dequant_q8_0",
     "vocab_lse_argmax_top64": "k_vocab_chunk + k_vocab_merge",
     "qk_norm_rope_kv": "k_qk_pairs",
@@ -115,7 +115,7 @@ KERNEL_OF = {
     "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
     "attn_prefill_4096": "k_attn_prefill<5,4,1,4>",
     "softmax_causal_softcap30": "k_softmax_fast<cap>",
-    "norm_rows_f32_embed": "k_norm_mixed",
+    "norm_rows_f32_embed": "k_norm_f32rows",
     "sample_rows_topk0": "k_sample_rows",
     "copy_256MiB": "torch copy (memory-only probe)",
     "launch_floor": "torch fill of one float (timing-protocol probe)",

@@ -225,6 +225,27 @@ def test_vocab_large_V(prims):
     vocab_check(prims, O.normal(22, (2, 300000), 0.0, 4.0, F32), F32, 256)
 
 
+@pytest.mark.parametrize("dt,rows,V,K", ((F32, 49, 201088, 64), (BF16, 41, 100000, 64), (F32, 70, 60000, 20),
+                                         (F32, 40, 201088, 256), (F32, 2, 4096 * 700, 64)))
+def test_vocab_many_chunks(prims, dt, rows, V, K):
+    """more chunk waves than the chip holds at once (49 x 50, 41 x 25 in bf16,
+    70 x 15, 40 x 50 at K = 256), and a row of 700 chunks"""
+    vocab_check(prims, O.normal(27, (rows, V), 0.0, 4.0, dt), dt, K)
+
+
+def test_vocab_strided_rows(prims):
+    """rows 64 elements apart beyond V (ld > V)"""
+    rows, V, ld = 33, 131072, 131072 + 64
+    wide = O.normal(28, (rows, ld), 0.0, 4.0, F32)
+    dL = to_dev(wide, F32)[:, :V]
+    lse, am, ti, tv = prims.vocab_reduce(dL, 64)
+    r_lse, r_am, r_ti, r_tv = O.vocab_reduce(O.to_f64(wide, F32)[:, :V], 64)
+    assert np.abs(lse.cpu().numpy() / r_lse - 1).max() <= 1e-6
+    assert np.array_equal(am.cpu().numpy(), r_am)
+    assert np.array_equal(ti.cpu().numpy(), r_ti)
+    assert np.array_equal(tv.cpu().numpy().astype(np.float64), r_tv)
+
+
 def test_vocab_short_tails(prims):
     """last chunk holding 1, 63, 100 and 2047 entries"""
     for V in (2048 * 3 + 1, 2048 + 63, 2048 * 5 + 100, 2048 * 2 + 2047):
