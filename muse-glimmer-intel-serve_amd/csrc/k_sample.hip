@@ -13,6 +13,7 @@
 // One wave per row, candidate i in lane i / 4, slot i % 4 (K <= 256).
 #include "mg_device.hpp"
 #include "mg_internal.hpp"
+#include "mg_wave_sort.hpp"
 
 namespace mg
 {
@@ -170,21 +171,31 @@ namespace mg
     // found by an f64 prefix sum in that order; a row whose kept prefix does
     // not fit, or that holds +inf (whose reference probabilities are NaN, so
     // its draw raises), gets count -1 and is left to the host.
-    // Selections are MSD radix passes over the 32-bit order-preserving image
-    // of the values with an LDS count histogram; counts are integers, so every
-    // result is independent of the order in which threads add, and the f64
-    // sums reduce in a fixed order.
+    // The gathering: pass 1 also counts the candidates per 12-bit prefix of
+    // their 32-bit order-preserving image (4096 bins); the bin holding the
+    // kSortMax-th largest fixes a threshold, and the pass that sums S gathers
+    // every candidate at or above it into LDS (at most kGatherCap; positions
+    // from an LDS counter, in no particular order: the keys are unique and
+    // sorted next). Rows whose threshold bin overflows that room, and the
+    // top_k selection, take MSD radix passes over the image (and the index
+    // among equal values) with an LDS count histogram instead. Counts are
+    // integers, so every result is independent of the order in which threads
+    // add, and the f64 sums reduce in a fixed order.
     constexpr int kSortMax = 4096;
+    constexpr int kGatherCap = 8192;
+    constexpr int kHistBits = 12;
     constexpr int kSfThreads = 1024;
 
     struct SfLds
     {
         uint32_t cnt[256];
-        uint64_t keys[kSortMax];
+        uint32_t hist[1 << kHistBits];
+        uint64_t keys[kGatherCap];
         double red[kSortMax / 4];
         double redd[kSfThreads / 64];
         uint64_t redu[kSfThreads / 64];
         uint32_t bc[4]; // broadcast words
+        uint32_t gcount; // keys gathered so far
     };
 
     MG_DEV uint32_t sf_img(float x) { return f32_key(x + 0.0f); } // -0 ranks with +0
@@ -264,26 +275,116 @@ namespace mg
         return base + in_wave;
     }
 
-    // f(i, x) for every entry of the row; 16-byte loads on 16-byte-aligned rows
-    // (thread t takes entries 4t..4t+3 of each 4096-entry block, four blocks in
-    // flight), entry by entry otherwise. Every lane of a wave calls f the same
-    // number of times except in the row's last block (lanes past the end idle).
+    // keys[0, n) sorted descending, n a power of two: each wave sorts its n/16
+    // contiguous keys in registers (wave_bitonic, direction alternating by
+    // wave as the network's runs do), then each merge level takes its strides
+    // of n/16 and more through LDS and the rest in registers
+    // (wave_bitonic_merge). Callers synchronize before (the keys written).
+    template <int R>
+    MG_DEV void sf_sort_regs(uint64_t *keys, int n)
+    {
+        constexpr int SEG = 64 * R;
+        const int lane = threadIdx.x & 63;
+        const int base = int(threadIdx.x >> 6) * SEG;
+        uint64_t a[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) a[r] = keys[base + 64 * r + lane];
+        if ((base & SEG) == 0)
+            wave_bitonic<uint64_t, R, true>(a);
+        else
+            wave_bitonic<uint64_t, R, false>(a);
+        for (int size = 2 * SEG; size <= n; size <<= 1) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) keys[base + 64 * r + lane] = a[r];
+            __syncthreads();
+            for (int stride = size >> 1; stride >= SEG; stride >>= 1) {
+                for (int i = threadIdx.x; i < n; i += kSfThreads) {
+                    const int j = i ^ stride;
+                    if (j > i) {
+                        const bool desc = (i & size) == 0;
+                        const uint64_t x = keys[i], y = keys[j];
+                        if (desc ? x < y : x > y) {
+                            keys[i] = y;
+                            keys[j] = x;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) a[r] = keys[base + 64 * r + lane];
+            wave_bitonic_merge<uint64_t, R>(a, (base & size) == 0);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) keys[base + 64 * r + lane] = a[r];
+        __syncthreads();
+    }
+    MG_DEV void sf_sort_desc(uint64_t *keys, int n)
+    {
+        static_assert(kGatherCap == 8 * kSfThreads, "sf_sort_desc: at most eight keys a thread");
+        switch (n) {
+        case kSfThreads: sf_sort_regs<1>(keys, n); return;
+        case 2 * kSfThreads: sf_sort_regs<2>(keys, n); return;
+        case 4 * kSfThreads: sf_sort_regs<4>(keys, n); return;
+        case 8 * kSfThreads: sf_sort_regs<8>(keys, n); return;
+        default: break;
+        }
+        // fewer keys than threads: the network in LDS
+        for (int size = 2; size <= n; size <<= 1)
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                const int i = threadIdx.x;
+                const int j = i ^ stride;
+                if (i < n && j > i) {
+                    const bool desc = (i & size) == 0;
+                    const uint64_t x = keys[i], y = keys[j];
+                    if (desc ? x < y : x > y) {
+                        keys[i] = y;
+                        keys[j] = x;
+                    }
+                }
+                __syncthreads();
+            }
+    }
+
+    // f(i, x) for every entry of the row, in a fixed order per thread; 16-byte
+    // loads on 16-byte-aligned rows, entry by entry otherwise. Aligned rows go
+    // in groups of 4 x 4096 entries (thread t takes entries 4t..4t+3 of each
+    // 4096), the next group's loads in flight while f runs over the current
+    // one (two register sets; the last group's successor is re-read in place
+    // of a group past the end, so no branch stands between the loads and
+    // their waits). Every lane of a wave calls f the same number of times
+    // except in the row's last 16 384 entries (lanes past the end idle).
     template <class F>
     MG_DEV void sf_each(const float *lr, int64_t V, bool al16, F f)
     {
         if (al16) {
             const int64_t V4 = V >> 2;
             const Vec<float, 4> *p = reinterpret_cast<const Vec<float, 4> *>(lr);
-            int64_t g = threadIdx.x;
-            for (; g + 3 * kSfThreads < V4; g += 4 * kSfThreads) {
-                Vec<float, 4> a[4];
+            constexpr int64_t G = 4 * kSfThreads; // vectors per group
+            const int64_t ng = V4 / G;            // whole groups
+            auto load = [&](Vec<float, 4>(&r)[4], int64_t grp) {
+                const int64_t q = (grp < ng ? grp : ng - 1) * G + threadIdx.x;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) a[u] = p[g + u * kSfThreads];
+                for (int u = 0; u < 4; ++u) r[u] = p[q + u * kSfThreads];
+            };
+            auto run = [&](const Vec<float, 4>(&r)[4], int64_t grp) {
+                const int64_t q = grp * G + threadIdx.x;
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) f(4 * (g + u * kSfThreads) + e, a[u].v[e]);
+                    for (int e = 0; e < 4; ++e) f(4 * (q + u * kSfThreads) + e, r[u].v[e]);
+            };
+            if (ng > 0) {
+                Vec<float, 4> A[4], B[4];
+                load(A, 0);
+                for (int64_t grp = 0; grp < ng; grp += 2) {
+                    load(B, grp + 1);
+                    run(A, grp);
+                    load(A, grp + 2);
+                    if (grp + 1 < ng) run(B, grp + 1);
+                }
             }
+            int64_t g = ng * G + threadIdx.x;
             for (; g < V4; g += kSfThreads) {
                 const Vec<float, 4> a = p[g];
 #pragma unroll
@@ -426,8 +527,16 @@ namespace mg
         float *op = out_p + row * V;
         const bool al16 = (reinterpret_cast<uintptr_t>(lr) & 15u) == 0;
 
+        // sorted outputs (value order) when top_k > 0 or top_p < 1
+        const bool sorted = top_k > 0 || top_p < 1.0f;
+        constexpr int kBins = 1 << kHistBits;
+        if (sorted) {
+            for (int b = threadIdx.x; b < kBins; b += kSfThreads) L.hist[b] = 0;
+            __syncthreads();
+        }
+
         // pass 1: finite count, candidate count, the candidates' largest
-        // image, np.argmax
+        // image, np.argmax; for sorted outputs the candidates' image prefixes
         int64_t nfin = 0, nc = 0;
         uint64_t mk = 0;   // image of the candidates' maximum (0: none)
         uint64_t best = 0; // (image with NaN on top) << 32 | ~index
@@ -436,6 +545,7 @@ namespace mg
             if (sf_cand(x)) {
                 ++nc;
                 mk = sf_img(x) > mk ? sf_img(x) : mk;
+                if (sorted) atomicAdd(&L.hist[sf_img(x) >> (32 - kHistBits)], 1u);
             }
             const uint32_t g = x != x ? 0xffffffffu : sf_img(x);
             const uint64_t key = (uint64_t(g) << 32) | uint64_t(0xffffffffu - uint32_t(i));
@@ -471,10 +581,65 @@ namespace mg
             return g > kimg || (g == kimg && uint32_t(i) <= kidx);
         };
 
-        // S = sum of e over C (f64, fixed order)
+        // sorted outputs: the largest ng = min(|C|, kSortMax) entries of C,
+        // which are C's largest (C is a prefix of the candidates in that
+        // order). They lie in the bins at or above bstar, the bin holding the
+        // candidates' ng-th largest (every bin when ng = |C|): gathered when
+        // those bins hold at most kGatherCap candidates.
+        const int64_t ng = ncand < kSortMax ? ncand : kSortMax;
+        uint32_t bstar = 0;
+        bool gather = false;
+        if (sorted) {
+            gather = true;
+            if (ng < ncand) {
+                // thread t holds bins kBins-1-BPT*t-e: its exclusive prefix
+                // counts the candidates in higher bins
+                constexpr int BPT = kBins / kSfThreads;
+                uint32_t c[BPT];
+                int own = 0;
+#pragma unroll
+                for (int e = 0; e < BPT; ++e) {
+                    c[e] = L.hist[kBins - 1 - BPT * int(threadIdx.x) - e];
+                    own += int(c[e]);
+                }
+                int tot;
+                int64_t acc = sf_scan(own, L, &tot);
+#pragma unroll
+                for (int e = 0; e < BPT; ++e) {
+                    if (acc < ng && acc + c[e] >= ng) {
+                        L.bc[0] = uint32_t(kBins - 1 - BPT * int(threadIdx.x) - e);
+                        L.bc[1] = uint32_t(acc + c[e]);
+                    }
+                    acc += c[e];
+                }
+                __syncthreads();
+                bstar = L.bc[0];
+                gather = L.bc[1] <= uint32_t(kGatherCap);
+                __syncthreads();
+            }
+            if (threadIdx.x == 0) L.gcount = 0;
+            __syncthreads();
+        }
+
+        // S = sum of e over C (f64, fixed order), gathering alongside: a
+        // wave's takers share one LDS counter update
         double S = 0.0;
         sf_each(lr, V, al16, [&](int64_t i, float x) {
-            if (inC(i, x)) S += double(exp_diff(x, mx));
+            const bool in = inC(i, x);
+            if (in) S += double(exp_diff(x, mx));
+            if (gather) {
+                const bool take = in && (sf_img(x) >> (32 - kHistBits)) >= bstar;
+                const uint64_t m = __builtin_amdgcn_ballot_w64(take);
+                if (m) {
+                    const int lead = int(__builtin_ctzll(m));
+                    uint32_t at = 0;
+                    if (int(threadIdx.x & 63) == lead) at = atomicAdd(&L.gcount, uint32_t(__builtin_popcountll(m)));
+                    at = uint32_t(__builtin_amdgcn_readlane(int(at), lead));
+                    if (take)
+                        L.keys[at + uint32_t(lane_rank(m))] =
+                            (uint64_t(sf_img(x)) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+                }
+            }
         });
         S = sf_sum_f64(S, L);
         // min_p: p >= min_p * max(p), p = e / S rounded to f32
@@ -482,7 +647,7 @@ namespace mg
         auto minp_ok = [=](float x) { return !(min_p > 0.0f) || float(double(exp_diff(x, mx)) / S) >= thr; };
         const float y0 = mx / temperature;
 
-        if (!(top_k > 0 || top_p < 1.0f)) {
+        if (!sorted) {
             // every candidate (top_k <= 0) passing min_p, in index order
             auto kept = [=](int64_t, float x) { return sf_cand(x) && minp_ok(x); };
             double F = 0.0;
@@ -498,42 +663,34 @@ namespace mg
             return;
         }
 
-        // sorted outputs: the largest min(|C|, kSortMax) candidates, gathered and
-        // sorted in LDS
-        const int64_t ng = ncand < kSortMax ? ncand : kSortMax;
-        uint32_t gimg = 0, gidx = 0xffffffffu;
-        if (ng < ncand) sf_select(lr, V, al16, inC, ng, L, &gimg, &gidx);
-        for (int i = threadIdx.x; i < kSortMax; i += kSfThreads) L.keys[i] = 0;
-        __syncthreads();
-        sf_compact(
-            lr, V, al16, L,
-            [=](int64_t i, float x) {
-                if (!inC(i, x)) return false;
-                const uint32_t g = sf_img(x);
-                return g > gimg || (g == gimg && uint32_t(i) <= gidx);
-            },
-            [&](int64_t pos, int64_t i, float x) {
-                if (pos < kSortMax) L.keys[pos] = (uint64_t(sf_img(x)) << 32) | uint64_t(0xffffffffu - uint32_t(i));
-            });
-        __syncthreads();
+        // the sorted outputs' keys (value desc, index asc) in LDS, sorted; the
+        // first ng are the largest ng of C
         int np2 = 1;
-        while (np2 < ng) np2 <<= 1;
-        // bitonic sort, descending, of keys[0, np2) (zeros sort last)
-        for (int size = 2; size <= np2; size <<= 1)
-            for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                for (int i = threadIdx.x; i < np2; i += kSfThreads) {
-                    const int j = i ^ stride;
-                    if (j > i) {
-                        const bool desc = (i & size) == 0;
-                        const uint64_t a = L.keys[i], b = L.keys[j];
-                        if (desc ? a < b : a > b) {
-                            L.keys[i] = b;
-                            L.keys[j] = a;
-                        }
-                    }
-                }
-                __syncthreads();
-            }
+        if (gather) {
+            const int gn = int(L.gcount); // at least ng, at most kGatherCap
+            while (np2 < gn) np2 <<= 1;
+            for (int i = gn + int(threadIdx.x); i < np2; i += kSfThreads) L.keys[i] = 0; // zeros sort last
+        } else {
+            // the threshold bin overflows the room: the ng-th largest of C by
+            // radix passes, then C's entries up to it in index order
+            uint32_t gimg = 0, gidx = 0xffffffffu;
+            sf_select(lr, V, al16, inC, ng, L, &gimg, &gidx);
+            for (int i = threadIdx.x; i < kSortMax; i += kSfThreads) L.keys[i] = 0;
+            __syncthreads();
+            sf_compact(
+                lr, V, al16, L,
+                [=](int64_t i, float x) {
+                    if (!inC(i, x)) return false;
+                    const uint32_t g = sf_img(x);
+                    return g > gimg || (g == gimg && uint32_t(i) <= gidx);
+                },
+                [&](int64_t pos, int64_t i, float x) {
+                    if (pos < kSortMax) L.keys[pos] = (uint64_t(sf_img(x)) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+                });
+            while (np2 < ng) np2 <<= 1;
+        }
+        __syncthreads();
+        sf_sort_desc(L.keys, np2);
         // the cut: thread t holds sorted entries 4t..4t+3
         const int t0 = 4 * int(threadIdx.x);
         float xv[4];

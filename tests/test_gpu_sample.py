@@ -139,7 +139,8 @@ def test_sample_rows_matches_reference_golden(prims):
 
 
 @pytest.mark.parametrize("top_k,top_p,min_p,temp", ((0, 0.95, 0.0, 1.0), (0, 0.95, 0.02, 0.7), (0, 1.0, 0.01, 1.0),
-                                                    (1000, 1.0, 0.0, 0.8), (3000, 0.95, 0.0, 1.0)))
+                                                    (1000, 1.0, 0.0, 0.8), (3000, 0.95, 0.0, 1.0),
+                                                    (10000, 0.95, 0.0, 1.0)))
 def test_sample_rows_vocab_scale(prims, top_k, top_p, min_p, temp):
     """[8, 201088] rows at the vocab pass's shape against oracle.sample_rows (pinned
     to the reference above): top_k = 0 with top_p = 0.95 (nuclei of a few hundred
@@ -177,6 +178,39 @@ def test_sample_rows_vocab_scale(prims, top_k, top_p, min_p, temp):
         assert n[r] == len(wi), (r, n[r], len(wi))
         assert np.array_equal(ids[r, :n[r]], wi), r
         assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, r
+
+
+@pytest.mark.parametrize("tied", (False, True))
+def test_sample_rows_crowded_threshold_bin(prims, tied):
+    """the 4096th largest candidate in a bin of the 12-bit image prefix that holds
+    60 000 candidates (all of them in [1, 1.1), or all equal to 1.0): more than
+    the gathering room, so the rows take the radix selection (ties broken by
+    index) and the ordered compaction; 3000 larger logits hold the nucleus"""
+    import torch
+    rows, V = 2, 201088
+    rng = np.random.default_rng(52)
+    L = np.full((rows, V), -5.0, np.float32)
+    for r in range(rows):
+        pos = rng.permutation(V)
+        L[r, pos[:3000]] = rng.uniform(10.0, 12.0, 3000).astype(np.float32)
+        L[r, pos[3000:63000]] = 1.0 if tied else rng.uniform(1.0, 1.1, 60000).astype(np.float32)
+    for top_k, top_p in ((0, 0.95), (20000, 0.9)):
+        for r in range(rows):
+            # the float32 and exact cumulative sums cut at the same place
+            x = np.sort(L[r])[::-1][:top_k or V]
+            e32 = np.exp(x - x[0])
+            p64 = softmax(x.astype(np.float64))
+            c32 = np.searchsorted(np.cumsum(e32 / e32.sum()), np.float32(top_p)) + 1
+            c64 = np.searchsorted(np.cumsum(p64), np.float64(np.float32(top_p))) + 1
+            assert c32 == c64 and c32 < 3000, (r, c32, c64)
+        want = O.sample_rows(L, np.argmax(L, axis=1), top_k, 1.0, top_p, 0.0)
+        ids, probs, n = prims.sample_rows(torch.from_numpy(L).cuda(), top_k, 1.0, top_p, 0.0)
+        ids, probs, n = ids.cpu().numpy(), probs.cpu().numpy(), n.cpu().numpy()
+        for r in range(rows):
+            wi, wp = want[r]
+            assert n[r] == len(wi), (top_k, r, n[r], len(wi))
+            assert np.array_equal(ids[r, :n[r]], wi), (top_k, r)
+            assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, (top_k, r)
 
 
 def test_sample_rows_left_to_host(prims):
