@@ -171,31 +171,33 @@ namespace mg
     // found by an f64 prefix sum in that order; a row whose kept prefix does
     // not fit, or that holds +inf (whose reference probabilities are NaN, so
     // its draw raises), gets count -1 and is left to the host.
-    // The gathering: pass 1 also counts the candidates per 12-bit prefix of
-    // their 32-bit order-preserving image (4096 bins); the bin holding the
-    // kSortMax-th largest fixes a threshold, and the pass that sums S gathers
-    // every candidate at or above it into LDS (at most kGatherCap; positions
-    // from an LDS counter, in no particular order: the keys are unique and
-    // sorted next). Rows whose threshold bin overflows that room, and the
-    // top_k selection, take MSD radix passes over the image (and the index
-    // among equal values) with an LDS count histogram instead. Counts are
-    // integers, so every result is independent of the order in which threads
-    // add, and the f64 sums reduce in a fixed order.
+    // The gathering: pass 1 also counts the candidates per 13-bit prefix of
+    // their 32-bit order-preserving image (8192 bins); the bin holding the
+    // kSortMax-th largest (bstar) fixes a threshold, and the pass that sums S
+    // gathers the candidates above it (fewer than kSortMax) and those in it
+    // (when at most kSortMax) into two LDS regions (positions from LDS
+    // counters, in no particular order: the keys are unique and sorted
+    // next); the two are sorted apart and the second's largest appended.
+    // Rows whose threshold bin holds more, and the top_k selection, take MSD
+    // radix passes over the image (and the index among equal values) with an
+    // LDS count histogram instead. Counts are integers, so every result is
+    // independent of the order in which threads add, and the f64 sums reduce
+    // in a fixed order.
     constexpr int kSortMax = 4096;
-    constexpr int kGatherCap = 8192;
-    constexpr int kHistBits = 12;
+    constexpr int kGatherCap = 2 * kSortMax;
+    constexpr int kHistBits = 13;
     constexpr int kSfThreads = 1024;
 
     struct SfLds
     {
         uint32_t cnt[256];
-        uint32_t hist[1 << kHistBits];
+        uint32_t hist[(1 << kHistBits) + 1]; // the last: a spare bin for non-candidates
         uint64_t keys[kGatherCap];
         double red[kSortMax / 4];
         double redd[kSfThreads / 64];
         uint64_t redu[kSfThreads / 64];
         uint32_t bc[4]; // broadcast words
-        uint32_t gcount; // keys gathered so far
+        uint32_t gcount[2]; // keys gathered so far above the threshold bin, in it
     };
 
     MG_DEV uint32_t sf_img(float x) { return f32_key(x + 0.0f); } // -0 ranks with +0
@@ -321,12 +323,11 @@ namespace mg
     }
     MG_DEV void sf_sort_desc(uint64_t *keys, int n)
     {
-        static_assert(kGatherCap == 8 * kSfThreads, "sf_sort_desc: at most eight keys a thread");
+        static_assert(kSortMax <= 4 * kSfThreads, "sf_sort_desc: at most four keys a thread");
         switch (n) {
         case kSfThreads: sf_sort_regs<1>(keys, n); return;
         case 2 * kSfThreads: sf_sort_regs<2>(keys, n); return;
         case 4 * kSfThreads: sf_sort_regs<4>(keys, n); return;
-        case 8 * kSfThreads: sf_sort_regs<8>(keys, n); return;
         default: break;
         }
         // fewer keys than threads: the network in LDS
@@ -538,23 +539,28 @@ namespace mg
         // pass 1: finite count, candidate count, the candidates' largest
         // image, np.argmax; for sorted outputs the candidates' image prefixes
         int64_t nfin = 0, nc = 0;
-        uint64_t mk = 0;   // image of the candidates' maximum (0: none)
-        uint64_t best = 0; // (image with NaN on top) << 32 | ~index
+        uint32_t mk = 0; // image of the candidates' maximum (0: none)
+        // the thread's first largest entry (image with NaN on top) and its
+        // index: a thread visits its entries in index order
+        uint32_t bg = 0, bi = 0xffffffffu;
         sf_each(lr, V, al16, [&](int64_t i, float x) {
             nfin += __builtin_isfinite(x) ? 1 : 0;
-            if (sf_cand(x)) {
-                ++nc;
-                mk = sf_img(x) > mk ? sf_img(x) : mk;
-                if (sorted) atomicAdd(&L.hist[sf_img(x) >> (32 - kHistBits)], 1u);
+            const bool cand = sf_cand(x);
+            const uint32_t img = sf_img(x);
+            nc += cand ? 1 : 0;
+            mk = cand && img > mk ? img : mk;
+            if (sorted) atomicAdd(&L.hist[cand ? img >> (32 - kHistBits) : uint32_t(kBins)], 1u);
+            const uint32_t g = x != x ? 0xffffffffu : img;
+            if (g > bg) {
+                bg = g;
+                bi = uint32_t(i);
             }
-            const uint32_t g = x != x ? 0xffffffffu : sf_img(x);
-            const uint64_t key = (uint64_t(g) << 32) | uint64_t(0xffffffffu - uint32_t(i));
-            best = key > best ? key : best;
         });
         nfin = int64_t(sf_sum_u64(uint64_t(nfin), L));
         nc = int64_t(sf_sum_u64(uint64_t(nc), L));
-        best = sf_max_u64(best, L);
-        mk = sf_max_u64(mk, L);
+        // (image, ~index): the largest is np.argmax's entry
+        const uint64_t best = sf_max_u64((uint64_t(bg) << 32) | uint64_t(0xffffffffu - bi), L);
+        mk = uint32_t(sf_max_u64(mk, L));
         if (nfin == 0 || !(temperature > 0.0f)) {
             if (threadIdx.x == 0) {
                 oi[0] = nfin == 0 && raw_amax ? raw_amax[row] : int64_t(0xffffffffu - uint32_t(best));
@@ -582,16 +588,17 @@ namespace mg
         };
 
         // sorted outputs: the largest ng = min(|C|, kSortMax) entries of C,
-        // which are C's largest (C is a prefix of the candidates in that
-        // order). They lie in the bins at or above bstar, the bin holding the
-        // candidates' ng-th largest (every bin when ng = |C|): gathered when
-        // those bins hold at most kGatherCap candidates.
+        // which are the candidates' largest (C is a prefix of the candidates
+        // in that order). They lie in the bins above bstar, the bin holding
+        // the candidates' ng-th largest, and in bstar (every one of C when
+        // ng = |C|): gathered when bstar holds at most kSortMax candidates.
         const int64_t ng = ncand < kSortMax ? ncand : kSortMax;
+        const bool gall = ng == ncand;
         uint32_t bstar = 0;
         bool gather = false;
         if (sorted) {
             gather = true;
-            if (ng < ncand) {
+            if (!gall) {
                 // thread t holds bins kBins-1-BPT*t-e: its exclusive prefix
                 // counts the candidates in higher bins
                 constexpr int BPT = kBins / kSfThreads;
@@ -608,36 +615,32 @@ namespace mg
                 for (int e = 0; e < BPT; ++e) {
                     if (acc < ng && acc + c[e] >= ng) {
                         L.bc[0] = uint32_t(kBins - 1 - BPT * int(threadIdx.x) - e);
-                        L.bc[1] = uint32_t(acc + c[e]);
+                        L.bc[1] = c[e];
                     }
                     acc += c[e];
                 }
                 __syncthreads();
                 bstar = L.bc[0];
-                gather = L.bc[1] <= uint32_t(kGatherCap);
+                gather = L.bc[1] <= uint32_t(kSortMax);
                 __syncthreads();
             }
-            if (threadIdx.x == 0) L.gcount = 0;
+            if (threadIdx.x < 2) L.gcount[threadIdx.x] = 0;
             __syncthreads();
         }
 
-        // S = sum of e over C (f64, fixed order), gathering alongside: a
-        // wave's takers share one LDS counter update
+        // S = sum of e over C (f64, fixed order), gathering alongside: region
+        // 0 (keys[0, kSortMax)) the entries above bstar, or all of C; region
+        // 1 (keys[kSortMax, 2 kSortMax)) those in bstar
         double S = 0.0;
         sf_each(lr, V, al16, [&](int64_t i, float x) {
             const bool in = inC(i, x);
             if (in) S += double(exp_diff(x, mx));
             if (gather) {
-                const bool take = in && (sf_img(x) >> (32 - kHistBits)) >= bstar;
-                const uint64_t m = __builtin_amdgcn_ballot_w64(take);
-                if (m) {
-                    const int lead = int(__builtin_ctzll(m));
-                    uint32_t at = 0;
-                    if (int(threadIdx.x & 63) == lead) at = atomicAdd(&L.gcount, uint32_t(__builtin_popcountll(m)));
-                    at = uint32_t(__builtin_amdgcn_readlane(int(at), lead));
-                    if (take)
-                        L.keys[at + uint32_t(lane_rank(m))] =
-                            (uint64_t(sf_img(x)) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+                const uint32_t img = sf_img(x), bin = img >> (32 - kHistBits);
+                if (in && (gall || bin >= bstar)) {
+                    const int reg = gall || bin > bstar ? 0 : 1;
+                    const uint32_t at = atomicAdd(&L.gcount[reg], 1u);
+                    L.keys[reg * kSortMax + int(at)] = (uint64_t(img) << 32) | uint64_t(0xffffffffu - uint32_t(i));
                 }
             }
         });
@@ -665,12 +668,25 @@ namespace mg
 
         // the sorted outputs' keys (value desc, index asc) in LDS, sorted; the
         // first ng are the largest ng of C
-        int np2 = 1;
         if (gather) {
-            const int gn = int(L.gcount); // at least ng, at most kGatherCap
-            while (np2 < gn) np2 <<= 1;
-            for (int i = gn + int(threadIdx.x); i < np2; i += kSfThreads) L.keys[i] = 0; // zeros sort last
+            // region 0 sorted; region 1 (the rest of the largest ng) sorted and
+            // its largest ng - n0 appended (every one of them is below region
+            // 0's keys: a lower bin)
+            const int n0 = int(L.gcount[0]), n1 = gall ? 0 : int(L.gcount[1]);
+            int p0 = 1, p1 = 1;
+            while (p0 < n0) p0 <<= 1;
+            while (p1 < n1) p1 <<= 1;
+            for (int i = n0 + int(threadIdx.x); i < p0; i += kSfThreads) L.keys[i] = 0; // zeros sort last
+            for (int i = n1 + int(threadIdx.x); i < p1; i += kSfThreads) L.keys[kSortMax + i] = 0;
+            __syncthreads();
+            sf_sort_desc(L.keys, p0);
+            if (!gall) {
+                sf_sort_desc(L.keys + kSortMax, p1);
+                for (int i = threadIdx.x; i < int(ng) - n0; i += kSfThreads) L.keys[n0 + i] = L.keys[kSortMax + i];
+                __syncthreads();
+            }
         } else {
+            int np2 = 1;
             // the threshold bin overflows the room: the ng-th largest of C by
             // radix passes, then C's entries up to it in index order
             uint32_t gimg = 0, gidx = 0xffffffffu;
@@ -688,9 +704,9 @@ namespace mg
                     if (pos < kSortMax) L.keys[pos] = (uint64_t(sf_img(x)) << 32) | uint64_t(0xffffffffu - uint32_t(i));
                 });
             while (np2 < ng) np2 <<= 1;
+            __syncthreads();
+            sf_sort_desc(L.keys, np2);
         }
-        __syncthreads();
-        sf_sort_desc(L.keys, np2);
         // the cut: thread t holds sorted entries 4t..4t+3
         const int t0 = 4 * int(threadIdx.x);
         float xv[4];

@@ -213,6 +213,23 @@ def test_sample_rows_crowded_threshold_bin(prims, tied):
             assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, (top_k, r)
 
 
+def test_sample_rows_threshold_bin_on_top(prims):
+    """the 4096 largest candidates all in the top bin of the image prefix (992 <=
+    x < 1024, a bin 32 wide), nothing above it: the whole sorted prefix comes
+    from the gathered threshold bin"""
+    import torch
+    V = 20000
+    rng = np.random.default_rng(53)
+    L = np.full((1, V), -5.0, np.float32)
+    L[0, rng.permutation(V)[:4096]] = rng.uniform(992.0, 1024.0, 4096).astype(np.float32)
+    want = O.sample_rows(L, np.argmax(L, axis=1), 0, 8.0, 0.95, 0.0)
+    ids, probs, n = prims.sample_rows(torch.from_numpy(L).cuda(), 0, 8.0, 0.95, 0.0)
+    (wi, wp), = want
+    assert int(n.cpu()[0]) == len(wi)
+    assert np.array_equal(ids.cpu().numpy()[0, :len(wi)], wi)
+    assert np.abs(probs.cpu().numpy()[0, :len(wi)].astype(np.float64) - wp).max() <= 2e-6
+
+
 def test_sample_rows_left_to_host(prims):
     """count -1: a nucleus of more than 4096 sorted candidates (flat logits), and a
     row holding +inf (the reference's probabilities are NaN there); other rows of
