@@ -188,15 +188,19 @@ namespace mg
     constexpr int kHistBits = 13;
     constexpr int kSfThreads = 1024;
 
-    struct SfLds
+    // work-group reduction scratch, and each kernel's LDS around it
+    struct SfRed
+    {
+        double red[kSfThreads];
+        double redd[kSfThreads / 64];
+        uint64_t redu[kSfThreads / 64];
+        uint32_t bc[4]; // broadcast words
+    };
+    struct SfLds : SfRed
     {
         uint32_t cnt[256];
         uint32_t hist[(1 << kHistBits) + 1]; // the last: a spare bin for non-candidates
         uint64_t keys[kGatherCap];
-        double red[kSortMax / 4];
-        double redd[kSfThreads / 64];
-        uint64_t redu[kSfThreads / 64];
-        uint32_t bc[4]; // broadcast words
         uint32_t gcount[2]; // keys gathered so far above the threshold bin, in it
     };
 
@@ -204,7 +208,7 @@ namespace mg
     MG_DEV bool sf_cand(float x) { return x > -__builtin_huge_valf(); } // NaN and -inf fail
 
     // work-group sums in a fixed order (every thread returns the total)
-    MG_DEV double sf_sum_f64(double v, SfLds &L)
+    MG_DEV double sf_sum_f64(double v, SfRed &L)
     {
         v = dpp_sum(v);
         if ((threadIdx.x & 63) == 0) L.redd[threadIdx.x >> 6] = v;
@@ -215,7 +219,7 @@ namespace mg
         return t;
     }
     template <class OP>
-    MG_DEV uint64_t sf_red_u64(uint64_t v, SfLds &L, OP op)
+    MG_DEV uint64_t sf_red_u64(uint64_t v, SfRed &L, OP op)
     {
         const int lane = threadIdx.x & 63;
 #pragma unroll
@@ -230,20 +234,20 @@ namespace mg
         __syncthreads();
         return t;
     }
-    MG_DEV uint64_t sf_sum_u64(uint64_t v, SfLds &L)
+    MG_DEV uint64_t sf_sum_u64(uint64_t v, SfRed &L)
     {
         return sf_red_u64(v, L, [](uint64_t a, uint64_t b) { return a + b; });
     }
-    MG_DEV uint64_t sf_max_u64(uint64_t v, SfLds &L)
+    MG_DEV uint64_t sf_max_u64(uint64_t v, SfRed &L)
     {
         return sf_red_u64(v, L, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
     }
-    MG_DEV uint64_t sf_min_u64(uint64_t v, SfLds &L)
+    MG_DEV uint64_t sf_min_u64(uint64_t v, SfRed &L)
     {
         return sf_red_u64(v, L, [](uint64_t a, uint64_t b) { return a < b ? a : b; });
     }
     // exclusive prefix over the work-group in thread order; total in *tot
-    MG_DEV int sf_scan(int v, SfLds &L, int *tot)
+    MG_DEV int sf_scan(int v, SfRed &L, int *tot)
     {
         const int incl = wave_prefix_sum(v);
         if ((threadIdx.x & 63) == 63) L.redu[threadIdx.x >> 6] = uint64_t(incl);
@@ -260,7 +264,7 @@ namespace mg
     }
     // the same for f64 values: each thread's exclusive prefix, summed in a
     // fixed order (the lanes' values through LDS, then the waves')
-    MG_DEV double sf_scan_f64(double v, SfLds &L)
+    MG_DEV double sf_scan_f64(double v, SfRed &L)
     {
         L.red[threadIdx.x] = v;
         __syncthreads();
@@ -515,14 +519,101 @@ namespace mg
         *idx = ipre;
     }
 
-    __global__ __launch_bounds__(kSfThreads) void k_sample_rows(const float *__restrict__ lg, int64_t ld, int64_t V,
-                                                               const int64_t *__restrict__ raw_amax, int64_t top_k,
-                                                               float temperature, float top_p, float min_p,
-                                                               int64_t *__restrict__ out_ids,
-                                                               float *__restrict__ out_p, int64_t *__restrict__ out_n)
+    // The sorted outputs from keys[0, ng) (LDS), C's largest ng in (value
+    // desc, index asc) order (ncand = |C|, S its e sum, mx its maximum): the
+    // top_p and min_p cuts as prefixes of that order, then softmax(x / T)
+    // over the kept prefix into oi / op and its length into *out_n (-1 when
+    // the cut lies past the ng keys at hand).
+    MG_DEV void sf_emit_sorted(SfRed &L, const uint64_t *keys, int64_t ng, int64_t ncand, double S, float mx,
+                               float temperature, float top_p, float min_p, int64_t *oi, float *op, int64_t *out_n)
     {
-        __shared__ SfLds L;
-        const int64_t row = blockIdx.x;
+        const float pmax = float(1.0 / S), thr = min_p * pmax;
+        auto minp_ok = [=](float x) { return !(min_p > 0.0f) || float(double(exp_diff(x, mx)) / S) >= thr; };
+        const float y0 = mx / temperature;
+        // thread t holds sorted entries 4t..4t+3
+        const int t0 = 4 * int(threadIdx.x);
+        float xv[4];
+        double ev[4], own = 0.0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bool in = t0 + e < ng;
+            xv[e] = in ? key_f32(uint32_t(keys[t0 + e] >> 32)) : 0.0f;
+            ev[e] = in ? double(exp_diff(xv[e], mx)) : 0.0;
+            own += ev[e];
+        }
+        int64_t n = ncand;
+        if (top_p < 1.0f) {
+            // searchsorted(cumsum(p), top_p) + 1: the first position whose
+            // cumulative e reaches top_p * S
+            const double target = double(top_p) * S;
+            double run = sf_scan_f64(own, L);
+            uint64_t first = ~uint64_t(0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                run += ev[e];
+                if (t0 + e < ng && run >= target && first == ~uint64_t(0)) first = uint64_t(t0 + e);
+            }
+            first = sf_min_u64(first, L);
+            if (first != ~uint64_t(0))
+                n = int64_t(first) + 1;
+            else if (ng < ncand)
+                n = kSortMax + 1; // the cut lies beyond the gathered candidates
+        }
+        if (min_p > 0.0f) {
+            // a prefix too: p falls along the sorted order
+            int nm = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) nm += t0 + e < ng && minp_ok(xv[e]) ? 1 : 0;
+            int64_t nmt = int64_t(sf_sum_u64(uint64_t(nm), L));
+            if (nmt == ng && ng < ncand) nmt = kSortMax + 1; // min_p keeps past the gathered ones
+            n = nmt < n ? nmt : n;
+        }
+        if (n > ng) {
+            if (threadIdx.x == 0) *out_n = -1;
+            return;
+        }
+        double F = 0.0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (t0 + e < n) F += double(exp_diff(xv[e] / temperature, y0));
+        F = sf_sum_f64(F, L);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (t0 + e < n) {
+                oi[t0 + e] = int64_t(0xffffffffu - uint32_t(keys[t0 + e]));
+                op[t0 + e] = float(double(exp_diff(xv[e] / temperature, y0)) / F);
+            }
+        if (threadIdx.x == 0) *out_n = n;
+    }
+
+    // region 0 (keys[0, n0)) sorted; region 1 (keys[kSortMax, kSortMax + n1)),
+    // when two, sorted too and, unless ng < 0, its largest ng - n0 appended
+    // to region 0 (every key of region 1 lies below region 0's)
+    MG_DEV void sf_sort_regions(uint64_t *keys, int n0, int n1, int64_t ng, bool two)
+    {
+        int p0 = 1, p1 = 1;
+        while (p0 < n0) p0 <<= 1;
+        while (p1 < n1) p1 <<= 1;
+        for (int i = n0 + int(threadIdx.x); i < p0; i += kSfThreads) keys[i] = 0; // zeros sort last
+        if (two)
+            for (int i = n1 + int(threadIdx.x); i < p1; i += kSfThreads) keys[kSortMax + i] = 0;
+        __syncthreads();
+        sf_sort_desc(keys, p0);
+        if (two) {
+            sf_sort_desc(keys + kSortMax, p1);
+            if (ng >= 0) {
+                for (int i = threadIdx.x; i < int(ng) - n0; i += kSfThreads) keys[n0 + i] = keys[kSortMax + i];
+                __syncthreads();
+            }
+        }
+    }
+
+    // row `row` of lg, one work-group
+    MG_DEV void sample_row(SfLds &L, int64_t row, const float *__restrict__ lg, int64_t ld, int64_t V,
+                           const int64_t *__restrict__ raw_amax, int64_t top_k, float temperature, float top_p,
+                           float min_p, int64_t *__restrict__ out_ids, float *__restrict__ out_p,
+                           int64_t *__restrict__ out_n)
+    {
         const float *lr = lg + row * ld;
         int64_t *oi = out_ids + row * V;
         float *op = out_p + row * V;
@@ -645,12 +736,12 @@ namespace mg
             }
         });
         S = sf_sum_f64(S, L);
-        // min_p: p >= min_p * max(p), p = e / S rounded to f32
-        const float pmax = float(1.0 / S), thr = min_p * pmax;
-        auto minp_ok = [=](float x) { return !(min_p > 0.0f) || float(double(exp_diff(x, mx)) / S) >= thr; };
-        const float y0 = mx / temperature;
 
         if (!sorted) {
+            // min_p: p >= min_p * max(p), p = e / S rounded to f32
+            const float pmax = float(1.0 / S), thr = min_p * pmax;
+            auto minp_ok = [=](float x) { return !(min_p > 0.0f) || float(double(exp_diff(x, mx)) / S) >= thr; };
+            const float y0 = mx / temperature;
             // every candidate (top_k <= 0) passing min_p, in index order
             auto kept = [=](int64_t, float x) { return sf_cand(x) && minp_ok(x); };
             double F = 0.0;
@@ -669,22 +760,7 @@ namespace mg
         // the sorted outputs' keys (value desc, index asc) in LDS, sorted; the
         // first ng are the largest ng of C
         if (gather) {
-            // region 0 sorted; region 1 (the rest of the largest ng) sorted and
-            // its largest ng - n0 appended (every one of them is below region
-            // 0's keys: a lower bin)
-            const int n0 = int(L.gcount[0]), n1 = gall ? 0 : int(L.gcount[1]);
-            int p0 = 1, p1 = 1;
-            while (p0 < n0) p0 <<= 1;
-            while (p1 < n1) p1 <<= 1;
-            for (int i = n0 + int(threadIdx.x); i < p0; i += kSfThreads) L.keys[i] = 0; // zeros sort last
-            for (int i = n1 + int(threadIdx.x); i < p1; i += kSfThreads) L.keys[kSortMax + i] = 0;
-            __syncthreads();
-            sf_sort_desc(L.keys, p0);
-            if (!gall) {
-                sf_sort_desc(L.keys + kSortMax, p1);
-                for (int i = threadIdx.x; i < int(ng) - n0; i += kSfThreads) L.keys[n0 + i] = L.keys[kSortMax + i];
-                __syncthreads();
-            }
+            sf_sort_regions(L.keys, int(L.gcount[0]), gall ? 0 : int(L.gcount[1]), ng, !gall);
         } else {
             int np2 = 1;
             // the threshold bin overflows the room: the ng-th largest of C by
@@ -707,60 +783,340 @@ namespace mg
             __syncthreads();
             sf_sort_desc(L.keys, np2);
         }
-        // the cut: thread t holds sorted entries 4t..4t+3
-        const int t0 = 4 * int(threadIdx.x);
-        float xv[4];
-        double ev[4], own = 0.0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const bool in = t0 + e < ng;
-            xv[e] = in ? key_f32(uint32_t(L.keys[t0 + e] >> 32)) : 0.0f;
-            ev[e] = in ? double(exp_diff(xv[e], mx)) : 0.0;
-            own += ev[e];
-        }
-        int64_t n = ncand;
-        if (top_p < 1.0f) {
-            // searchsorted(cumsum(p), top_p) + 1: the first position whose
-            // cumulative e reaches top_p * S
-            const double target = double(top_p) * S;
-            double run = sf_scan_f64(own, L);
-            uint64_t first = ~uint64_t(0);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                run += ev[e];
-                if (t0 + e < ng && run >= target && first == ~uint64_t(0)) first = uint64_t(t0 + e);
+        sf_emit_sorted(L, L.keys, ng, ncand, S, mx, temperature, top_p, min_p, oi, op, out_n + row);
+    }
+
+    __global__ __launch_bounds__(kSfThreads) void k_sample_rows(const float *__restrict__ lg, int64_t ld, int64_t V,
+                                                               const int64_t *__restrict__ raw_amax, int64_t top_k,
+                                                               float temperature, float top_p, float min_p,
+                                                               int64_t *__restrict__ out_ids,
+                                                               float *__restrict__ out_p, int64_t *__restrict__ out_n)
+    {
+        __shared__ SfLds L;
+        sample_row(L, blockIdx.x, lg, ld, V, raw_amax, top_k, temperature, top_p, min_p, out_ids, out_p, out_n);
+    }
+
+    // ------------------------------------------------ split rows (sorted, no top_k cut)
+    // Rows with sorted outputs and every candidate in C (top_k <= 0 or >= V)
+    // split over G work-groups per row, one slice of slen entries each (64
+    // rows then fill the chip): pass 1 per slice with its prefix histogram
+    // (k_sample_split_stats), the row's decision from the slices' counts
+    // (k_sample_split_decide: the point masses, the threshold bin bstar, and
+    // where each slice's keys go), S per slice with the gathering into the
+    // row's two key regions at those offsets (k_sample_split_gather, no
+    // atomics between work-groups), the sort and cut per row
+    // (k_sample_split_finish). A row whose threshold bin holds more than
+    // kSortMax candidates is marked 2, and the finishing work-group runs the
+    // one-work-group algorithm (sample_row) on it instead.
+    constexpr int kSplitMax = 8; // work-groups per row
+
+    struct SplitStat
+    {
+        uint64_t nfin, nc, best; // best: (image with NaN on top) << 32 | ~index
+        uint32_t mk, pad;
+    };
+    struct SplitRow
+    {
+        float mx;
+        uint32_t bstar;
+        int32_t gall, pad;
+        int64_t ncand;
+        uint32_t n0, n1;               // keys in regions 0 and 1
+        uint32_t off0[kSplitMax], off1[kSplitMax];
+    };
+    struct SplitWork
+    {
+        SplitStat *stat;  // [rows][G]
+        uint32_t *hist;   // [rows][G][2^kHistBits]
+        SplitRow *prm;    // [rows]
+        int32_t *flag;    // [rows]: 0 finished, 1 split path, 2 left to k_sample_rows
+        double *spart;    // [rows][G]
+        uint64_t *keys;   // [rows][2 kSortMax]
+        int64_t slen;     // entries per slice (a multiple of 4)
+    };
+
+    struct SfHistLds : SfRed
+    {
+        uint32_t hist[(1 << kHistBits) + 1]; // the last: a spare bin for non-candidates
+    };
+    struct SfKeysLds : SfRed
+    {
+        uint64_t keys[kGatherCap];
+        uint32_t gcount[2];
+    };
+    struct SfMergeLds : SfRed
+    {
+        uint64_t keys[kGatherCap];
+        uint64_t merged[kSortMax];
+    };
+
+    __global__ __launch_bounds__(kSfThreads) void k_sample_split_stats(const float *__restrict__ lg, int64_t ld,
+                                                                      int64_t V, SplitWork w)
+    {
+        __shared__ SfHistLds L;
+        constexpr int kBins = 1 << kHistBits;
+        const int G = int(gridDim.x), g = int(blockIdx.x);
+        const int64_t row = blockIdx.y;
+        const int64_t base = int64_t(g) * w.slen;
+        const int64_t len = base < V ? (V - base < w.slen ? V - base : w.slen) : 0;
+        const float *lr = lg + row * ld + base;
+        const bool al16 = (reinterpret_cast<uintptr_t>(lr) & 15u) == 0;
+        for (int b = threadIdx.x; b < kBins; b += kSfThreads) L.hist[b] = 0;
+        __syncthreads();
+        int64_t nfin = 0, nc = 0;
+        uint32_t mk = 0, bg = 0, bi = 0xffffffffu;
+        sf_each(lr, len, al16, [&](int64_t i, float x) {
+            nfin += __builtin_isfinite(x) ? 1 : 0;
+            const bool cand = sf_cand(x);
+            const uint32_t img = sf_img(x);
+            nc += cand ? 1 : 0;
+            mk = cand && img > mk ? img : mk;
+            atomicAdd(&L.hist[cand ? img >> (32 - kHistBits) : uint32_t(kBins)], 1u);
+            const uint32_t gg = x != x ? 0xffffffffu : img;
+            if (gg > bg) {
+                bg = gg;
+                bi = uint32_t(base + i);
             }
-            first = sf_min_u64(first, L);
-            if (first != ~uint64_t(0))
-                n = int64_t(first) + 1;
-            else if (ng < ncand)
-                n = kSortMax + 1; // the cut lies beyond the gathered candidates
-        }
-        if (min_p > 0.0f) {
-            // a prefix too: p falls along the sorted order
-            int nm = 0;
+        });
+        nfin = int64_t(sf_sum_u64(uint64_t(nfin), L));
+        nc = int64_t(sf_sum_u64(uint64_t(nc), L));
+        const uint64_t best = sf_max_u64((uint64_t(bg) << 32) | uint64_t(0xffffffffu - bi), L);
+        mk = uint32_t(sf_max_u64(mk, L));
+        const int64_t sl = row * G + g;
+        if (threadIdx.x == 0) w.stat[sl] = SplitStat{uint64_t(nfin), uint64_t(nc), best, mk, 0u};
+        uint32_t *h = w.hist + sl * kBins;
+        for (int b = threadIdx.x; b < kBins; b += kSfThreads) h[b] = L.hist[b];
+    }
+
+    __global__ __launch_bounds__(kSfThreads) void k_sample_split_decide(int64_t V, const int64_t *__restrict__ raw_amax,
+                                                                       int G, float temperature,
+                                                                       int64_t *__restrict__ out_ids,
+                                                                       float *__restrict__ out_p,
+                                                                       int64_t *__restrict__ out_n, SplitWork w)
+    {
+        __shared__ SfRed L;
+        constexpr int kBins = 1 << kHistBits;
+        const int64_t row = blockIdx.x;
+        // the slices' counts, folded in slice order by every thread alike
+        int64_t nfin = 0, nc = 0;
+        uint64_t best = 0;
+        uint32_t mk = 0;
+        int64_t ncs[kSplitMax];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) nm += t0 + e < ng && minp_ok(xv[e]) ? 1 : 0;
-            int64_t nmt = int64_t(sf_sum_u64(uint64_t(nm), L));
-            if (nmt == ng && ng < ncand) nmt = kSortMax + 1; // min_p keeps past the gathered ones
-            n = nmt < n ? nmt : n;
+        for (int g = 0; g < kSplitMax; ++g) {
+            const SplitStat t = w.stat[row * G + (g < G ? g : G - 1)];
+            const bool live = g < G;
+            nfin += live ? int64_t(t.nfin) : 0;
+            nc += live ? int64_t(t.nc) : 0;
+            ncs[g] = live ? int64_t(t.nc) : 0;
+            best = live && t.best > best ? t.best : best;
+            mk = live && t.mk > mk ? t.mk : mk;
         }
-        if (n > ng) {
-            if (threadIdx.x == 0) out_n[row] = -1;
+        int64_t *oi = out_ids + row * V;
+        float *op = out_p + row * V;
+        if (nfin == 0 || !(temperature > 0.0f)) {
+            if (threadIdx.x == 0) {
+                oi[0] = nfin == 0 && raw_amax ? raw_amax[row] : int64_t(0xffffffffu - uint32_t(best));
+                op[0] = 1.0f;
+                out_n[row] = 1;
+                w.flag[row] = 0;
+            }
             return;
         }
-        double F = 0.0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (t0 + e < n) F += double(exp_diff(xv[e] / temperature, y0));
-        F = sf_sum_f64(F, L);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (t0 + e < n) {
-                oi[t0 + e] = int64_t(0xffffffffu - uint32_t(L.keys[t0 + e]));
-                op[t0 + e] = float(double(exp_diff(xv[e] / temperature, y0)) / F);
+        const float mx = key_f32(mk);
+        if (!(mx < __builtin_huge_valf())) { // +inf among the candidates
+            if (threadIdx.x == 0) {
+                out_n[row] = -1;
+                w.flag[row] = 0;
             }
-        if (threadIdx.x == 0) out_n[row] = n;
+            return;
+        }
+        const int64_t ng = nc < kSortMax ? nc : kSortMax;
+        const bool gall = ng == nc;
+        SplitRow r{};
+        r.mx = mx;
+        r.gall = gall ? 1 : 0;
+        r.ncand = nc;
+        if (gall) {
+            // every candidate into region 0, slice by slice
+            uint32_t acc = 0;
+#pragma unroll
+            for (int g = 0; g < kSplitMax; ++g) {
+                r.off0[g] = acc;
+                acc += uint32_t(ncs[g]);
+            }
+            r.n0 = acc;
+        } else {
+            // thread t holds bins kBins-1-BPT*t-e of every slice (all requested
+            // at once: slices past G re-read the last and count nothing)
+            constexpr int BPT = kBins / kSfThreads;
+            const uint32_t *h = w.hist + row * G * kBins;
+            uint32_t hv[kSplitMax][BPT];
+#pragma unroll
+            for (int g = 0; g < kSplitMax; ++g)
+#pragma unroll
+                for (int e = 0; e < BPT; ++e)
+                    hv[g][e] = h[(g < G ? g : G - 1) * kBins + kBins - 1 - BPT * int(threadIdx.x) - e];
+            uint32_t c[BPT];
+            int own = 0;
+#pragma unroll
+            for (int e = 0; e < BPT; ++e) {
+                c[e] = 0;
+#pragma unroll
+                for (int g = 0; g < kSplitMax; ++g) c[e] += g < G ? hv[g][e] : 0u;
+                own += int(c[e]);
+            }
+            int tot;
+            int64_t acc = sf_scan(own, L, &tot);
+#pragma unroll
+            for (int e = 0; e < BPT; ++e) {
+                if (acc < ng && acc + c[e] >= ng) {
+                    L.bc[0] = uint32_t(kBins - 1 - BPT * int(threadIdx.x) - e);
+                    L.bc[1] = c[e];
+                }
+                acc += c[e];
+            }
+            __syncthreads();
+            const uint32_t bstar = L.bc[0], inb = L.bc[1];
+            __syncthreads();
+            if (inb > uint32_t(kSortMax)) {
+                if (threadIdx.x == 0) w.flag[row] = 2;
+                return;
+            }
+            // each slice's keys above bstar and in it, in slice order
+            uint32_t a0 = 0, a1 = 0;
+#pragma unroll
+            for (int g = 0; g < kSplitMax; ++g) {
+                if (g < G) {
+                    int above = 0;
+#pragma unroll
+                    for (int e = 0; e < BPT; ++e)
+                        above += uint32_t(kBins - 1 - BPT * int(threadIdx.x) - e) > bstar ? int(hv[g][e]) : 0;
+                    const uint32_t na = uint32_t(sf_sum_u64(uint64_t(above), L));
+                    const uint32_t nb = h[g * kBins + bstar];
+                    r.off0[g] = a0;
+                    r.off1[g] = a1;
+                    a0 += na;
+                    a1 += nb;
+                }
+            }
+            r.bstar = bstar;
+            r.n0 = a0;
+            r.n1 = a1;
+        }
+        if (threadIdx.x == 0) {
+            w.prm[row] = r;
+            w.flag[row] = 1;
+        }
+    }
+
+    // S over the slice and its gathered keys, sorted in LDS, written as the
+    // slice's runs of the row's two regions
+    __global__ __launch_bounds__(kSfThreads) void k_sample_split_gather(const float *__restrict__ lg, int64_t ld,
+                                                                       int64_t V, SplitWork w)
+    {
+        __shared__ SfKeysLds L;
+        const int G = int(gridDim.x), g = int(blockIdx.x);
+        const int64_t row = blockIdx.y;
+        if (w.flag[row] != 1) return;
+        const SplitRow &r = w.prm[row]; // read in place (uniform loads)
+        const int64_t base = int64_t(g) * w.slen;
+        const int64_t len = base < V ? (V - base < w.slen ? V - base : w.slen) : 0;
+        const float *lr = lg + row * ld + base;
+        const bool al16 = (reinterpret_cast<uintptr_t>(lr) & 15u) == 0;
+        if (threadIdx.x < 2) L.gcount[threadIdx.x] = 0;
+        __syncthreads();
+        const bool gall = r.gall != 0;
+        const float mx = r.mx;
+        const uint32_t bstar = r.bstar;
+        double S = 0.0;
+        sf_each(lr, len, al16, [&](int64_t i, float x) {
+            if (!sf_cand(x)) return;
+            S += double(exp_diff(x, mx));
+            const uint32_t img = sf_img(x), bin = img >> (32 - kHistBits);
+            if (gall || bin >= bstar) {
+                const int reg = gall || bin > bstar ? 0 : 1;
+                const uint32_t at = atomicAdd(&L.gcount[reg], 1u);
+                L.keys[reg * kSortMax + int(at)] = (uint64_t(img) << 32) | uint64_t(0xffffffffu - uint32_t(base + i));
+            }
+        });
+        S = sf_sum_f64(S, L); // (its barriers also publish the gathered keys)
+        if (threadIdx.x == 0) w.spart[row * G + g] = S;
+        const int n0 = int(L.gcount[0]), n1 = gall ? 0 : int(L.gcount[1]);
+        sf_sort_regions(L.keys, n0, n1, -1, !gall);
+        uint64_t *k0 = w.keys + row * (2 * kSortMax) + r.off0[g];
+        uint64_t *k1 = w.keys + row * (2 * kSortMax) + kSortMax + r.off1[g];
+        for (int i = threadIdx.x; i < n0; i += kSfThreads) k0[i] = L.keys[i];
+        for (int i = threadIdx.x; i < n1; i += kSfThreads) k1[i] = L.keys[kSortMax + i];
+    }
+
+    // keys[0, n) as G descending runs (run q from off[q] to off[q+1], off[G]
+    // = n): every key to its place in their merged order, when below lim
+    // (its place is its index in its run plus, in every other run, the number
+    // of larger keys: the keys are unique)
+    MG_DEV void sf_merge_runs(const uint64_t *keys, int n, const uint32_t *off, int G, int lim, uint64_t *dst,
+                              int at)
+    {
+        for (int i = threadIdx.x; i < n; i += kSfThreads) {
+            const uint64_t k = keys[i];
+            int pos = 0;
+            for (int q = 0; q < G; ++q) {
+                const int lo = int(off[q]), hi = q + 1 < G ? int(off[q + 1]) : n;
+                if (i >= lo && i < hi) {
+                    pos += i - lo;
+                    continue;
+                }
+                // larger keys of run q: a prefix, found by bisection
+                int a = lo, b = hi;
+                while (a < b) {
+                    const int m = (a + b) >> 1;
+                    if (keys[m] > k)
+                        a = m + 1;
+                    else
+                        b = m;
+                }
+                pos += a - lo;
+            }
+            if (pos < lim) dst[at + pos] = k;
+        }
+    }
+
+    __global__ __launch_bounds__(kSfThreads) void k_sample_split_finish(const float *__restrict__ lg, int64_t ld,
+                                                                       int64_t V, const int64_t *__restrict__ raw_amax,
+                                                                       int64_t top_k, int G, float temperature,
+                                                                       float top_p, float min_p,
+                                                                       int64_t *__restrict__ out_ids,
+                                                                       float *__restrict__ out_p,
+                                                                       int64_t *__restrict__ out_n, SplitWork w)
+    {
+        __shared__ union
+        {
+            SfMergeLds m;
+            SfLds full;
+        } U;
+        const int64_t row = blockIdx.x;
+        const int32_t flag = w.flag[row];
+        if (flag == 2) {
+            sample_row(U.full, row, lg, ld, V, raw_amax, top_k, temperature, top_p, min_p, out_ids, out_p, out_n);
+            return;
+        }
+        if (flag != 1) return;
+        SfMergeLds &L = U.m;
+        const SplitRow &r = w.prm[row]; // read in place (uniform loads)
+        double S = 0.0;
+        for (int g = 0; g < G; ++g) S += w.spart[row * G + g];
+        const int64_t ng = r.ncand < kSortMax ? r.ncand : kSortMax;
+        const int n0 = int(r.n0), n1 = r.gall ? 0 : int(r.n1);
+        const uint64_t *src = w.keys + row * (2 * kSortMax);
+        for (int i = threadIdx.x; i < n0; i += kSfThreads) L.keys[i] = src[i];
+        for (int i = threadIdx.x; i < n1; i += kSfThreads) L.keys[kSortMax + i] = src[kSortMax + i];
+        __syncthreads();
+        // region 0's runs merged in full, region 1's largest ng - n0 after them
+        sf_merge_runs(L.keys, n0, r.off0, G, n0, L.merged, 0);
+        if (n1 > 0) sf_merge_runs(L.keys + kSortMax, n1, r.off1, G, int(ng) - n0, L.merged, n0);
+        __syncthreads();
+        sf_emit_sorted(L, L.merged, ng, r.ncand, S, r.mx, temperature, top_p, min_p, out_ids + row * V,
+                       out_p + row * V, out_n + row);
     }
 
     void launch_sample_rows(mg_ctx *c, const float *lg, int64_t ld, int64_t rows, int64_t V,
@@ -773,8 +1129,43 @@ namespace mg
         if (ld == 0) ld = V;
         need(ld >= V, "sample_rows: row stride < V");
         if (rows == 0) return;
-        hipLaunchKernelGGL(k_sample_rows, dim3(unsigned(rows)), dim3(kSfThreads), 0, c->stream, lg, ld, V, raw_amax,
-                           top_k, float(temperature), float(top_p), float(min_p), out_ids, out_p, out_n);
-        check_launch("k_sample_rows");
+        const float T = float(temperature), tp = float(top_p), mp = float(min_p);
+        // the split path: sorted outputs with no top_k cut, few enough rows that
+        // G >= 2 work-groups per row fill the chip, and room in the workspace
+        const bool sorted = top_k > 0 || tp < 1.0f;
+        const int G = int(rows <= 256 / kSplitMax ? kSplitMax : 256 / rows);
+        constexpr int64_t kBins = int64_t(1) << kHistBits;
+        auto al = [](int64_t b) { return (b + 255) / 256 * 256; };
+        const int64_t b_stat = al(rows * G * int64_t(sizeof(SplitStat))), b_hist = al(rows * G * kBins * 4),
+                      b_prm = al(rows * int64_t(sizeof(SplitRow))), b_flag = al(rows * 4), b_sp = al(rows * G * 8),
+                      b_keys = al(rows * 2 * kSortMax * 8);
+        const bool split = sorted && (top_k <= 0 || top_k >= V) && G >= 2 && V >= 4 * 4096 &&
+                           b_stat + b_hist + b_prm + b_flag + b_sp + b_keys <= c->work_bytes;
+        if (!split) {
+            hipLaunchKernelGGL(k_sample_rows, dim3(unsigned(rows)), dim3(kSfThreads), 0, c->stream, lg, ld, V,
+                               raw_amax, top_k, T, tp, mp, out_ids, out_p, out_n);
+            check_launch("k_sample_rows");
+            return;
+        }
+        char *wb = static_cast<char *>(c->work);
+        SplitWork w;
+        w.stat = reinterpret_cast<SplitStat *>(wb);
+        w.hist = reinterpret_cast<uint32_t *>(wb + b_stat);
+        w.prm = reinterpret_cast<SplitRow *>(wb + b_stat + b_hist);
+        w.flag = reinterpret_cast<int32_t *>(wb + b_stat + b_hist + b_prm);
+        w.spart = reinterpret_cast<double *>(wb + b_stat + b_hist + b_prm + b_flag);
+        w.keys = reinterpret_cast<uint64_t *>(wb + b_stat + b_hist + b_prm + b_flag + b_sp);
+        w.slen = (V + 4 * G - 1) / (4 * G) * 4;
+        const dim3 gs{unsigned(G), unsigned(rows), 1u};
+        hipLaunchKernelGGL(k_sample_split_stats, gs, dim3(kSfThreads), 0, c->stream, lg, ld, V, w);
+        check_launch("k_sample_split_stats");
+        hipLaunchKernelGGL(k_sample_split_decide, dim3(unsigned(rows)), dim3(kSfThreads), 0, c->stream, V, raw_amax, G,
+                           T, out_ids, out_p, out_n, w);
+        check_launch("k_sample_split_decide");
+        hipLaunchKernelGGL(k_sample_split_gather, gs, dim3(kSfThreads), 0, c->stream, lg, ld, V, w);
+        check_launch("k_sample_split_gather");
+        hipLaunchKernelGGL(k_sample_split_finish, dim3(unsigned(rows)), dim3(kSfThreads), 0, c->stream, lg, ld, V,
+                           raw_amax, top_k, G, T, tp, mp, out_ids, out_p, out_n, w);
+        check_launch("k_sample_split_finish");
     }
 } // namespace mg

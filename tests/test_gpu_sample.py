@@ -230,6 +230,41 @@ def test_sample_rows_threshold_bin_on_top(prims):
     assert np.abs(probs.cpu().numpy()[0, :len(wi)].astype(np.float64) - wp).max() <= 2e-6
 
 
+@pytest.mark.parametrize("temp", (1.0, 0.0))
+def test_sample_rows_split_rows(prims, temp):
+    """rows of V >= 16384 with sorted outputs and no top_k cut run split over
+    several work-groups per row: a fully masked row (the raw argmax), NaN and
+    -inf entries, a row whose maximum sits in the last slice, and greedy rows
+    (temperature 0: np.argmax, NaN counting as the largest) beside sampled ones"""
+    import torch
+    rows, V = 5, 30000
+    L = O.normal(57, (rows, V), 0.0, 3.0, F32).view(np.float32).copy()
+    L[0] = -np.inf
+    L[1, ::7] = np.nan
+    L[2, ::3] = -np.inf
+    L[3, V - 1] = 40.0
+    L[4, 12345] = np.nan
+    raw = np.array([17, 0, 0, 0, 0], np.int64)
+    for r in range(rows):
+        f = np.isfinite(L[r])
+        if f.any():
+            x = np.sort(L[r][f])[::-1]
+            e32 = np.exp(x - x[0])
+            p64 = softmax(x.astype(np.float64))
+            c32 = np.searchsorted(np.cumsum(e32 / e32.sum()), np.float32(0.9)) + 1
+            c64 = np.searchsorted(np.cumsum(p64), np.float64(np.float32(0.9))) + 1
+            assert c32 == c64, (r, c32, c64)
+    want = O.sample_rows(L, raw, 0, temp, 0.9, 0.0)
+    ids, probs, n = prims.sample_rows(torch.from_numpy(L).cuda(), 0, temp, 0.9, 0.0,
+                                      raw_argmax=torch.from_numpy(raw).cuda())
+    ids, probs, n = ids.cpu().numpy(), probs.cpu().numpy(), n.cpu().numpy()
+    for r in range(rows):
+        wi, wp = want[r]
+        assert n[r] == len(wi), (r, n[r], len(wi))
+        assert np.array_equal(ids[r, :n[r]], wi), r
+        assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, r
+
+
 def test_sample_rows_left_to_host(prims):
     """count -1: a nucleus of more than 4096 sorted candidates (flat logits), and a
     row holding +inf (the reference's probabilities are NaN there); other rows of
