@@ -116,7 +116,7 @@ KERNEL_OF = {
     "attn_prefill_4096": "k_attn_prefill<5,4,1,4>",
     "softmax_causal_softcap30": "k_softmax_fast<cap>",
     "norm_rows_f32_embed": "k_norm_f32rows",
-    "sample_rows_topk0": "k_sample_rows",
+    "sample_rows_topk0": "k_sample_split_stats + decide + gather + finish",
     "copy_256MiB": "torch copy (memory-only probe)",
     "launch_floor": "torch fill of one float (timing-protocol probe)",
     "probe_copy_256MiB": "k_probe<0> (copy)",
