@@ -265,6 +265,31 @@ def test_sample_rows_split_rows(prims, temp):
         assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, r
 
 
+@pytest.mark.parametrize("V,ld", ((30001, 30001), (40000, 40003), (50000, 50000)))
+def test_sample_rows_split_unaligned(prims, V, ld):
+    """the split path on rows whose slices start off 16-byte boundaries (odd V or
+    row stride: entry-by-entry loads there), and on aligned rows of three rows"""
+    import torch
+    rows = 3
+    wide = O.normal(58, (rows, ld), 0.0, 3.0, F32).view(np.float32).copy()
+    L = wide[:, :V]
+    for r in range(rows):
+        x = np.sort(L[r])[::-1]
+        e32 = np.exp(x - x[0])
+        p64 = softmax(x.astype(np.float64))
+        c32 = np.searchsorted(np.cumsum(e32 / e32.sum()), np.float32(0.9)) + 1
+        c64 = np.searchsorted(np.cumsum(p64), np.float64(np.float32(0.9))) + 1
+        assert c32 == c64, (r, c32, c64)
+    want = O.sample_rows(np.ascontiguousarray(L), np.argmax(L, axis=1), 0, 1.0, 0.9, 0.0)
+    ids, probs, n = prims.sample_rows(torch.from_numpy(wide).cuda()[:, :V], 0, 1.0, 0.9, 0.0)
+    ids, probs, n = ids.cpu().numpy(), probs.cpu().numpy(), n.cpu().numpy()
+    for r in range(rows):
+        wi, wp = want[r]
+        assert n[r] == len(wi), (r, n[r], len(wi))
+        assert np.array_equal(ids[r, :n[r]], wi), r
+        assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, r
+
+
 def test_sample_rows_left_to_host(prims):
     """count -1: a nucleus of more than 4096 sorted candidates (flat logits), and a
     row holding +inf (the reference's probabilities are NaN there); other rows of
