@@ -290,6 +290,34 @@ def test_sample_rows_split_unaligned(prims, V, ld):
         assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, r
 
 
+@pytest.mark.parametrize("rows", (64, 100))
+def test_sample_rows_split_fewer_slices(prims, rows):
+    """64 rows split over 4 work-groups each (the bench's shape at a smaller V),
+    100 rows over 2"""
+    import torch
+    V = 20000
+    L = O.normal(59, (rows, V), 0.0, 3.0, F32).view(np.float32).copy()
+    keep = []
+    for r in range(rows):
+        x = np.sort(L[r])[::-1]
+        e32 = np.exp(x - x[0])
+        p64 = softmax(x.astype(np.float64))
+        c32 = np.searchsorted(np.cumsum(e32 / e32.sum()), np.float32(0.9)) + 1
+        c64 = np.searchsorted(np.cumsum(p64), np.float64(np.float32(0.9))) + 1
+        keep.append(c32 == c64)   # rows whose cut the two precisions place alike
+    assert sum(keep) >= rows - 2
+    want = O.sample_rows(L, np.argmax(L, axis=1), 0, 1.0, 0.9, 0.0)
+    ids, probs, n = prims.sample_rows(torch.from_numpy(L).cuda(), 0, 1.0, 0.9, 0.0)
+    ids, probs, n = ids.cpu().numpy(), probs.cpu().numpy(), n.cpu().numpy()
+    for r in range(rows):
+        if not keep[r]:
+            continue
+        wi, wp = want[r]
+        assert n[r] == len(wi), (r, n[r], len(wi))
+        assert np.array_equal(ids[r, :n[r]], wi), r
+        assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, r
+
+
 def test_sample_rows_left_to_host(prims):
     """count -1: a nucleus of more than 4096 sorted candidates (flat logits), and a
     row holding +inf (the reference's probabilities are NaN there); other rows of
