@@ -106,7 +106,7 @@ KERNEL_OF = {
     "softmax_causal": "k_softmax_fast<mg::SBf16,4,false,true>",
     "rope": "k_rope",
     "softmax_decode": "k_softmax_partial_buf + k_softmax_finish_buf",
-    "dequant_q8_0": "k_dequant_q8_0",
+    "dequant_q8_0": "k_dequant_q8_0_wide<mg::SBf16>",
     "vocab_lse_argmax_top64": "k_vocab_chunk + k_vocab_merge",
     "qk_norm_rope_kv": "k_qk_pairs",
     "quantize_q8_0": "k_quantize_q8_0",

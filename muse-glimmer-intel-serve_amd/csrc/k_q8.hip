@@ -73,6 +73,53 @@ namespace mg
         }
     }
 
+    // 16-bit outputs over whole 1 KiB chunks of quants, one chunk a wave: lane L
+    // loads quants 16L..16L+15 (one 16-byte load, so each load instruction
+    // reads 1 KiB where the 8-quant lanes above read 512 B), then takes the 8
+    // quants of outputs 8L.. and 512 + 8L.. from lanes L/2 and 32 + L/2
+    // (ds_bpermute, no LDS storage), so each of the two 16-byte stores still
+    // writes 1 KiB contiguously. The scale of outputs 8L.. is block L/4 of the
+    // chunk's 32, that of 512 + 8L.. block 16 + L/4: loaded by the lane itself.
+    template <class SO>
+    __global__ __launch_bounds__(64) void k_dequant_q8_0_wide(const int8_t *__restrict__ qs,
+                                                               const uint16_t *__restrict__ d,
+                                                               uint16_t *__restrict__ out)
+    {
+        const int lane = threadIdx.x;
+        const int64_t ch = blockIdx.x;
+        const Vec<uint32_t, 4> qv = ld16_stream<uint32_t, 4>(reinterpret_cast<const uint32_t *>(qs + 1024 * ch + 16 * lane));
+        const float sa = f16_f32(d[ch * 32 + (lane >> 2)]);
+        const float sb = f16_f32(d[ch * 32 + 16 + (lane >> 2)]);
+        // source lanes' words j, then the half (h) this lane's outputs take
+        const int h = lane & 1, srcA = (lane >> 1) * 4, srcB = (32 + (lane >> 1)) * 4;
+        uint32_t wa[4], wb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            wa[j] = uint32_t(__builtin_amdgcn_ds_bpermute(srcA, int(qv.v[j])));
+            wb[j] = uint32_t(__builtin_amdgcn_ds_bpermute(srcB, int(qv.v[j])));
+        }
+        const Vec<int8_t, 8> qa = __builtin_bit_cast(Vec<int8_t, 8>, Vec<uint32_t, 2>{{h ? wa[2] : wa[0], h ? wa[3] : wa[1]}});
+        const Vec<int8_t, 8> qb = __builtin_bit_cast(Vec<int8_t, 8>, Vec<uint32_t, 2>{{h ? wb[2] : wb[0], h ? wb[3] : wb[1]}});
+        Vec<uint16_t, 8> oa, ob;
+        if (__builtin_isfinite(sa) && __builtin_isfinite(sb)) {
+            // int8 x finite scale: finite products, no NaN to canonicalize
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                oa.v[e] = SO::enc_finite(float(qa.v[e]) * sa);
+                ob.v[e] = SO::enc_finite(float(qb.v[e]) * sb);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                oa.v[e] = SO::enc32(float(qa.v[e]) * sa);
+                ob.v[e] = SO::enc32(float(qb.v[e]) * sb);
+            }
+        }
+        uint16_t *o = out + 1024 * ch;
+        st16_stream<uint16_t, 8>(o + 8 * lane, oa);
+        st16_stream<uint16_t, 8>(o + 512 + 8 * lane, ob);
+    }
+
     // ------------------------------------------------------------ quantizer
     // up_w (src/gpu/gpu_engine.cpp:2722-2755), the llama.cpp quantize_row_q8_0
     // rule: per 32-block, amax = max |x| over the bf16 values, d = amax / 127
@@ -274,6 +321,16 @@ namespace mg
         const int64_t nspans = n / Q, blocks = (nspans + 64 * kDequantSpans - 1) / (64 * kDequantSpans);
         need(blocks < (int64_t(1) << 31), "dequant_q8_0: tensor too large");
         const dim3 g{unsigned(blocks), 1u, 1u};
+        if ((dt_out == BF16 || dt_out == F16) && n % 1024 == 0 && n / 1024 < (int64_t(1) << 31)) {
+            const dim3 gw{unsigned(n / 1024), 1u, 1u};
+            uint16_t *o = static_cast<uint16_t *>(out);
+            if (dt_out == BF16)
+                hipLaunchKernelGGL(k_dequant_q8_0_wide<SBf16>, gw, dim3(64), 0, c->stream, qs, d, o);
+            else
+                hipLaunchKernelGGL(k_dequant_q8_0_wide<SF16>, gw, dim3(64), 0, c->stream, qs, d, o);
+            check_launch("k_dequant_q8_0_wide");
+            return;
+        }
         switch (dt_out) {
         case BF16: hipLaunchKernelGGL(k_dequant_q8_0<SBf16>, g, dim3(64), 0, c->stream, qs, d, static_cast<uint16_t *>(out), nspans); break;
         case F16: hipLaunchKernelGGL(k_dequant_q8_0<SF16>, g, dim3(64), 0, c->stream, qs, d, static_cast<uint16_t *>(out), nspans); break;

@@ -50,6 +50,34 @@ def test_dequant_subnormal_and_special_scales(prims):
     assert np.array_equal(qf.astype(np.float64), qs.astype(np.float64) * np.repeat(O.to_f64(d, F16), 32, axis=1))
 
 
+@pytest.mark.parametrize("dt_out", (BF16, F16))
+def test_dequant_nonfinite_scales_and_short_tensors(prims, dt_out):
+    """inf, -inf and NaN scales through the kernel for whole 1024-quant chunks
+    (bf16: every NaN is 0x7FC0, so 0 x inf is checked too; f16 keeps a NaN's
+    sign, which 0 x inf leaves to the hardware, so there only nonzero quants meet
+    the infinite scales), and tensors of other sizes (5 x 96 and 3 x 32 quants)
+    through the 8-quant-lane kernel"""
+    import torch
+    qs, d = q8_case(64, 2048, seed=31)
+    qs = qs.copy()
+    d = d.copy()
+    if dt_out == BF16:
+        qs[0, :32] = 0  # block 0 of row 0: 0 x inf = NaN throughout
+        d[2, 5] = 0x7E00  # NaN
+    else:
+        qs[0, :32] = np.where(qs[0, :32] == 0, 1, qs[0, :32])
+        qs[1, 96:128] = np.where(qs[1, 96:128] == 0, 1, qs[1, 96:128])
+        qs[3, 2016:] = np.where(qs[3, 2016:] == 0, 1, qs[3, 2016:])
+    d[0, 0] = 0x7C00   # +inf
+    d[1, 3] = 0xFC00   # -inf
+    d[3, 63] = 0x7C00
+    for q, dd in ((qs, d), q8_case(5, 96, seed=32), q8_case(3, 32, seed=33)):
+        out = to_dev(np.zeros(q.shape, np.uint16), dt_out)
+        prims.dequant_q8_0(torch.from_numpy(q).to("cuda:0"), torch.from_numpy(dd.view(np.int16)).to("cuda:0"), out)
+        ref = O.dequant_q8_0(q, dd, dt_out)
+        assert same_bits(from_dev(out, dt_out), O.from_f64(ref, dt_out))
+
+
 def test_dequant_config5_full(prims):
     """Config 5 at full size: [25600 x 5120] int8 ~ U[-127,127], f16 scales ~ U[1e-3, 2e-2]."""
     import torch
