@@ -608,11 +608,13 @@ namespace mg
         }
     }
 
-    // row `row` of lg, one work-group
+    // row `row` of lg, one work-group; S_given >= 0 is C's e sum as another
+    // path summed it (then used in place of this one's, so a row gets the same
+    // bits whichever path finishes it)
     MG_DEV void sample_row(SfLds &L, int64_t row, const float *__restrict__ lg, int64_t ld, int64_t V,
                            const int64_t *__restrict__ raw_amax, int64_t top_k, float temperature, float top_p,
                            float min_p, int64_t *__restrict__ out_ids, float *__restrict__ out_p,
-                           int64_t *__restrict__ out_n)
+                           int64_t *__restrict__ out_n, double S_given = -1.0)
     {
         const float *lr = lg + row * ld;
         int64_t *oi = out_ids + row * V;
@@ -723,19 +725,22 @@ namespace mg
         // 0 (keys[0, kSortMax)) the entries above bstar, or all of C; region
         // 1 (keys[kSortMax, 2 kSortMax)) those in bstar
         double S = 0.0;
-        sf_each(lr, V, al16, [&](int64_t i, float x) {
-            const bool in = inC(i, x);
-            if (in) S += double(exp_diff(x, mx));
-            if (gather) {
-                const uint32_t img = sf_img(x), bin = img >> (32 - kHistBits);
-                if (in && (gall || bin >= bstar)) {
-                    const int reg = gall || bin > bstar ? 0 : 1;
-                    const uint32_t at = atomicAdd(&L.gcount[reg], 1u);
-                    L.keys[reg * kSortMax + int(at)] = (uint64_t(img) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+        if (gather || !(S_given >= 0.0)) {
+            sf_each(lr, V, al16, [&](int64_t i, float x) {
+                const bool in = inC(i, x);
+                if (in) S += double(exp_diff(x, mx));
+                if (gather) {
+                    const uint32_t img = sf_img(x), bin = img >> (32 - kHistBits);
+                    if (in && (gall || bin >= bstar)) {
+                        const int reg = gall || bin > bstar ? 0 : 1;
+                        const uint32_t at = atomicAdd(&L.gcount[reg], 1u);
+                        L.keys[reg * kSortMax + int(at)] = (uint64_t(img) << 32) | uint64_t(0xffffffffu - uint32_t(i));
+                    }
                 }
-            }
-        });
-        S = sf_sum_f64(S, L);
+            });
+            S = sf_sum_f64(S, L);
+        }
+        if (S_given >= 0.0) S = S_given;
 
         if (!sorted) {
             // min_p: p >= min_p * max(p), p = e / S rounded to f32
@@ -807,7 +812,8 @@ namespace mg
     // atomics between work-groups), the sort and cut per row
     // (k_sample_split_finish). A row whose threshold bin holds more than
     // kSortMax candidates is marked 2, and the finishing work-group runs the
-    // one-work-group algorithm (sample_row) on it instead.
+    // one-work-group algorithm (sample_row) on it instead, with the S the
+    // slices summed: the same selection and the same bits as the split path's.
     constexpr int kSplitMax = 8; // work-groups per row
 
     struct SplitStat
@@ -980,7 +986,12 @@ namespace mg
             const uint32_t bstar = L.bc[0], inb = L.bc[1];
             __syncthreads();
             if (inb > uint32_t(kSortMax)) {
-                if (threadIdx.x == 0) w.flag[row] = 2;
+                // left to the one-work-group algorithm; the gathering kernel
+                // still sums S by slices (mx)
+                if (threadIdx.x == 0) {
+                    w.prm[row] = r;
+                    w.flag[row] = 2;
+                }
                 return;
             }
             // each slice's keys above bstar and in it, in slice order
@@ -1018,7 +1029,8 @@ namespace mg
         __shared__ SfKeysLds L;
         const int G = int(gridDim.x), g = int(blockIdx.x);
         const int64_t row = blockIdx.y;
-        if (w.flag[row] != 1) return;
+        const int32_t flag = w.flag[row];
+        if (flag != 1 && flag != 2) return;
         const SplitRow &r = w.prm[row]; // read in place (uniform loads)
         const int64_t base = int64_t(g) * w.slen;
         const int64_t len = base < V ? (V - base < w.slen ? V - base : w.slen) : 0;
@@ -1026,7 +1038,7 @@ namespace mg
         const bool al16 = (reinterpret_cast<uintptr_t>(lr) & 15u) == 0;
         if (threadIdx.x < 2) L.gcount[threadIdx.x] = 0;
         __syncthreads();
-        const bool gall = r.gall != 0;
+        const bool gall = r.gall != 0, gather = flag == 1;
         const float mx = r.mx;
         const uint32_t bstar = r.bstar;
         double S = 0.0;
@@ -1034,7 +1046,7 @@ namespace mg
             if (!sf_cand(x)) return;
             S += double(exp_diff(x, mx));
             const uint32_t img = sf_img(x), bin = img >> (32 - kHistBits);
-            if (gall || bin >= bstar) {
+            if (gather && (gall || bin >= bstar)) {
                 const int reg = gall || bin > bstar ? 0 : 1;
                 const uint32_t at = atomicAdd(&L.gcount[reg], 1u);
                 L.keys[reg * kSortMax + int(at)] = (uint64_t(img) << 32) | uint64_t(0xffffffffu - uint32_t(base + i));
@@ -1042,6 +1054,7 @@ namespace mg
         });
         S = sf_sum_f64(S, L); // (its barriers also publish the gathered keys)
         if (threadIdx.x == 0) w.spart[row * G + g] = S;
+        if (!gather) return;
         const int n0 = int(L.gcount[0]), n1 = gall ? 0 : int(L.gcount[1]);
         sf_sort_regions(L.keys, n0, n1, -1, !gall);
         uint64_t *k0 = w.keys + row * (2 * kSortMax) + r.off0[g];
@@ -1097,7 +1110,9 @@ namespace mg
         const int64_t row = blockIdx.x;
         const int32_t flag = w.flag[row];
         if (flag == 2) {
-            sample_row(U.full, row, lg, ld, V, raw_amax, top_k, temperature, top_p, min_p, out_ids, out_p, out_n);
+            double S = 0.0;
+            for (int g = 0; g < G; ++g) S += w.spart[row * G + g];
+            sample_row(U.full, row, lg, ld, V, raw_amax, top_k, temperature, top_p, min_p, out_ids, out_p, out_n, S);
             return;
         }
         if (flag != 1) return;
