@@ -332,9 +332,11 @@ int mg_sample_dist(mg_ctx *ctx, const int64_t *top_idx, const float *top_val, co
  * <= 0 every value > -inf. Candidates come out in value order (ties by
  * index) when top_k > 0 or top_p < 1, as the reference sorts them, else in
  * index order. cand_ids/cand_probs are [rows, V]; cand_count[r] is the
- * number written, or -1 for a row left to the host: one whose sorted
- * candidates exceed 4096, or one holding +inf (the reference's probabilities
- * are NaN there and its draw raises). */
+ * number written, or -1 for a row left to the host: one whose kept prefix in
+ * value order (after the top_p and min_p cuts) exceeds 4096 candidates, or one
+ * holding +inf (the reference's probabilities are NaN there and its draw
+ * raises). Rows with value-order outputs and no top_k cut use the context's
+ * workspace for per-slice counts and gathered keys when they fit it. */
 int mg_sample_rows(mg_ctx *ctx, const float *logits, int64_t ld, int64_t rows, int64_t V, const int64_t *raw_argmax,
                    int64_t top_k, double temperature, double top_p, double min_p, int64_t *cand_ids,
                    float *cand_probs, int64_t *cand_count);
