@@ -150,7 +150,8 @@ namespace mg
     // ------------------------------------------------------------------
     // The whole filter chain on full logit rows, for any top_k
     // (serve/sampler.py:43-112, Sampler._transformed after the logit edits):
-    // one 1024-thread work-group per row of lg (f32, the edited logits).
+    // one 1024-thread work-group per row of lg (f32, the edited logits), or,
+    // for the rows the split section below takes, several per row.
     //   no finite lg            point mass on raw_amax[row] (the raw logits'
     //                           argmax, 70-74; the row's own argmax if NULL)
     //   temperature <= 0        point mass on np.argmax(lg): the first
