@@ -318,6 +318,53 @@ def test_sample_rows_split_fewer_slices(prims, rows):
         assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, r
 
 
+@pytest.mark.parametrize("case", range(8))
+def test_sample_rows_split_random(prims, case):
+    """seeded random configurations through the split path (sorted outputs, no
+    top_k cut): row counts giving 8 down to 2 work-groups per row, widths off
+    whole groups, spreads, -inf and NaN entries, top_p / min_p / temperature;
+    rows whose cut float32 and f64 place apart are skipped (asserted rare)"""
+    import torch
+    rng = np.random.default_rng(1000 + case)
+    rows = int(rng.choice([1, 7, 33, 64, 100]))
+    V = int(rng.integers(16384, 60000))
+    sigma = float(rng.choice([1.0, 3.0, 6.0]))
+    top_k = int(rng.choice([0, V, V + 5]))
+    top_p = float(rng.choice([0.5, 0.9, 0.99]))
+    min_p = float(rng.choice([0.0, 0.02]))
+    temp = float(rng.choice([0.5, 1.0, 1.5]))
+    L = (rng.standard_normal((rows, V)) * sigma).astype(np.float32)
+    L[rng.random((rows, V)) < 0.01] = -np.inf
+    if case % 2:
+        L[rng.random((rows, V)) < 0.001] = np.nan
+    keep = []
+    for r in range(rows):
+        x = L[r][np.isfinite(L[r])]
+        x = np.sort(x)[::-1]
+        e32 = np.exp(x - x[0])
+        p64 = softmax(x.astype(np.float64))
+        c32 = np.searchsorted(np.cumsum(e32 / e32.sum()), np.float32(top_p)) + 1
+        c64 = np.searchsorted(np.cumsum(p64), np.float64(np.float32(top_p))) + 1
+        ok = c32 == c64 or min(c32, c64) > 4096  # (past 4096 the device leaves the row to the host)
+        if min_p > 0.0:
+            ok = ok and np.min(np.abs(p64 / p64[0] - np.float32(min_p))) > 1e-6
+        keep.append(ok)
+    assert sum(keep) >= rows - max(2, rows // 10), (rows, sum(keep))
+    want = O.sample_rows(L, np.argmax(L, axis=1), top_k, temp, top_p, min_p)
+    ids, probs, n = prims.sample_rows(torch.from_numpy(L).cuda(), top_k, temp, top_p, min_p)
+    ids, probs, n = ids.cpu().numpy(), probs.cpu().numpy(), n.cpu().numpy()
+    for r in range(rows):
+        if not keep[r]:
+            continue
+        wi, wp = want[r]
+        if len(wi) > 4096:
+            assert n[r] == -1, r
+            continue
+        assert n[r] == len(wi), (case, r, n[r], len(wi))
+        assert np.array_equal(ids[r, :n[r]], wi), (case, r)
+        assert np.abs(probs[r, :n[r]].astype(np.float64) - wp).max() <= 2e-6, (case, r)
+
+
 def test_sample_rows_left_to_host(prims):
     """count -1: a nucleus of more than 4096 sorted candidates (flat logits), and a
     row holding +inf (the reference's probabilities are NaN there); other rows of
