@@ -14,10 +14,13 @@
 // schedule with bf16 probabilities in the second product, gated on an
 // envelope rather than bits.
 //
-// Layout of the work: a work-group serves one KV head, 32 query rows and up to
-// 8 query heads of its GQA group (two waves per head, one per 16-row tile), so
-// every K/V tile staged in LDS is used by all of them; larger groups (16 for
-// 32 q / 2 kv heads) take several work-groups. Per 64-key step j:
+// Layout of the work: a work-group serves one KV head and 192 (query row,
+// head) pairs of up to 8 query heads of its GQA group, row-major (38.4 rows of
+// a 5-head group), in twelve waves of 16 pairs: three waves on each of the
+// CU's four SIMDs (ten waves of one head and 16-row tile each left two SIMDs
+// a wave short and ran 4 % slower), and every K/V tile staged in LDS is used
+// by all of them; larger groups (16 for 32 q / 2 kv heads) take several
+// work-groups. Per 64-key step j:
 //   staging   coalesced 16-byte loads (whole 256-byte key rows per
 //             instruction) of K(j+2) and V(j+1), held in registers while the
 //             step computes, then written to free LDS buffers (padded rows,
@@ -38,7 +41,7 @@
 
 namespace mg
 {
-    constexpr int kPfTiles = 2; // 16-row query tiles per work-group (one per wave and head)
+    constexpr int kPfWaves = 12; // waves per work-group, 16 (row, head) pairs each
 
     struct PfArgs
     {
@@ -48,14 +51,16 @@ namespace mg
         uint32_t qsign;    // 0x80008000 when scaling < 0: q enters with its sign flipped
     };
 
-    // HPG query heads per work-group, KB = head_dim / 32, RT 16-row tiles per
-    // wave, KT 16-key tiles per step, QT 16-row query tiles per work-group (it
-    // has HPG * QT / RT waves)
-    template <int HPG, int KB, int RT, int KT, int QT>
-    __global__ __launch_bounds__(64 * HPG * QT / RT) void k_attn_prefill(const uint16_t *__restrict__ q,
-                                                                        const uint16_t *__restrict__ kc,
-                                                                        const uint16_t *__restrict__ vc, PfArgs a,
-                                                                        float *__restrict__ out)
+    // HPG query heads per work-group, KB = head_dim / 32, KT 16-key tiles per
+    // step, W waves of 16 (query row, head) pairs each: pair p of the
+    // work-group's (kv head, head subset) is query row p / HPG, head p % HPG,
+    // so a wave's columns may mix rows and heads (each column is masked and
+    // normalised on its own) and every SIMD gets the same number of waves
+    template <int HPG, int KB, int KT, int W>
+    __global__ __launch_bounds__(64 * W) void k_attn_prefill(const uint16_t *__restrict__ q,
+                                                            const uint16_t *__restrict__ kc,
+                                                            const uint16_t *__restrict__ vc, PfArgs a,
+                                                            float *__restrict__ out)
     {
         constexpr int D = 32 * KB, NT = 2 * KB; // NT output tiles of 16 dims
         // LDS row strides (elements), D + 16 for both: the 16-byte reads of K rows
@@ -63,8 +68,8 @@ namespace mg
         // stalled a quarter of the LDS cycles)
         constexpr int SK = D + 16, SV = D + 16;
         constexpr int KS = 16 * KT;             // keys per step
-        constexpr int NTHR = 64 * HPG * QT / RT;
-        constexpr int QR = 16 * QT; // query rows per work-group
+        constexpr int NTHR = 64 * W;
+        constexpr int PW = 16 * W;                       // pairs per work-group
         constexpr int LPR = D / 8;                       // 16-byte pieces per key row
         constexpr int NPC = KS * LPR;                    // pieces per tile of K (or V)
         constexpr int PPH = (NPC + NTHR - 1) / NTHR;     // staged pieces per thread (K or V)
@@ -72,40 +77,40 @@ namespace mg
         __shared__ __align__(16) uint16_t lv[2][KS * SV];
         const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
         const int n = lane & 15, c = lane >> 4;
-        // the last query tiles attend the most keys: they start first
+        // the last pair tiles attend the most keys: they start first
         const int64_t per_tile = a.nkv * a.nsub;
         const int64_t qt = a.nqt - 1 - int64_t(blockIdx.x) / per_tile;
         const int64_t gs = int64_t(blockIdx.x) - (int64_t(blockIdx.x) / per_tile) * per_tile;
         const int64_t g = gs / a.nsub;
-        const int64_t h = g * a.hpg + (gs - g * a.nsub) * HPG + wv % HPG;
-        const int u0 = (wv / HPG) * RT;                           // this wave's first row tile
-        const int64_t q0 = qt * QR;                               // the work-group's first query row
-        const int64_t qlast = (q0 + QR < a.T ? q0 + QR : a.T) - 1; // last live row
-        const int64_t khi = a.pos0 + qlast;                       // last key any row attends
-        const int64_t p0 = a.pos0 + q0;
+        const int64_t h0 = g * a.hpg + (gs - g * a.nsub) * HPG; // the subset's first query head
+        const int64_t npair = a.T * HPG;
+        const int64_t pb0 = qt * PW;                                   // the work-group's first pair
+        const int64_t pl = (pb0 + PW < npair ? pb0 + PW : npair) - 1;  // its last live pair
+        const int64_t khi = a.pos0 + pl / HPG;                         // last key any row attends
+        const int64_t p0 = a.pos0 + pb0 / HPG;
         const int64_t klo = a.window > 0 ? (p0 - a.window + 1 > 0 ? p0 - a.window + 1 : 0) : 0;
         const int64_t rowstride = a.nkv * D;
+        const int64_t pw0 = pb0 + 16 * wv; // this wave's first pair
 
-        // B of S^T: lane (query n, c) of tile u holds q[q0 + 16(u0 + u) + n][h][32 kb + 8c ..]
-        const bf16x8 zero8 = {};
-        bf16x8 qop[RT][KB];
-        int64_t qp[RT], ql[RT]; // this lane's query position and window start
-#pragma unroll
-        for (int u = 0; u < RT; ++u) {
-            const int64_t r0 = q0 + 16 * (u0 + u) + n;
-            const int64_t row = r0 <= qlast ? r0 : qlast;
+        // B of S^T: lane (pair n, c) holds q[row][head][32 kb + 8c ..] of pair pw0 + n
+        bf16x8 qop[KB];
+        int64_t qp, ql; // this lane's query position and window start
+        {
+            const int64_t pr = pw0 + n;
+            const int64_t pc = pr <= pl ? pr : pl;
+            const int64_t row = pc / HPG, hd = h0 + (pc - row * HPG);
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
-                Vec<uint32_t, 4> w = __builtin_bit_cast(Vec<uint32_t, 4>, ld_bf16x8(q + row * a.ldq + h * D + 32 * kb + 8 * c));
+                Vec<uint32_t, 4> w = __builtin_bit_cast(Vec<uint32_t, 4>, ld_bf16x8(q + row * a.ldq + hd * D + 32 * kb + 8 * c));
 #pragma unroll
                 for (int i = 0; i < 4; ++i) w.v[i] ^= a.qsign;
-                qop[u][kb] = __builtin_bit_cast(bf16x8, w);
+                qop[kb] = __builtin_bit_cast(bf16x8, w);
             }
-            qp[u] = a.pos0 + r0;
-            ql[u] = a.window > 0 ? (qp[u] - a.window + 1 > 0 ? qp[u] - a.window + 1 : 0) : 0;
+            qp = a.pos0 + pr / HPG;
+            ql = a.window > 0 ? (qp - a.window + 1 > 0 ? qp - a.window + 1 : 0) : 0;
         }
         // the wave's rows: first and last position (for the unmasked-step test)
-        const int64_t wp0 = p0 + 16 * u0, wp1 = p0 + 16 * (u0 + RT) - 1;
+        const int64_t wp0 = a.pos0 + pw0 / HPG, wp1 = a.pos0 + (pw0 + 15) / HPG;
 
         // staging, K and V separately (one of them in registers at a time):
         // piece i of a tile is key i / LPR, 16 bytes at column i % LPR;
@@ -143,22 +148,15 @@ namespace mg
             }
         };
 
-        f32x4 o[RT][NT];
+        f32x4 o[NT];
 #pragma unroll
-        for (int u = 0; u < RT; ++u)
-#pragma unroll
-            for (int t = 0; t < NT; ++t) o[u][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        float m[RT], l[RT];
-#pragma unroll
-        for (int u = 0; u < RT; ++u) {
-            m[u] = -__builtin_huge_valf();
-            l[u] = 0.0f;
-        }
+        for (int t = 0; t < NT; ++t) o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float m = -__builtin_huge_valf(), l = 0.0f;
 
-        // S^T tiles of one step from a K buffer: lane (query n, c) holds keys
+        // S^T tiles of one step from a K buffer: lane (pair n, c) holds keys
         // 16 t + 4c + r, unscaled (scale2 > 0 multiplies inside the exponent,
         // and the row maximum of the scaled scores is the scaled maximum)
-        auto scores = [&](const uint16_t *sk, float (&sx)[RT][KT][4]) {
+        auto scores = [&](const uint16_t *sk, float (&sx)[KT][4]) {
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
                 bf16x8 kt[KB]; // K as A: lane (key n, c) holds dims 32 kb + 8c.. of key 16 t + n
@@ -166,14 +164,11 @@ namespace mg
                 for (int kb = 0; kb < KB; ++kb)
                     kt[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const Vec<uint32_t, 4> *>(
                                                             sk + (16 * t + n) * SK + 32 * kb + 8 * c));
+                f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int u = 0; u < RT; ++u) {
-                    f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int kb = 0; kb < KB; ++kb) st = mfma_bf16(kt[kb], qop[kb], st);
 #pragma unroll
-                    for (int kb = 0; kb < KB; ++kb) st = mfma_bf16(kt[kb], qop[u][kb], st);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) sx[u][t][r] = st[r];
-                }
+                for (int r = 0; r < 4; ++r) sx[t][r] = st[r];
             }
         };
         auto wrap = [&](int64_t sl) { return sl >= a.slots ? sl - a.slots : sl; };
@@ -188,7 +183,7 @@ namespace mg
         stage(vc, klo, sb);
         commit(lv[0], SV);
         __syncthreads();
-        float sA[RT][KT][4], sB[RT][KT][4];
+        float sA[KT][4], sB[KT][4];
         scores(lk[0], sA);
         if (klo + KS <= khi) {
             stage(kc, klo + KS, wrap(sb + KS));
@@ -198,7 +193,7 @@ namespace mg
         int cur = 0;
         // one step: S(j) in s, S(j+1) computed into sx; the loop below takes two
         // steps a pass with the arrays swapped, so no copy carries S(j+1) over
-        auto step = [&](int64_t jb, float (&s)[RT][KT][4], float (&sx)[RT][KT][4]) {
+        auto step = [&](int64_t jb, float (&s)[KT][4], float (&sx)[KT][4]) {
             const int64_t s1 = wrap(sb + KS), s2 = wrap(s1 + KS);
             const bool more = jb + KS <= khi, more2 = jb + 2 * KS <= khi;
             if (more2) stage(kc, jb + 2 * KS, s2); // K(j+2), in flight through this step
@@ -207,77 +202,66 @@ namespace mg
             const bool full = jb + KS - 1 <= wp0 && (a.window <= 0 || jb >= wp1 - a.window + 1);
             if (!full) {
 #pragma unroll
-                for (int u = 0; u < RT; ++u)
+                for (int t = 0; t < KT; ++t)
 #pragma unroll
-                    for (int t = 0; t < KT; ++t)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int64_t j = jb + 16 * t + 4 * c + r;
-                            s[u][t][r] = (j > qp[u] || j < ql[u]) ? -__builtin_huge_valf() : s[u][t][r];
-                        }
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t j = jb + 16 * t + 4 * c + r;
+                        s[t][r] = (j > qp || j < ql) ? -__builtin_huge_valf() : s[t][r];
+                    }
             }
             // S(j+1) (from whatever lk[cur ^ 1] holds after the last step: in
             // bounds, unused), issued ahead of step j's softmax
             scores(lk[cur ^ 1], sx);
-            // online softmax per row; P for the p.v product, element 4(t%2) + r
+            // online softmax per pair; P for the p.v product, element 4(t%2) + r
             // of pair t/2 is key 16 t + 4c + r
-            bf16x8 pb[RT][KT / 2];
-            bool moved = false;
-            float corr[RT];
+            bf16x8 pb[KT / 2];
+            float mx = -__builtin_huge_valf();
 #pragma unroll
-            for (int u = 0; u < RT; ++u) {
-                float mx = -__builtin_huge_valf();
+            for (int t = 0; t < KT; ++t)
 #pragma unroll
-                for (int t = 0; t < KT; ++t)
+                for (int r = 0; r < 4; ++r) mx = __builtin_fmaxf(mx, s[t][r]);
+            mx = rows4_max(mx) * a.scale2;
+            // lazy reference: a pair's reference moves only when its new
+            // maximum passes the old by more than 8 (log2 units), so its
+            // weights stay at most 2^8 (exact to scale in f32 and bf16)
+            // and most steps rescale nothing; a pair with nothing attended
+            // yet (m = -inf) takes the first finite maximum
+            const bool mv = mx > m + 8.0f;
+            const float mn = mv ? mx : m;
+            // a pair with nothing attended yet keeps a zero reference: its
+            // weights are 2^-inf = 0 and nothing is rescaled into NaN
+            const float mref = mn == -__builtin_huge_valf() ? 0.0f : mn;
+            float ev[KT][4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) mx = __builtin_fmaxf(mx, s[u][t][r]);
-                mx = rows4_max(mx) * a.scale2;
-                // lazy reference: a row's reference moves only when its new
-                // maximum passes the old by more than 8 (log2 units), so its
-                // weights stay at most 2^8 (exact to scale in f32 and bf16)
-                // and most steps rescale nothing; a row with nothing attended
-                // yet (m = -inf) takes the first finite maximum
-                const bool mv = mx > m[u] + 8.0f;
-                const float mn = mv ? mx : m[u];
-                // a row with nothing attended yet keeps a zero reference: its
-                // weights are 2^-inf = 0 and nothing is rescaled into NaN
-                const float mref = mn == -__builtin_huge_valf() ? 0.0f : mn;
-                float ev[KT][4];
-#pragma unroll
-                for (int t = 0; t < KT; ++t)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        ev[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][r], a.scale2, -mref));
-                        pb[u][t / 2][4 * (t % 2) + r] = __bf16(ev[t][r]);
-                    }
-                // four partial sums: a short chain ahead of the barrier
-                float ps4[4];
+            for (int t = 0; t < KT; ++t)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    ps4[r] = ev[0][r];
-#pragma unroll
-                    for (int t = 1; t < KT; ++t) ps4[r] += ev[t][r];
+                    ev[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][r], a.scale2, -mref));
+                    pb[t / 2][4 * (t % 2) + r] = __bf16(ev[t][r]);
                 }
-                const float ps = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
-                corr[u] = __builtin_amdgcn_exp2f(m[u] - mref);
-                moved |= mv;
-                l[u] = (mv ? l[u] * corr[u] : l[u]) + ps;
-                m[u] = mn;
+            // four partial sums: a short chain ahead of the barrier
+            float ps4[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                ps4[r] = ev[0][r];
+#pragma unroll
+                for (int t = 1; t < KT; ++t) ps4[r] += ev[t][r];
             }
+            const float ps = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
+            const float corr = __builtin_amdgcn_exp2f(m - mref);
+            l = (mv ? l * corr : l) + ps;
+            m = mn;
             if (more2) commit(lk[cur], SK); // K(j+2) over K(j)
             if (more) stage(vc, jb + KS, s1);
-            if (__builtin_amdgcn_ballot_w64(moved) != 0) {
-                // O rows are query rows 4c + r: their factors come from lanes 4c + r
+            if (__builtin_amdgcn_ballot_w64(mv) != 0) {
+                // O rows are pairs 4c + r: their factors come from lanes 4c + r
+                float cr[4];
 #pragma unroll
-                for (int u = 0; u < RT; ++u) {
-                    float cr[4];
+                for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * c + r, 64);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr[u], 4 * c + r, 64);
+                for (int t = 0; t < NT; ++t)
 #pragma unroll
-                    for (int t = 0; t < NT; ++t)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) o[u][t][r] *= cr[r];
-                }
+                    for (int r = 0; r < 4; ++r) o[t][r] *= cr[r];
             }
             // V as B of P V: lane (dim n, c) gets keys 32 i + 4c + r and
             // 32 i + 16 + 4c + r of dim 16 s + n from the transposing read (lanes
@@ -290,8 +274,7 @@ namespace mg
                     const bf16x4 v0 = lds_read_tr(vr + 32 * i * SV + 16 * t);
                     const bf16x4 v1 = lds_read_tr(vr + (32 * i + 16) * SV + 16 * t);
                     const bf16x8 vb = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-#pragma unroll
-                    for (int u = 0; u < RT; ++u) o[u][t] = mfma_bf16(pb[u][i], vb, o[u][t]);
+                    o[t] = mfma_bf16(pb[i], vb, o[t]);
                 }
             if (more) commit(lv[cur ^ 1], SV); // V(j+1) over V(j-1)
             __syncthreads(); // the next buffers are written; these are free again
@@ -304,20 +287,18 @@ namespace mg
             step(jb + KS, sB, sA);
         }
 
-        // out = acc / sumexp, rows 4c + r of each tile from lanes 4c + r
+        // out = acc / sumexp, pairs 4c + r from lanes 4c + r
+        const float lt = rows4_sum(l);
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
-        for (int u = 0; u < RT; ++u) {
-            const float lt = rows4_sum(l[u]);
-            const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        for (int r = 0; r < 4; ++r) {
+            const float ir = __shfl(inv, 4 * c + r, 64);
+            const int64_t pr = pw0 + 4 * c + r;
+            if (pr <= pl) {
+                const int64_t row = pr / HPG, hd = h0 + (pr - row * HPG);
+                float *dst = out + row * a.ldo + hd * D + n;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float ir = __shfl(inv, 4 * c + r, 64);
-                const int64_t row = q0 + 16 * (u0 + u) + 4 * c + r;
-                if (row <= qlast) {
-                    float *dst = out + row * a.ldo + h * D + n;
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) dst[16 * t] = o[u][t][r] * ir;
-                }
+                for (int t = 0; t < NT; ++t) dst[16 * t] = o[t][r] * ir;
             }
         }
     }
@@ -328,8 +309,8 @@ namespace mg
     {
         need(nq > 0 && nkv > 0 && nq % nkv == 0, "attn_prefill: q_heads must be a multiple of kv_heads");
         const int64_t hpg = nq / nkv;
-        // a work-group serves up to 8 query heads of one kv head (2 waves
-        // each); larger groups split over work-groups of the largest divisor <= 8
+        // a work-group serves up to 8 query heads of one kv head; larger
+        // groups split over work-groups of the largest divisor <= 8
         int64_t hw = hpg;
         while (hw > 8 || hpg % hw != 0) --hw;
         const int64_t nsub = hpg / hw;
@@ -344,7 +325,7 @@ namespace mg
         const int64_t lo0 = window > 0 ? (pos0 - window + 1 > 0 ? pos0 - window + 1 : 0) : 0;
         need(pos0 + T - 1 - lo0 + 1 <= slots,
              "attn_prefill: the attended keys do not fit the cache ring (pos0 + T - lo > cache_slots)");
-        const int64_t nqt = (T + 16 * kPfTiles - 1) / (16 * kPfTiles);
+        const int64_t nqt = (T * hw + 16 * kPfWaves - 1) / (16 * kPfWaves);
         need(nqt * nkv * nsub <= int64_t(0x7fffffff), "attn_prefill: too many query tiles");
         // the kernel scales inside the exponent by a positive factor: a negative
         // scaling flips the sign of q instead (exact in bf16 and in the products),
@@ -357,12 +338,10 @@ namespace mg
         auto go = [&](auto kern, int waves) {
             hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * waves)), 0, c->stream, q, kc, vc, a, out);
         };
-        // one 16-row tile per wave (kPfTiles * HPG waves) for groups of up to 8 heads;
-        // 64-key steps
+        // kPfWaves waves of 16 (row, head) pairs for groups of up to 8 heads; 64-key steps
 #define MG_PF_CASE(H)                                                                                               \
     case H:                                                                                                         \
-        D == 128 ? go(k_attn_prefill<H, 4, 1, 4, kPfTiles>, kPfTiles * H)                                          \
-                 : go(k_attn_prefill<H, 2, 1, 4, kPfTiles>, kPfTiles * H);                                         \
+        D == 128 ? go(k_attn_prefill<H, 4, 4, kPfWaves>, kPfWaves) : go(k_attn_prefill<H, 2, 4, kPfWaves>, kPfWaves); \
         break;
         switch (hw) {
             MG_PF_CASE(1)
