@@ -18,7 +18,11 @@ drawn with torch's generator on the device (N(0,1) activations, N(1,0.05)
 weights, N(0,3) scores, U{-127..127} quants, U[1e-3,2e-2] f16 scales, N(0,4)
 logits). Per-op times are the median of R launches bracketed by HIP events on
 the launch stream, with a 512 MiB buffer rewritten before each launch so no op
-is served from the 256 MiB Infinity Cache.
+is served from the 256 MiB Infinity Cache. Each single launch so timed carries
+the protocol's own floor (`launch_floor`, a few us), so every op also reports
+`us_in_stream`: R (rewrite, op) pairs against R rewrites alone, both as one
+bracketed sequence, the difference divided by R, i.e. the op's kernels and the
+gaps between launches inside a stream of work, with the same HBM-resident inputs.
 
 `cpu_baseline` times the CPU restatement of the reference's own tensor path
 (oracle/liboracle.so: f64 twin arithmetic with OpenMP over rows, as
@@ -113,7 +117,7 @@ KERNEL_OF = {
     "attn_decode_131072": "k_attn_split<5,4> + k_attn_combine",
     "gemv_q8_0_decode": "k_gemv_q8_0<1>",
     "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
-    "attn_prefill_4096": "k_attn_prefill<5,4,1,4>",
+    "attn_prefill_4096": "k_attn_prefill<5,4,4,12>",
     "softmax_causal_softcap30": "k_softmax_fast<cap>",
     "norm_rows_f32_embed": "k_norm_f32rows",
     "sample_rows_topk0": "k_sample_split_stats + decide + gather + finish",
@@ -273,6 +277,33 @@ def time_op(torch, fn, reps, flush):
         b.synchronize()
         times.append(a.elapsed_time(b) * 1e3)  # us
     return statistics.median(times), min(times)
+
+
+def time_in_stream(torch, fn, reps, flush, rounds=11):
+    """An op's cost inside a stream of work, free of the per-launch event floor:
+    `reps` (flush, op) pairs and `reps` flushes alone, each sequence bracketed by
+    one pair of HIP events; the difference over `reps` is the op's kernels plus
+    the gaps between launches, with inputs in HBM as for the per-launch median.
+    The median over `rounds` such differences, the two sequences' order
+    alternating from round to round."""
+    stream = torch.cuda.current_stream()
+    diffs = []
+    for k in range(rounds):
+        spans = {}
+        for with_op in ((False, True) if k % 2 == 0 else (True, False)):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record(stream)
+            for _ in range(reps):
+                flush.zero_()
+                if with_op:
+                    fn()
+            b.record(stream)
+            b.synchronize()
+            spans[with_op] = a.elapsed_time(b) * 1e3
+        diffs.append((spans[True] - spans[False]) / reps)
+    return statistics.median(diffs)
 
 
 def lib_digest():
@@ -471,19 +502,22 @@ def main():
     per = {}
     for name, fn in ops.items():
         med, best = time_op(torch, fn, args.reps, flush)
+        ins = time_in_stream(torch, fn, args.reps, flush)
         gbps = BYTES[name] / (med * 1e-6) / 1e9
         per[name] = {"us": round(med, 2), "us_min": round(best, 2), "bytes": BYTES[name],
                      "GBps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
-                     "kernel": KERNEL_OF[name]}
+                     "us_in_stream": round(ins, 2), "kernel": KERNEL_OF[name]}
+        if name not in FLOPS and ins > 0:
+            per[name]["GBps_in_stream"] = round(BYTES[name] / (ins * 1e-6) / 1e9, 1)
         if name in FLOPS:
             tf = FLOPS[name] / (med * 1e-6) / 1e12
             per[name].update({"flops": FLOPS[name], "TFLOPs": round(tf, 1), "bound": "mfma",
                               "pct_peak": round(100 * tf / PEAK_TFLOPS, 1)})
-            print(f"# {name:28s} {med:9.2f} us  {tf:8.1f} TFLOP/s {100 * tf / PEAK_TFLOPS:5.1f} % of bf16 MFMA",
-                  file=sys.stderr, flush=True)
+            print(f"# {name:28s} {med:9.2f} us  {tf:8.1f} TFLOP/s {100 * tf / PEAK_TFLOPS:5.1f} % of bf16 MFMA"
+                  f"  (in stream {ins:8.2f} us)", file=sys.stderr, flush=True)
             continue
-        print(f"# {name:28s} {med:9.2f} us  {gbps:8.1f} GB/s  {100 * gbps / PEAK_GBPS:5.1f} %",
-              file=sys.stderr, flush=True)
+        print(f"# {name:28s} {med:9.2f} us  {gbps:8.1f} GB/s  {100 * gbps / PEAK_GBPS:5.1f} %"
+              f"  (in stream {ins:8.2f} us)", file=sys.stderr, flush=True)
 
     dom = max(STEP_OPS, key=lambda n: per[n]["us"])
     kern = KERNEL_OF[dom]
