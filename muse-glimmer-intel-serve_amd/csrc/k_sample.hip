@@ -195,7 +195,8 @@ namespace mg
         double red[kSfThreads];
         double redd[kSfThreads / 64];
         uint64_t redu[kSfThreads / 64];
-        uint32_t bc[4]; // broadcast words
+        uint32_t bc[4];     // broadcast words
+        uint32_t bslice[8]; // per-slice broadcast words (split rows)
     };
     struct SfLds : SfRed
     {
@@ -816,6 +817,7 @@ namespace mg
     // one-work-group algorithm (sample_row) on it instead, with the S the
     // slices summed: the same selection and the same bits as the split path's.
     constexpr int kSplitMax = 8; // work-groups per row
+    static_assert(kSplitMax <= int(sizeof(SfRed::bslice) / sizeof(uint32_t)), "a broadcast word per slice");
 
     struct SplitStat
     {
@@ -903,7 +905,25 @@ namespace mg
     {
         __shared__ SfRed L;
         constexpr int kBins = 1 << kHistBits;
+        constexpr int BPT = kBins / kSfThreads;
         const int64_t row = blockIdx.x;
+        // every request first, so that the slices' counts and histograms come
+        // back in one trip: lane g < G of each wave fetches slice g's counts
+        // (read across the wave below), and thread t bins kBins-1-BPT*t-e of
+        // every slice (slices past G re-read the last and count nothing)
+        const int lane = int(threadIdx.x) & 63;
+        const SplitStat my = w.stat[row * G + (lane < G ? lane : G - 1)];
+        const uint32_t *h = w.hist + row * G * kBins;
+        uint32_t hv[kSplitMax][BPT];
+#pragma unroll
+        for (int g = 0; g < kSplitMax; ++g)
+#pragma unroll
+            for (int e = 0; e < BPT; ++e)
+                hv[g][e] = h[(g < G ? g : G - 1) * kBins + kBins - 1 - BPT * int(threadIdx.x) - e];
+        auto rd64 = [](uint64_t v, int l) {
+            return uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v)), l))) |
+                   (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(v >> 32)), l))) << 32);
+        };
         // the slices' counts, folded in slice order by every thread alike
         int64_t nfin = 0, nc = 0;
         uint64_t best = 0;
@@ -911,14 +931,29 @@ namespace mg
         int64_t ncs[kSplitMax];
 #pragma unroll
         for (int g = 0; g < kSplitMax; ++g) {
-            const SplitStat t = w.stat[row * G + (g < G ? g : G - 1)];
             const bool live = g < G;
-            nfin += live ? int64_t(t.nfin) : 0;
-            nc += live ? int64_t(t.nc) : 0;
-            ncs[g] = live ? int64_t(t.nc) : 0;
-            best = live && t.best > best ? t.best : best;
-            mk = live && t.mk > mk ? t.mk : mk;
+            const int64_t tn = int64_t(rd64(my.nfin, g)), tc = int64_t(rd64(my.nc, g));
+            const uint64_t tb = rd64(my.best, g);
+            const uint32_t tm = uint32_t(__builtin_amdgcn_readlane(int(my.mk), g));
+            nfin += live ? tn : 0;
+            nc += live ? tc : 0;
+            ncs[g] = live ? tc : 0;
+            best = live && tb > best ? tb : best;
+            mk = live && tm > mk ? tm : mk;
         }
+        // the bins summed over the slices and their prefix from the top, for
+        // every row alike (rows that need no threshold leave them unused)
+        uint32_t c[BPT];
+        int own = 0;
+#pragma unroll
+        for (int e = 0; e < BPT; ++e) {
+            c[e] = 0;
+#pragma unroll
+            for (int g = 0; g < kSplitMax; ++g) c[e] += g < G ? hv[g][e] : 0u;
+            own += int(c[e]);
+        }
+        int tot;
+        int64_t acc = sf_scan(own, L, &tot);
         int64_t *oi = out_ids + row * V;
         float *op = out_p + row * V;
         if (nfin == 0 || !(temperature > 0.0f)) {
@@ -946,35 +981,14 @@ namespace mg
         r.ncand = nc;
         if (gall) {
             // every candidate into region 0, slice by slice
-            uint32_t acc = 0;
+            uint32_t at = 0;
 #pragma unroll
             for (int g = 0; g < kSplitMax; ++g) {
-                r.off0[g] = acc;
-                acc += uint32_t(ncs[g]);
+                r.off0[g] = at;
+                at += uint32_t(ncs[g]);
             }
-            r.n0 = acc;
+            r.n0 = at;
         } else {
-            // thread t holds bins kBins-1-BPT*t-e of every slice (all requested
-            // at once: slices past G re-read the last and count nothing)
-            constexpr int BPT = kBins / kSfThreads;
-            const uint32_t *h = w.hist + row * G * kBins;
-            uint32_t hv[kSplitMax][BPT];
-#pragma unroll
-            for (int g = 0; g < kSplitMax; ++g)
-#pragma unroll
-                for (int e = 0; e < BPT; ++e)
-                    hv[g][e] = h[(g < G ? g : G - 1) * kBins + kBins - 1 - BPT * int(threadIdx.x) - e];
-            uint32_t c[BPT];
-            int own = 0;
-#pragma unroll
-            for (int e = 0; e < BPT; ++e) {
-                c[e] = 0;
-#pragma unroll
-                for (int g = 0; g < kSplitMax; ++g) c[e] += g < G ? hv[g][e] : 0u;
-                own += int(c[e]);
-            }
-            int tot;
-            int64_t acc = sf_scan(own, L, &tot);
 #pragma unroll
             for (int e = 0; e < BPT; ++e) {
                 if (acc < ng && acc + c[e] >= ng) {
@@ -995,21 +1009,34 @@ namespace mg
                 }
                 return;
             }
-            // each slice's keys above bstar and in it, in slice order
+            // each slice's keys above bstar and in it, in slice order: the keys
+            // above number fewer than ng <= kSortMax in all, so every partial
+            // count of a slice fits 16 bits and four slices' counts travel in
+            // one 64-bit sum; thread g < G fetches slice g's bstar bin, all G
+            // requests in flight together, published by the sum's barriers
+            const bool fetch = int(threadIdx.x) < G;
+            const uint32_t nbl = h[(fetch ? int(threadIdx.x) : 0) * kBins + bstar];
+            uint64_t ab[2] = {0, 0};
+#pragma unroll
+            for (int g = 0; g < kSplitMax; ++g) {
+                uint32_t above = 0;
+#pragma unroll
+                for (int e = 0; e < BPT; ++e)
+                    above += g < G && uint32_t(kBins - 1 - BPT * int(threadIdx.x) - e) > bstar ? hv[g][e] : 0u;
+                ab[g / 4] += uint64_t(above) << (16 * (g % 4));
+            }
+            if (fetch) L.bslice[threadIdx.x] = nbl;
+            ab[0] = sf_sum_u64(ab[0], L);
+            if (G > 4) ab[1] = sf_sum_u64(ab[1], L);
             uint32_t a0 = 0, a1 = 0;
 #pragma unroll
             for (int g = 0; g < kSplitMax; ++g) {
                 if (g < G) {
-                    int above = 0;
-#pragma unroll
-                    for (int e = 0; e < BPT; ++e)
-                        above += uint32_t(kBins - 1 - BPT * int(threadIdx.x) - e) > bstar ? int(hv[g][e]) : 0;
-                    const uint32_t na = uint32_t(sf_sum_u64(uint64_t(above), L));
-                    const uint32_t nb = h[g * kBins + bstar];
+                    const uint32_t na = uint32_t(ab[g / 4] >> (16 * (g % 4))) & 0xffffu;
                     r.off0[g] = a0;
                     r.off1[g] = a1;
                     a0 += na;
-                    a1 += nb;
+                    a1 += L.bslice[g];
                 }
             }
             r.bstar = bstar;
