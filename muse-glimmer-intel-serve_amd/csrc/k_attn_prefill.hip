@@ -14,20 +14,21 @@
 // schedule with bf16 probabilities in the second product, gated on an
 // envelope rather than bits.
 //
-// Layout of the work: a work-group serves one KV head and 192 (query row,
-// head) pairs of up to 8 query heads of its GQA group, row-major (38.4 rows of
-// a 5-head group), in twelve waves of 16 pairs: three waves on each of the
-// CU's four SIMDs (ten waves of one head and 16-row tile each left two SIMDs
-// a wave short and ran 4 % slower), and every K/V tile staged in LDS is used
-// by all of them; larger groups (16 for 32 q / 2 kv heads) take several
-// work-groups. Per 64-key step j:
+// Layout of the work: a work-group serves one KV head and 256 (query row,
+// head) pairs of up to 8 query heads of its GQA group, row-major (51.2 rows of
+// a 5-head group), in sixteen waves of 16 pairs: four waves on each of the
+// CU's four SIMDs, at most 128 VGPRs a wave, so that while one wave waits on
+// its LDS reads or its exponentials the others keep the matrix cores and the
+// VALU busy (twelve waves that computed the next step's scores ahead of the
+// softmax in their own registers ran 7 % slower); every K/V tile staged in
+// LDS is used by all of them; larger groups (16 for 32 q / 2 kv heads) take
+// several work-groups. Per 64-key step j:
 //   staging   coalesced 16-byte loads (whole 256-byte key rows per
-//             instruction) of K(j+2) and V(j+1), held in registers while the
-//             step computes, then written to free LDS buffers (padded rows,
-//             conflict-free reads); one barrier per step;
-//   S^T       of step j + 1, computed ahead of step j's softmax: A = 16 keys
-//             x 32 dims of K from LDS, B = the wave's 16 query rows
-//             (registers): C lane (query n, c) holds keys 4c..4c+3 of the
+//             instruction) of K(j+1) and then V(j+1), held in registers while
+//             the step computes, then written to the free LDS buffers (padded
+//             rows, conflict-free reads); one barrier per step;
+//   S^T       A = 16 keys x 32 dims of K(j) from LDS, B = the wave's 16 pairs
+//             (registers): C lane (pair n, c) holds keys 4c..4c+3 of the
 //             tile, four key tiles per step;
 //   softmax   per query row in f32 (hardware exp2 of fma(score, scale, -ref)),
 //             the row max and sum across the four lane groups by permlane
@@ -41,7 +42,7 @@
 
 namespace mg
 {
-    constexpr int kPfWaves = 12; // waves per work-group, 16 (row, head) pairs each
+    constexpr int kPfWaves = 16; // waves per work-group, 16 (row, head) pairs each
 
     struct PfArgs
     {
@@ -173,30 +174,22 @@ namespace mg
         };
         auto wrap = [&](int64_t sl) { return sl >= a.slots ? sl - a.slots : sl; };
 
-        // Software pipeline: the scores of step j + 1 run on the matrix cores
-        // while step j's softmax runs on the VALU. At the top of step j, K(j+1)
-        // is in lk[cur ^ 1], V(j) in lv[cur], and S(j) in registers; lk[cur]
-        // (K(j), read during step j - 1) is free for K(j+2).
+        // At the top of step j, K(j) is in lk[cur] and V(j) in lv[cur]; the
+        // other buffers (K(j-1) and V(j-1), read before the last barrier) are
+        // free for K(j+1) and V(j+1).
         int64_t sb = klo % a.slots; // ring slot of key jb
         stage(kc, klo, sb);
         commit(lk[0], SK);
         stage(vc, klo, sb);
         commit(lv[0], SV);
         __syncthreads();
-        float sA[KT][4], sB[KT][4];
-        scores(lk[0], sA);
-        if (klo + KS <= khi) {
-            stage(kc, klo + KS, wrap(sb + KS));
-            commit(lk[1], SK);
-        }
-        __syncthreads(); // K(1) is in lk[1]; every wave is done with lk[0]
         int cur = 0;
-        // one step: S(j) in s, S(j+1) computed into sx; the loop below takes two
-        // steps a pass with the arrays swapped, so no copy carries S(j+1) over
-        auto step = [&](int64_t jb, float (&s)[KT][4], float (&sx)[KT][4]) {
-            const int64_t s1 = wrap(sb + KS), s2 = wrap(s1 + KS);
-            const bool more = jb + KS <= khi, more2 = jb + 2 * KS <= khi;
-            if (more2) stage(kc, jb + 2 * KS, s2); // K(j+2), in flight through this step
+        auto step = [&](int64_t jb) {
+            const int64_t s1 = wrap(sb + KS);
+            const bool more = jb + KS <= khi;
+            if (more) stage(kc, jb + KS, s1); // K(j+1), in flight through the scores and softmax
+            float s[KT][4];
+            scores(lk[cur], s);
             // every row of the wave attends the whole step unless it reaches
             // past the wave's first row or before its last row's window
             const bool full = jb + KS - 1 <= wp0 && (a.window <= 0 || jb >= wp1 - a.window + 1);
@@ -209,9 +202,6 @@ namespace mg
                         s[t][r] = (j > qp || j < ql) ? -__builtin_huge_valf() : s[t][r];
                     }
             }
-            // S(j+1) (from whatever lk[cur ^ 1] holds after the last step: in
-            // bounds, unused), issued ahead of step j's softmax
-            scores(lk[cur ^ 1], sx);
             // online softmax per pair; P for the p.v product, element 4(t%2) + r
             // of pair t/2 is key 16 t + 4c + r
             bf16x8 pb[KT / 2];
@@ -251,7 +241,7 @@ namespace mg
             const float corr = __builtin_amdgcn_exp2f(m - mref);
             l = (mv ? l * corr : l) + ps;
             m = mn;
-            if (more2) commit(lk[cur], SK); // K(j+2) over K(j)
+            if (more) commit(lk[cur ^ 1], SK); // K(j+1) over K(j-1)
             if (more) stage(vc, jb + KS, s1);
             if (__builtin_amdgcn_ballot_w64(mv) != 0) {
                 // O rows are pairs 4c + r: their factors come from lanes 4c + r
@@ -281,11 +271,7 @@ namespace mg
             cur ^= 1;
             sb = s1;
         };
-        for (int64_t jb = klo; jb <= khi; jb += 2 * KS) {
-            step(jb, sA, sB);
-            if (jb + KS > khi) break;
-            step(jb + KS, sB, sA);
-        }
+        for (int64_t jb = klo; jb <= khi; jb += KS) step(jb);
 
         // out = acc / sumexp, pairs 4c + r from lanes 4c + r
         const float lt = rows4_sum(l);
