@@ -117,7 +117,7 @@ KERNEL_OF = {
     "attn_decode_131072": "k_attn_split<5,4> + k_attn_combine",
     "gemv_q8_0_decode": "k_gemv_q8_0<1>",
     "vocab_tail_top64_dist": "k_vocab_chunk<tail> + k_vocab_merge<tail> + k_sample_dist",
-    "attn_prefill_4096": "k_attn_prefill<5,4,4,16>",
+    "attn_prefill_4096": "k_attn_prefill<5,4,4,8,2>",
     "softmax_causal_softcap30": "k_softmax_fast<cap>",
     "norm_rows_f32_embed": "k_norm_f32rows",
     "sample_rows_topk0": "k_sample_split_stats + decide + gather + finish",

@@ -16,20 +16,21 @@
 //
 // Layout of the work: a work-group serves one KV head and 256 (query row,
 // head) pairs of up to 8 query heads of its GQA group, row-major (51.2 rows of
-// a 5-head group), in sixteen waves of 16 pairs: four waves on each of the
-// CU's four SIMDs, at most 128 VGPRs a wave, so that while one wave waits on
-// its LDS reads or its exponentials the others keep the matrix cores and the
-// VALU busy (twelve waves that computed the next step's scores ahead of the
-// softmax in their own registers ran 7 % slower); every K/V tile staged in
+// a 5-head group), in eight waves of two 16-pair tiles each: two waves on each
+// of the CU's four SIMDs, up to 256 VGPRs a wave (225 at head_dim 128), and
+// every K and V fragment a wave reads from LDS feeds both of its tiles, so the
+// LDS carries half the bytes per pair that one-tile waves need (sixteen such
+// waves, four a SIMD, ran 8 % slower; twelve that also computed the next
+// step's scores ahead of the softmax, 15 % slower); every K/V tile staged in
 // LDS is used by all of them; larger groups (16 for 32 q / 2 kv heads) take
 // several work-groups. Per 64-key step j:
 //   staging   coalesced 16-byte loads (whole 256-byte key rows per
 //             instruction) of K(j+1) and then V(j+1), held in registers while
 //             the step computes, then written to the free LDS buffers (padded
 //             rows, conflict-free reads); one barrier per step;
-//   S^T       A = 16 keys x 32 dims of K(j) from LDS, B = the wave's 16 pairs
-//             (registers): C lane (pair n, c) holds keys 4c..4c+3 of the
-//             tile, four key tiles per step;
+//   S^T       A = 16 keys x 32 dims of K(j) from LDS, B = one of the wave's
+//             16-pair tiles (registers): C lane (pair n, c) holds keys
+//             4c..4c+3 of the key tile, four key tiles per step;
 //   softmax   per query row in f32 (hardware exp2 of fma(score, scale, -ref)),
 //             the row max and sum across the four lane groups by permlane
 //             swaps; a row's reference maximum moves only when passed by more
@@ -42,7 +43,8 @@
 
 namespace mg
 {
-    constexpr int kPfWaves = 16; // waves per work-group, 16 (row, head) pairs each
+    constexpr int kPfWaves = 8; // waves per work-group
+    constexpr int kPfRT = 2;    // 16-pair tiles per wave
 
     struct PfArgs
     {
@@ -53,11 +55,12 @@ namespace mg
     };
 
     // HPG query heads per work-group, KB = head_dim / 32, KT 16-key tiles per
-    // step, W waves of 16 (query row, head) pairs each: pair p of the
+    // step, W waves of RT x 16 (query row, head) pairs each: pair p of the
     // work-group's (kv head, head subset) is query row p / HPG, head p % HPG,
     // so a wave's columns may mix rows and heads (each column is masked and
-    // normalised on its own) and every SIMD gets the same number of waves
-    template <int HPG, int KB, int KT, int W>
+    // normalised on its own); a wave's RT tiles share every K and V fragment
+    // it reads from LDS
+    template <int HPG, int KB, int KT, int W, int RT>
     __global__ __launch_bounds__(64 * W) void k_attn_prefill(const uint16_t *__restrict__ q,
                                                             const uint16_t *__restrict__ kc,
                                                             const uint16_t *__restrict__ vc, PfArgs a,
@@ -70,7 +73,7 @@ namespace mg
         constexpr int SK = D + 16, SV = D + 16;
         constexpr int KS = 16 * KT;             // keys per step
         constexpr int NTHR = 64 * W;
-        constexpr int PW = 16 * W;                       // pairs per work-group
+        constexpr int PW = 16 * RT * W;                  // pairs per work-group
         constexpr int LPR = D / 8;                       // 16-byte pieces per key row
         constexpr int NPC = KS * LPR;                    // pieces per tile of K (or V)
         constexpr int PPH = (NPC + NTHR - 1) / NTHR;     // staged pieces per thread (K or V)
@@ -91,13 +94,15 @@ namespace mg
         const int64_t p0 = a.pos0 + pb0 / HPG;
         const int64_t klo = a.window > 0 ? (p0 - a.window + 1 > 0 ? p0 - a.window + 1 : 0) : 0;
         const int64_t rowstride = a.nkv * D;
-        const int64_t pw0 = pb0 + 16 * wv; // this wave's first pair
+        const int64_t pw0 = pb0 + 16 * RT * wv; // this wave's first pair
 
-        // B of S^T: lane (pair n, c) holds q[row][head][32 kb + 8c ..] of pair pw0 + n
-        bf16x8 qop[KB];
-        int64_t qp, ql; // this lane's query position and window start
-        {
-            const int64_t pr = pw0 + n;
+        // B of S^T: lane (pair n, c) of tile u holds q[row][head][32 kb + 8c ..]
+        // of pair pw0 + 16 u + n
+        bf16x8 qop[RT][KB];
+        int64_t qp[RT], ql[RT]; // this lane's query positions and window starts
+#pragma unroll
+        for (int u = 0; u < RT; ++u) {
+            const int64_t pr = pw0 + 16 * u + n;
             const int64_t pc = pr <= pl ? pr : pl;
             const int64_t row = pc / HPG, hd = h0 + (pc - row * HPG);
 #pragma unroll
@@ -105,13 +110,13 @@ namespace mg
                 Vec<uint32_t, 4> w = __builtin_bit_cast(Vec<uint32_t, 4>, ld_bf16x8(q + row * a.ldq + hd * D + 32 * kb + 8 * c));
 #pragma unroll
                 for (int i = 0; i < 4; ++i) w.v[i] ^= a.qsign;
-                qop[kb] = __builtin_bit_cast(bf16x8, w);
+                qop[u][kb] = __builtin_bit_cast(bf16x8, w);
             }
-            qp = a.pos0 + pr / HPG;
-            ql = a.window > 0 ? (qp - a.window + 1 > 0 ? qp - a.window + 1 : 0) : 0;
+            qp[u] = a.pos0 + pr / HPG;
+            ql[u] = a.window > 0 ? (qp[u] - a.window + 1 > 0 ? qp[u] - a.window + 1 : 0) : 0;
         }
         // the wave's rows: first and last position (for the unmasked-step test)
-        const int64_t wp0 = a.pos0 + pw0 / HPG, wp1 = a.pos0 + (pw0 + 15) / HPG;
+        const int64_t wp0 = a.pos0 + pw0 / HPG, wp1 = a.pos0 + (pw0 + 16 * RT - 1) / HPG;
 
         // staging, K and V separately (one of them in registers at a time):
         // piece i of a tile is key i / LPR, 16 bytes at column i % LPR;
@@ -149,15 +154,22 @@ namespace mg
             }
         };
 
-        f32x4 o[NT];
+        f32x4 o[RT][NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        float m = -__builtin_huge_valf(), l = 0.0f;
+        for (int u = 0; u < RT; ++u)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) o[u][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float m[RT], l[RT];
+#pragma unroll
+        for (int u = 0; u < RT; ++u) {
+            m[u] = -__builtin_huge_valf();
+            l[u] = 0.0f;
+        }
 
-        // S^T tiles of one step from a K buffer: lane (pair n, c) holds keys
-        // 16 t + 4c + r, unscaled (scale2 > 0 multiplies inside the exponent,
-        // and the row maximum of the scaled scores is the scaled maximum)
-        auto scores = [&](const uint16_t *sk, float (&sx)[KT][4]) {
+        // S^T tiles of one step from a K buffer: lane (pair n, c) of tile u
+        // holds keys 16 t + 4c + r, unscaled (scale2 > 0 multiplies inside the
+        // exponent, and the row maximum of the scaled scores is the scaled maximum)
+        auto scores = [&](const uint16_t *sk, float (&sx)[RT][KT][4]) {
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
                 bf16x8 kt[KB]; // K as A: lane (key n, c) holds dims 32 kb + 8c.. of key 16 t + n
@@ -165,11 +177,14 @@ namespace mg
                 for (int kb = 0; kb < KB; ++kb)
                     kt[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const Vec<uint32_t, 4> *>(
                                                             sk + (16 * t + n) * SK + 32 * kb + 8 * c));
-                f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int kb = 0; kb < KB; ++kb) st = mfma_bf16(kt[kb], qop[kb], st);
+                for (int u = 0; u < RT; ++u) {
+                    f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sx[t][r] = st[r];
+                    for (int kb = 0; kb < KB; ++kb) st = mfma_bf16(kt[kb], qop[u][kb], st);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sx[u][t][r] = st[r];
+                }
             }
         };
         auto wrap = [&](int64_t sl) { return sl >= a.slots ? sl - a.slots : sl; };
@@ -188,70 +203,81 @@ namespace mg
             const int64_t s1 = wrap(sb + KS);
             const bool more = jb + KS <= khi;
             if (more) stage(kc, jb + KS, s1); // K(j+1), in flight through the scores and softmax
-            float s[KT][4];
+            float s[RT][KT][4];
             scores(lk[cur], s);
             // every row of the wave attends the whole step unless it reaches
             // past the wave's first row or before its last row's window
             const bool full = jb + KS - 1 <= wp0 && (a.window <= 0 || jb >= wp1 - a.window + 1);
             if (!full) {
 #pragma unroll
-                for (int t = 0; t < KT; ++t)
+                for (int u = 0; u < RT; ++u)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int64_t j = jb + 16 * t + 4 * c + r;
-                        s[t][r] = (j > qp || j < ql) ? -__builtin_huge_valf() : s[t][r];
-                    }
+                    for (int t = 0; t < KT; ++t)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int64_t j = jb + 16 * t + 4 * c + r;
+                            s[u][t][r] = (j > qp[u] || j < ql[u]) ? -__builtin_huge_valf() : s[u][t][r];
+                        }
             }
             // online softmax per pair; P for the p.v product, element 4(t%2) + r
             // of pair t/2 is key 16 t + 4c + r
-            bf16x8 pb[KT / 2];
-            float mx = -__builtin_huge_valf();
+            bf16x8 pb[RT][KT / 2];
+            bool moved = false;
+            float corr[RT];
 #pragma unroll
-            for (int t = 0; t < KT; ++t)
+            for (int u = 0; u < RT; ++u) {
+                float mx = -__builtin_huge_valf();
 #pragma unroll
-                for (int r = 0; r < 4; ++r) mx = __builtin_fmaxf(mx, s[t][r]);
-            mx = rows4_max(mx) * a.scale2;
-            // lazy reference: a pair's reference moves only when its new
-            // maximum passes the old by more than 8 (log2 units), so its
-            // weights stay at most 2^8 (exact to scale in f32 and bf16)
-            // and most steps rescale nothing; a pair with nothing attended
-            // yet (m = -inf) takes the first finite maximum
-            const bool mv = mx > m + 8.0f;
-            const float mn = mv ? mx : m;
-            // a pair with nothing attended yet keeps a zero reference: its
-            // weights are 2^-inf = 0 and nothing is rescaled into NaN
-            const float mref = mn == -__builtin_huge_valf() ? 0.0f : mn;
-            float ev[KT][4];
+                for (int t = 0; t < KT; ++t)
 #pragma unroll
-            for (int t = 0; t < KT; ++t)
+                    for (int r = 0; r < 4; ++r) mx = __builtin_fmaxf(mx, s[u][t][r]);
+                mx = rows4_max(mx) * a.scale2;
+                // lazy reference: a pair's reference moves only when its new
+                // maximum passes the old by more than 8 (log2 units), so its
+                // weights stay at most 2^8 (exact to scale in f32 and bf16)
+                // and most steps rescale nothing; a pair with nothing attended
+                // yet (m = -inf) takes the first finite maximum
+                const bool mv = mx > m[u] + 8.0f;
+                const float mn = mv ? mx : m[u];
+                // a pair with nothing attended yet keeps a zero reference: its
+                // weights are 2^-inf = 0 and nothing is rescaled into NaN
+                const float mref = mn == -__builtin_huge_valf() ? 0.0f : mn;
+                float ev[KT][4];
+#pragma unroll
+                for (int t = 0; t < KT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        ev[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][r], a.scale2, -mref));
+                        pb[u][t / 2][4 * (t % 2) + r] = __bf16(ev[t][r]);
+                    }
+                // four partial sums: a short chain ahead of the barrier
+                float ps4[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    ev[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][r], a.scale2, -mref));
-                    pb[t / 2][4 * (t % 2) + r] = __bf16(ev[t][r]);
+                    ps4[r] = ev[0][r];
+#pragma unroll
+                    for (int t = 1; t < KT; ++t) ps4[r] += ev[t][r];
                 }
-            // four partial sums: a short chain ahead of the barrier
-            float ps4[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ps4[r] = ev[0][r];
-#pragma unroll
-                for (int t = 1; t < KT; ++t) ps4[r] += ev[t][r];
+                const float ps = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
+                corr[u] = __builtin_amdgcn_exp2f(m[u] - mref);
+                moved |= mv;
+                l[u] = (mv ? l[u] * corr[u] : l[u]) + ps;
+                m[u] = mn;
             }
-            const float ps = (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
-            const float corr = __builtin_amdgcn_exp2f(m - mref);
-            l = (mv ? l * corr : l) + ps;
-            m = mn;
             if (more) commit(lk[cur ^ 1], SK); // K(j+1) over K(j-1)
             if (more) stage(vc, jb + KS, s1);
-            if (__builtin_amdgcn_ballot_w64(mv) != 0) {
+            if (__builtin_amdgcn_ballot_w64(moved) != 0) {
                 // O rows are pairs 4c + r: their factors come from lanes 4c + r
-                float cr[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * c + r, 64);
+                for (int u = 0; u < RT; ++u) {
+                    float cr[4];
 #pragma unroll
-                for (int t = 0; t < NT; ++t)
+                    for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr[u], 4 * c + r, 64);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) o[t][r] *= cr[r];
+                    for (int t = 0; t < NT; ++t)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[u][t][r] *= cr[r];
+                }
             }
             // V as B of P V: lane (dim n, c) gets keys 32 i + 4c + r and
             // 32 i + 16 + 4c + r of dim 16 s + n from the transposing read (lanes
@@ -264,7 +290,8 @@ namespace mg
                     const bf16x4 v0 = lds_read_tr(vr + 32 * i * SV + 16 * t);
                     const bf16x4 v1 = lds_read_tr(vr + (32 * i + 16) * SV + 16 * t);
                     const bf16x8 vb = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                    o[t] = mfma_bf16(pb[i], vb, o[t]);
+#pragma unroll
+                    for (int u = 0; u < RT; ++u) o[u][t] = mfma_bf16(pb[u][i], vb, o[u][t]);
                 }
             if (more) commit(lv[cur ^ 1], SV); // V(j+1) over V(j-1)
             __syncthreads(); // the next buffers are written; these are free again
@@ -273,18 +300,21 @@ namespace mg
         };
         for (int64_t jb = klo; jb <= khi; jb += KS) step(jb);
 
-        // out = acc / sumexp, pairs 4c + r from lanes 4c + r
-        const float lt = rows4_sum(l);
-        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        // out = acc / sumexp, pairs 16 u + 4c + r from lanes 4c + r
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float ir = __shfl(inv, 4 * c + r, 64);
-            const int64_t pr = pw0 + 4 * c + r;
-            if (pr <= pl) {
-                const int64_t row = pr / HPG, hd = h0 + (pr - row * HPG);
-                float *dst = out + row * a.ldo + hd * D + n;
+        for (int u = 0; u < RT; ++u) {
+            const float lt = rows4_sum(l[u]);
+            const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
-                for (int t = 0; t < NT; ++t) dst[16 * t] = o[t][r] * ir;
+            for (int r = 0; r < 4; ++r) {
+                const float ir = __shfl(inv, 4 * c + r, 64);
+                const int64_t pr = pw0 + 16 * u + 4 * c + r;
+                if (pr <= pl) {
+                    const int64_t row = pr / HPG, hd = h0 + (pr - row * HPG);
+                    float *dst = out + row * a.ldo + hd * D + n;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) dst[16 * t] = o[u][t][r] * ir;
+                }
             }
         }
     }
@@ -311,7 +341,7 @@ namespace mg
         const int64_t lo0 = window > 0 ? (pos0 - window + 1 > 0 ? pos0 - window + 1 : 0) : 0;
         need(pos0 + T - 1 - lo0 + 1 <= slots,
              "attn_prefill: the attended keys do not fit the cache ring (pos0 + T - lo > cache_slots)");
-        const int64_t nqt = (T * hw + 16 * kPfWaves - 1) / (16 * kPfWaves);
+        const int64_t nqt = (T * hw + 16 * kPfRT * kPfWaves - 1) / (16 * kPfRT * kPfWaves);
         need(nqt * nkv * nsub <= int64_t(0x7fffffff), "attn_prefill: too many query tiles");
         // the kernel scales inside the exponent by a positive factor: a negative
         // scaling flips the sign of q instead (exact in bf16 and in the products),
@@ -324,10 +354,10 @@ namespace mg
         auto go = [&](auto kern, int waves) {
             hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * waves)), 0, c->stream, q, kc, vc, a, out);
         };
-        // kPfWaves waves of 16 (row, head) pairs for groups of up to 8 heads; 64-key steps
+        // kPfWaves waves of kPfRT x 16 (row, head) pairs for groups of up to 8 heads; 64-key steps
 #define MG_PF_CASE(H)                                                                                               \
     case H:                                                                                                         \
-        D == 128 ? go(k_attn_prefill<H, 4, 4, kPfWaves>, kPfWaves) : go(k_attn_prefill<H, 2, 4, kPfWaves>, kPfWaves); \
+        D == 128 ? go(k_attn_prefill<H, 4, 4, kPfWaves, kPfRT>, kPfWaves) : go(k_attn_prefill<H, 2, 4, kPfWaves, kPfRT>, kPfWaves); \
         break;
         switch (hw) {
             MG_PF_CASE(1)
